@@ -1,0 +1,19 @@
+"""hilda-kernel_amd: the hilda-kernel operator hot path on MI355X (gfx950).
+
+Drop-in for the reference package ``kernels`` (triton-kernels/kernels/__init__.py:1-28),
+restricted to the hot path: the same functional names, autograd Functions and
+modules, backed by hand-written HIP kernels in ``libhilda_kernel_amd.so``.
+Put ``hilda-kernel_amd/`` on ``sys.path`` and ``from kernels import ...`` as
+with the reference.
+"""
+from .rms_norm import HildaRMSNormFunction, hilda_rms_norm, RMSNorm
+from .rope import HildaRopeFunction, hilda_rope, RotaryEmbedding
+from .swiglu import HildaSwiGLUFunction, hilda_swiglu, SwiGLU
+from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
+
+__all__ = [
+    "HildaRMSNormFunction", "hilda_rms_norm", "RMSNorm",
+    "HildaRopeFunction", "hilda_rope", "RotaryEmbedding",
+    "HildaSwiGLUFunction", "hilda_swiglu", "SwiGLU",
+    "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
+]

@@ -1,0 +1,124 @@
+"""ctypes binding of the gfx950 C-ABI library (``libhilda_kernel_amd.so``).
+
+The library is built in-tree by ``hilda-kernel_amd/build.py``. There is no
+fallback: if the library is missing, or a tensor is not on a ROCm device,
+the ops raise instead of computing anything elsewhere.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libhilda_kernel_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+F32, F16, BF16 = 0, 1, 2
+DW_AUTO, DW_ATOMIC, DW_PARTIAL = 0, 1, 2
+
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_i32, _i64, _f32, _p, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/hilda_kernel_amd.h
+SIGNATURES = {
+    "hk_abi_version": (_i32, []),
+    "hk_last_error": (ctypes.c_char_p, []),
+    "hk_device_cu_count": (_i32, [_i32]),
+    "hk_rms_norm_fwd": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _f32, _p]),
+    "hk_rms_norm_bwd_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32, _i32]),
+    "hk_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
+    "hk_fused_add_rms_norm_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p]),
+    "hk_fused_add_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
+    "hk_rope": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                       _i32, _i32, _i32, _p]),
+    "hk_swiglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
+    "hk_swiglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
+}
+
+ABI_VERSION = 1
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the C-ABI library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_NAME} is not built (expected at {LIB_PATH}); "
+                    "run `python hilda-kernel_amd/build.py` first")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            got = lib.hk_abi_version()
+            if got != ABI_VERSION:
+                raise RuntimeError(f"{LIB_NAME} ABI version {got}, expected {ABI_VERSION}; rebuild it")
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().hk_last_error().decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed (status {status}): {last_error()}")
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point and raise RuntimeError on failure."""
+    check(getattr(load(), name)(*args), name)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32, float16 or bfloat16") from None
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one ROCm device; there is no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                f"hilda-kernel_amd ops run only on a ROCm GPU; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+_cu_cache: dict[int, int] = {}
+
+
+def cu_count(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _cu_cache:
+        n = load().hk_device_cu_count(idx)
+        check(0 if n > 0 else n, "hk_device_cu_count")
+        _cu_cache[idx] = n
+    return _cu_cache[idx]

@@ -1,0 +1,120 @@
+/*
+ * hilda_kernel_amd.h — C ABI of the MI355X (gfx950) operator hot path.
+ *
+ * Every entry point replaces one Triton launch site (or launch wrapper) of
+ * kirsten-1/hilda-kernel; the citation in front of each declaration names the
+ * reference code it stands in for (paths relative to triton-kernels/kernels/).
+ *
+ * Conventions
+ *  - Plain pointers and sizes only. Device pointers are HIP device memory
+ *    (torch tensors' data_ptr()); `stream` is a hipStream_t passed as void*.
+ *  - The caller owns all memory. Scratch space an op needs is passed in as
+ *    `workspace`, sized by the matching *_workspace_size() call.
+ *  - No entry point synchronises the device or allocates device memory.
+ *  - dtype codes: HK_F32 = 0, HK_F16 = 1, HK_BF16 = 2.
+ *  - Return value: 0 on success; HK_EINVAL (-1) when an argument is rejected
+ *    (checked before any HIP call, so this is testable without a GPU);
+ *    a positive hipError_t when the HIP runtime reports an error.
+ *    hk_last_error() returns the thread-local text of the last failure.
+ */
+#ifndef HILDA_KERNEL_AMD_H
+#define HILDA_KERNEL_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HK_ABI_VERSION 1
+
+#define HK_F32 0
+#define HK_F16 1
+#define HK_BF16 2
+
+/* dW reduction path for the norm backward passes */
+#define HK_DW_AUTO 0    /* atomic when rows <= 8 * CU count, else partial */
+#define HK_DW_ATOMIC 1  /* fp64 atomics into one [cols] accumulator       */
+#define HK_DW_PARTIAL 2 /* per-row-group partial rows + a reduction pass  */
+
+typedef void* hk_stream_t;
+
+/* ----------------------------------------------------------------------- */
+/* library                                                                 */
+/* ----------------------------------------------------------------------- */
+int hk_abi_version(void);
+const char* hk_last_error(void);
+/* Number of compute units of `device` (cached). Used for the dW path choice
+ * that rms_norm.py:325-326 makes with multi_processor_count. */
+int hk_device_cu_count(int device);
+
+/* ----------------------------------------------------------------------- */
+/* RMSNorm                                                                 */
+/* ----------------------------------------------------------------------- */
+/* Replaces _rms_norm_forward_kernel launch, rms_norm.py:293-304.
+ * y[r,:] = ((x[r,:] * rstd[r]) rounded to dtype_x) * w ; rstd[r] = 1/sqrt(mean(x^2)+eps) */
+int hk_rms_norm_fwd(void* y, float* rstd, const void* x, const void* w, int64_t rows, int64_t cols,
+                    int64_t ld_x, int64_t ld_y, int dtype_x, int dtype_w, float eps, hk_stream_t stream);
+
+/* Bytes of workspace hk_rms_norm_bwd / hk_fused_add_rms_norm_bwd need. */
+size_t hk_rms_norm_bwd_workspace_size(int64_t rows, int64_t cols, int dtype_x, int dtype_w,
+                                      int dw_mode, int device);
+
+/* Replaces rms_norm_backward, rms_norm.py:309-359 (atomic kernel :152-193,
+ * partial kernel :200-254 plus the torch sum/cast at :357-359).
+ * dx = rstd*(dy*w) - rstd^3 * (sum(dy*w*x)/cols) * x ; dw = sum_r dy*x*rstd (cast to dtype_w). */
+int hk_rms_norm_bwd(void* dx, void* dw, const void* dy, const void* x, const void* w, const float* rstd,
+                    int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_x, int64_t ld_dx, int dtype_x,
+                    int dtype_w, int dw_mode, void* workspace, size_t workspace_bytes, hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* FusedAddRMSNorm                                                         */
+/* ----------------------------------------------------------------------- */
+/* Replaces _fused_add_rms_norm_fwd_kernel launch, fused_add_rms_norm.py:172-188.
+ * s = x + r (rounded to dtype_x, stored); y = RMSNorm(s) * w. All four row
+ * tensors share the row stride `ld`. */
+int hk_fused_add_rms_norm_fwd(void* y, void* s, float* rstd, const void* x, const void* r, const void* w,
+                              int64_t rows, int64_t cols, int64_t ld, int dtype_x, int dtype_w, float eps,
+                              hk_stream_t stream);
+
+/* Replaces fused_add_rms_norm_backward, fused_add_rms_norm.py:191-232.
+ * dx = RMSNormBwd(dy; s) + ds_out (ds_out may be NULL); the same dx is the
+ * gradient of both x and r. */
+int hk_fused_add_rms_norm_bwd(void* dx, void* dw, const void* dy, const void* ds_out, const void* s,
+                              const void* w, const float* rstd, int64_t rows, int64_t cols, int64_t ld,
+                              int dtype_x, int dtype_w, int dw_mode, void* workspace, size_t workspace_bytes,
+                              hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* RoPE                                                                    */
+/* ----------------------------------------------------------------------- */
+/* Replaces _rope_fwd_kernel launches (rope.py:95-106) for one tensor in
+ * either direction: rope_forward (rope.py:113-136) with inverse = 0 and
+ * rope_backward (rope.py:139-172) with inverse = 1 (sin negated in-kernel).
+ * x / out: (B, H, T, D) logical with element strides s*; the last dim must
+ * be contiguous. cos/sin: (cos_B, T', D/2) with cos_B in {1, B}, last dim
+ * contiguous, rows indexed by t. */
+int hk_rope(void* out, const void* in, const void* cos, const void* sin, int64_t B, int64_t H, int64_t T, int64_t D,
+            int64_t in_sB, int64_t in_sH, int64_t in_sT, int64_t out_sB, int64_t out_sH, int64_t out_sT,
+            int64_t cos_B, int64_t cos_sB, int64_t cos_sT, int dtype_x, int dtype_cs, int inverse,
+            hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* SwiGLU                                                                  */
+/* ----------------------------------------------------------------------- */
+/* Replaces _swiglu_fwd_kernel launch (swiglu.py:112-124) on n contiguous
+ * elements: c = (silu(a) in fp32, rounded to dtype) * b. */
+int hk_swiglu_fwd(void* c, const void* a, const void* b, int64_t n, int dtype, hk_stream_t stream);
+
+/* Replaces _swiglu_bwd_kernel launch (swiglu.py:127-141); writes da and db to
+ * separate buffers instead of over a and b:
+ * db = dc * silu(a); da = dc * b * sig(a) * (1 + a * (1 - sig(a))). */
+int hk_swiglu_bwd(void* da, void* db, const void* a, const void* b, const void* dc, int64_t n, int dtype,
+                  hk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HILDA_KERNEL_AMD_H */

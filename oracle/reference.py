@@ -1,0 +1,243 @@
+"""CPU restatements of the reference's PyTorch implementations (test infrastructure).
+
+Each function follows the reference file:line named in its docstring
+(paths relative to /root/reference/triton-kernels/). They are used only as
+the checker in tests, in ``__graft_entry__.smoke()`` and as the timed CPU
+baseline in ``bench.py``; the product never calls them.
+
+How each function is pinned (tests/test_oracle.py), independently of
+retyping its formula:
+  rms_norm_ref            torch.nn.functional.rms_norm (library); zeros -> zeros;
+                          scale invariance; fp64 gradcheck of rms_norm_bwd_closed_form
+  fused_add_rms_norm_ref  S bit-exact against bf16 addition; Y against rms_norm_ref of S
+  rope_ref                complex-number rotation (x1 + i x2) * e^{i theta} (independent form);
+                          position-0 identity; norm preservation; all-ones backward
+                          known answer [cos+sin, cos-sin] (benchmarks/bench_rope.py:133-146)
+  swiglu_ref              x * sigmoid(x) from torch.sigmoid; a = 0 -> da = 0.5*dc*b
+  cross_entropy_ref       torch.nn.functional.cross_entropy (library); uniform logits -> log V;
+                          shift invariance; brute-force python loop on tiny inputs
+  selective_log_softmax_ref  brute-force python loop (log-sum-exp by hand) on tiny inputs
+  grpo_loss_ref           closed forms: old = logp, beta = 0 -> loss = -mean(A) and
+                          dlogits = -A_b/(len_b*B) * (onehot - p); ref = logp -> kl = 0;
+                          brute-force python loop of the per-token objective
+  linear_ce_ref           fp64 brute force (explicit dot products) on tiny shapes
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
+    "rope_ref", "swiglu_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
+    "linear_ce_ref", "fwd_bwd",
+]
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm / FusedAddRMSNorm
+# ---------------------------------------------------------------------------
+def _wide(t):
+    """The reference's ``.float()``: at least fp32 (fp64 inputs stay fp64 so tests can run the oracle in fp64)."""
+    return t if t.dtype == torch.float64 else t.float()
+
+
+def rms_norm_ref(x, weight, eps=1e-6):
+    """tests/test_rms_norm.py:22-28: everything in fp32, one cast at the end."""
+    x_f32 = _wide(x)
+    variance = x_f32.pow(2).mean(-1, keepdim=True)
+    x_normed = x_f32 * torch.rsqrt(variance + eps)
+    return (x_normed * _wide(weight)).to(x.dtype)
+
+
+def rms_norm_bwd_closed_form(dy, x, w, eps=1e-6):
+    """Closed-form RMSNorm gradients in fp64 (the formula of kernels/rms_norm.py:186-193).
+
+    dx = rstd*(dy*w) - rstd^3 * mean(dy*w*x) * x ;  dw = sum_rows dy * x * rstd
+    """
+    x, dy, w = x.double(), dy.double(), w.double()
+    rstd = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    m = dy * w
+    dx = rstd * m - rstd.pow(3) * (m * x).mean(-1, keepdim=True) * x
+    dw = (dy * x * rstd).reshape(-1, x.shape[-1]).sum(0)
+    return dx, dw
+
+
+def fused_add_rms_norm_ref(X, R, W, eps=1e-6):
+    """benchmarks/bench_fused_add_rms_norm.py:37-41: S = X + R; Y = (S/rms).to(S.dtype) * W."""
+    S = X + R
+    rms = torch.sqrt(torch.mean(_wide(S) ** 2, dim=-1, keepdim=True) + eps)
+    Y = (_wide(S) / rms).to(S.dtype) * W
+    return Y, S
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+def rope_tables(dim, max_position_embeddings=2048, base=10000.0, dtype=torch.float32):
+    """cos/sin tables of shape (1, max_pos, dim//2), as kernels/rope.py:209-222 builds them."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    t = torch.arange(max_position_embeddings, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos()[None, :, : dim // 2].to(dtype), emb.sin()[None, :, : dim // 2].to(dtype)
+
+
+def rotate_half(x):
+    """benchmarks/bench_rope.py:40-43."""
+    x1 = x[..., : x.shape[-1] // 2]
+    x2 = x[..., x.shape[-1] // 2:]
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def rope_ref(q, k, cos, sin):
+    """benchmarks/bench_rope.py:46-58 (HuggingFace rotate-half RoPE).
+
+    q, k: (B, H, T, D) logical layout (any strides); cos, sin: (1 or B, T, D//2).
+    """
+    cos_full = torch.cat([cos, cos], dim=-1).unsqueeze(1)
+    sin_full = torch.cat([sin, sin], dim=-1).unsqueeze(1)
+    q_embed = (q * cos_full) + (rotate_half(q) * sin_full)
+    k_embed = (k * cos_full) + (rotate_half(k) * sin_full)
+    return q_embed, k_embed
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU
+# ---------------------------------------------------------------------------
+def swiglu_ref(a, b):
+    """benchmarks/bench_swiglu.py:46-47: F.silu(a) * b."""
+    return F.silu(a) * b
+
+
+# ---------------------------------------------------------------------------
+# CrossEntropy
+# ---------------------------------------------------------------------------
+def cross_entropy_ref(logits, targets, ignore_index=-100, reduction="mean"):
+    """benchmarks/bench_cross_entropy.py:77-79,101-103: F.cross_entropy.
+
+    Restates two behaviours of kernels/cross_entropy.py that differ from
+    torch: ``ignore_index == -1`` means "ignore nothing" (:197-198,219-225),
+    and a mean over zero valid rows is 0, not NaN (:141,248).
+    """
+    if ignore_index == -1:
+        return F.cross_entropy(logits, targets, reduction=reduction)
+    if reduction == "mean":
+        n_valid = (targets != ignore_index).sum()
+        total = F.cross_entropy(logits, targets, ignore_index=ignore_index, reduction="sum")
+        return total / n_valid.clamp(min=1).to(total.dtype)
+    return F.cross_entropy(logits, targets, ignore_index=ignore_index, reduction=reduction)
+
+
+# ---------------------------------------------------------------------------
+# GRPO
+# ---------------------------------------------------------------------------
+def selective_log_softmax_ref(logits, input_ids, temperature=1.0, mask=None):
+    """kernels/grpo_loss.py:65-80 semantics (log_softmax(logits/T).gather, benchmarks/bench_grpo.py:37-40).
+
+    logits (B, L+1, V) -> logp (B, L) fp32 for the first L positions;
+    ids = input_ids[:, -L:], mask = mask[:, -L:]; masked positions are 0.
+    """
+    B, L1, V = logits.shape
+    L = L1 - 1
+    ids = input_ids[:, -L:]
+    logp = (_wide(logits[:, :-1, :]) / temperature).log_softmax(-1).gather(-1, ids.unsqueeze(-1)).squeeze(-1)
+    if mask is not None:
+        logp = torch.where(mask[:, -L:] != 0, logp, torch.zeros_like(logp))
+    return logp
+
+
+def grpo_loss_ref(logits, completion_ids, advantages, old_logp=None, ref_logp=None, completion_mask=None,
+                  temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2):
+    """benchmarks/bench_grpo.py:30-57 for the loss; kl_mean and clip_ratio restated
+    from kernels/grpo_loss.py:129-134,290-292 (the bench has no reference for them).
+
+    Returns (loss, kl_mean or None, clip_ratio).
+    """
+    B, L_plus_1, V = logits.shape
+    L = L_plus_1 - 1
+    logits_shifted = logits[:, :-1, :] / temperature
+    log_probs = logits_shifted.log_softmax(dim=-1)
+    ids = completion_ids[:, -L:].unsqueeze(-1)
+    logp = log_probs.gather(-1, ids).squeeze(-1)
+
+    if old_logp is None:
+        old_logp = logp.detach()
+    ratio = torch.exp(logp - old_logp)
+    ratio_clipped = torch.clamp(ratio, 1 - eps_low, 1 + eps_high)
+    adv = advantages.unsqueeze(-1)
+    loss1 = ratio * adv
+    loss2 = ratio_clipped * adv
+    per_token_loss = -torch.min(loss1, loss2)
+
+    kl = None
+    if beta != 0.0 and ref_logp is not None:
+        kl = torch.exp(ref_logp - logp) - (ref_logp - logp) - 1
+        per_token_loss = per_token_loss + beta * kl
+
+    mask = completion_mask.float() if completion_mask is not None else torch.ones_like(per_token_loss)
+    seq_lens = mask.sum(-1).clamp(min=1.0)
+    loss = ((per_token_loss * mask).sum(-1) / seq_lens).mean()
+
+    mask_sum = mask.sum().clamp(min=1.0)
+    kl_mean = (kl * mask).sum() / mask_sum if kl is not None else None
+    with torch.no_grad():
+        r = ratio.detach()
+        is_clipped = ((r < 1 - eps_low) & (adv < 0)) | ((r > 1 + eps_high) & (adv > 0))
+        clip_ratio = (is_clipped.float() * mask).sum() / mask_sum
+    return loss, kl_mean, clip_ratio
+
+
+# ---------------------------------------------------------------------------
+# FusedLinearCrossEntropy
+# ---------------------------------------------------------------------------
+def linear_ce_ref(hidden, weight, targets, ignore_index=-100, reduction="mean"):
+    """benchmarks/bench_fused_linear_ce.py:36-38: logits = hidden @ weight.T, then CE.
+
+    Keeps the reference's "mean over zero valid rows is 0" rule
+    (kernels/fused_linear_cross_entropy.py:124-127,164-165).
+    """
+    logits = hidden @ weight.T
+    return cross_entropy_ref(logits, targets, ignore_index=ignore_index, reduction=reduction)
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def fwd_bwd(fn, inputs, grads=None, dtype=torch.float32, differentiable=None):
+    """Run ``fn`` on fp32 (or ``dtype``) CPU copies of ``inputs`` and backprop.
+
+    inputs: list of tensors (or None); entries with ``differentiable[i]`` True
+    become leaves requiring grad. grads: upstream gradients for the outputs
+    (None -> the outputs are scalars and backward() uses 1.0).
+    Returns (outputs tuple, list of input grads).
+    """
+    if differentiable is None:
+        differentiable = [t is not None and t.is_floating_point() for t in inputs]
+    leaves = []
+    for t, d in zip(inputs, differentiable):
+        if t is None:
+            leaves.append(None)
+            continue
+        c = t.detach().cpu()
+        if c.is_floating_point():
+            c = c.to(dtype)
+        if d:
+            c.requires_grad_(True)
+        leaves.append(c)
+    outs = fn(*leaves)
+    if not isinstance(outs, (tuple, list)):
+        outs = (outs,)
+    diff_outs = [o for o in outs if o is not None and o.requires_grad]
+    if grads is None:
+        torch.autograd.backward(diff_outs[0])
+    else:
+        gl = [g.detach().cpu().to(o.dtype) for g, o in zip(grads, diff_outs)]
+        torch.autograd.backward(diff_outs[: len(gl)], gl)
+    return tuple(outs), [None if (t is None or not d) else t.grad for t, d in zip(leaves, differentiable)]
+
+
+def log_v(v: int) -> float:
+    return math.log(v)

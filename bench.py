@@ -1,0 +1,346 @@
+"""Benchmark of the hilda-kernel_amd hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops all|c2|none] [--no-cpu]
+
+Headline (``value``): fwd+bwd throughput of the BASELINE.json configs[1]
+workload, the Llama-3-8B layer ops in bf16 — FusedAddRMSNorm [8192,4096],
+RoPE q[4,2048,32,128] + k[4,2048,8,128] ([B,T,H,D] storage), SwiGLU
+[8192,14336] — as algorithmic HBM GB/s. One step = one fwd+bwd of the three
+ops (inputs resident in HBM, grads via torch.autograd.grad so nothing is
+accumulated). ``ops`` adds each configuration's op on its own (C1-C5), timed
+with HIP events and a 512 MiB cache flush between reps. ``roofline`` is the
+dominant kernel of the step (SwiGLU backward), timed per launch with HIP
+events on its stream inside the timed region. ``cpu_baseline`` times the CPU
+PyTorch reference path (the oracle) on a quarter-size C2 sample.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "hilda-kernel_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+import workloads  # noqa: E402
+
+METRIC = "fwd+bwd HBM GB/s & % roofline per op; FusedLinearCE TFLOP/s (1 GPU)"
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# algorithmic work (each required input read once, each output written once)
+# ---------------------------------------------------------------------------
+def bytes_fused_add(rows, hidden, es=2):
+    # fwd: X, R read; S, Y write; bwd: dY, dS, S read; dX write; plus W, RSTD, dW
+    return 8 * rows * hidden * es + 3 * hidden * es + 2 * rows * 4
+
+
+def bytes_rms_norm(rows, hidden, es=4):
+    # fwd: X read, Y write; bwd: dY, X read, dX write; plus W, RSTD, dW
+    return 5 * rows * hidden * es + 3 * hidden * es + 2 * rows * 4
+
+
+def bytes_rope(q_elems, k_elems, T, D, es=2):
+    # each direction reads q,k and writes q',k'; cos/sin fp32 [T, D/2] read per direction
+    return 4 * (q_elems + k_elems) * es + 2 * 2 * T * (D // 2) * 4
+
+
+def bytes_swiglu(rows, inter, es=2):
+    # fwd: a, b read, c write; bwd: a, b, dc read, da, db write
+    return 8 * rows * inter * es
+
+
+def bytes_swiglu_bwd(rows, inter, es=2):
+    return 5 * rows * inter * es
+
+
+# ---------------------------------------------------------------------------
+# the C2 step
+# ---------------------------------------------------------------------------
+class C2Step:
+    def __init__(self, K, dev, scale=1):
+        fa = workloads.c2_fused_add_rms_norm(rows=8192 // scale, device=dev)
+        rp = workloads.c2_rope(B=max(1, 4 // scale), device=dev)
+        sw = workloads.c2_swiglu(rows=8192 // scale, device=dev)
+        self.K = K
+        self.x = fa["x"].requires_grad_(True)
+        self.r = fa["r"].requires_grad_(True)
+        self.w = fa["w"].requires_grad_(True)
+        self.dy, self.ds = fa["dy"], fa["ds"]
+        self.q = rp["q"].detach().requires_grad_(True)   # (B,H,T,D) view of [B,T,H,D] storage
+        self.k = rp["k"].detach().requires_grad_(True)
+        self.cos, self.sin = rp["cos"], rp["sin"]
+        self.dq, self.dk = rp["dq"], rp["dk"]
+        self.a = sw["a"].requires_grad_(True)
+        self.b = sw["b"].requires_grad_(True)
+        self.dc = sw["dc"]
+        rows, hidden = self.x.shape
+        self.bytes = {
+            "fused_add_rms_norm": bytes_fused_add(rows, hidden),
+            "rope": bytes_rope(self.q.numel(), self.k.numel(), self.q.shape[2], self.q.shape[3]),
+            "swiglu": bytes_swiglu(*self.a.shape),
+        }
+        self.swiglu_bwd_bytes = bytes_swiglu_bwd(*self.a.shape)
+
+    def fused_add(self):
+        K = self.K
+        y, s = K.hilda_fused_add_rms_norm(self.x, self.r, self.w)
+        return torch.autograd.grad([y, s], [self.x, self.r, self.w], [self.dy, self.ds])
+
+    def rope(self):
+        K = self.K
+        qo, ko = K.hilda_rope(self.q, self.k, self.cos, self.sin)
+        return torch.autograd.grad([qo, ko], [self.q, self.k], [self.dq, self.dk])
+
+    def swiglu(self):
+        K = self.K
+        c = K.hilda_swiglu(self.a, self.b)
+        return torch.autograd.grad([c], [self.a, self.b], [self.dc])
+
+    def step(self):
+        self.fused_add()
+        self.rope()
+        self.swiglu()
+
+    def total_bytes(self):
+        return sum(self.bytes.values())
+
+
+# ---------------------------------------------------------------------------
+# per-op timing with HIP events and a cache flush between reps
+# ---------------------------------------------------------------------------
+class Flusher:
+    """Writes a 512 MiB buffer so MI355X's 256 MB MALL and the L2s hold none of the op's data."""
+
+    def __init__(self, dev):
+        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+    def __call__(self):
+        self.buf.zero_()
+
+
+def time_events(fn, reps, flush=None, warmup=2):
+    for _ in range(warmup):
+        fn()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        if flush is not None:
+            flush()
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def op_entry(config, ms_list, work, unit, peak):
+    ms = statistics.median(ms_list)
+    rate = work / (ms * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
+    return {"config": config, "ms": round(ms, 5), "value": round(rate, 2), "unit": unit,
+            "frac": round(rate / peak, 4), "work": work, "reps": len(ms_list)}
+
+
+def bench_c2_ops(c2, reps, flush):
+    out = {}
+    for name, fn in (("fused_add_rms_norm", c2.fused_add), ("rope", c2.rope), ("swiglu", c2.swiglu)):
+        out[name] = op_entry("C2", time_events(fn, reps, flush), c2.bytes[name], "GB/s", HBM_PEAK_GBPS)
+        log(f"  {name}: {out[name]['ms']:.4f} ms  {out[name]['value']:.0f} GB/s  ({out[name]['frac']:.1%})")
+    return out
+
+
+def bench_c1(K, dev, reps, flush):
+    c = workloads.c1_rms_norm(device=dev)
+    x = c["x"].requires_grad_(True)
+    w = c["w"].requires_grad_(True)
+    dy = c["dy"]
+
+    def fn():
+        y = K.hilda_rms_norm(x, w, c["eps"])
+        return torch.autograd.grad([y], [x, w], [dy])
+
+    e = op_entry("C1", time_events(fn, reps, flush), bytes_rms_norm(*x.shape), "GB/s", HBM_PEAK_GBPS)
+    log(f"  rms_norm (C1 fp32): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (the reference's PyTorch path) on the host cores
+# ---------------------------------------------------------------------------
+def cpu_baseline(reps=3):
+    import oracle
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    scale = 4
+    fa = workloads.c2_fused_add_rms_norm(rows=8192 // scale, device="cpu")
+    rp = workloads.c2_rope(B=4 // scale, device="cpu")
+    sw = workloads.c2_swiglu(rows=8192 // scale, device="cpu")
+    x, r, w = (fa[k].clone().requires_grad_(True) for k in ("x", "r", "w"))
+    q = rp["q"].detach().requires_grad_(True)
+    k = rp["k"].detach().requires_grad_(True)
+    a, b = (sw[n].clone().requires_grad_(True) for n in ("a", "b"))
+    work = (bytes_fused_add(*x.shape) + bytes_rope(q.numel(), k.numel(), q.shape[2], q.shape[3])
+            + bytes_swiglu(*a.shape))
+
+    def step():
+        y, s = oracle.fused_add_rms_norm_ref(x, r, w)
+        torch.autograd.grad([y, s], [x, r, w], [fa["dy"], fa["ds"]])
+        qo, ko = oracle.rope_ref(q, k, rp["cos"], rp["sin"])
+        torch.autograd.grad([qo, ko], [q, k], [rp["dq"].float(), rp["dk"].float()])
+        c = oracle.swiglu_ref(a, b)
+        torch.autograd.grad([c], [a, b], [sw["dc"]])
+
+    step()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(work / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"C2 step on 1/{scale} of the tokens (FusedAddRMSNorm [2048,4096], RoPE B=1, "
+                      f"SwiGLU [2048,14336]), bf16 PyTorch reference path fwd+bwd, median of {reps}",
+            "seconds_per_step": round(t, 4), "cpu_model": cpu_model}
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        e = data["kernels"][kernel]
+        return int(e["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--ops", choices=["all", "c2", "none"], default="all")
+    ap.add_argument("--op-reps", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    import kernels as K
+    from kernels import swiglu as swiglu_mod
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device: {torch.cuda.get_device_name(dev)}")
+    c2 = C2Step(K, dev)
+
+    # events around every SwiGLU backward launch inside the timed region
+    sw_events = []
+    recording = {"on": False}
+    orig_bwd = swiglu_mod.swiglu_backward
+
+    def timed_bwd(a, b, dc):
+        if not recording["on"]:
+            return orig_bwd(a, b, dc)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(torch.cuda.current_stream(a.device))
+        out = orig_bwd(a, b, dc)
+        e.record(torch.cuda.current_stream(a.device))
+        sw_events.append((s, e))
+        return out
+
+    swiglu_mod.swiglu_backward = timed_bwd
+
+    for _ in range(args.warmup):
+        c2.step()
+    torch.cuda.synchronize()
+    recording["on"] = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        c2.step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    recording["on"] = False
+    swiglu_mod.swiglu_backward = orig_bwd
+
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    total_bytes = c2.total_bytes()
+    value = total_bytes / (ms_per_step * 1e-3) / 1e9
+    sw_ms = statistics.mean(s.elapsed_time(e) for s, e in sw_events)
+    achieved = c2.swiglu_bwd_bytes / (sw_ms * 1e-3) / 1e9
+    log(f"C2 step: {ms_per_step:.4f} ms/step, {value:.0f} GB/s; swiglu bwd {sw_ms * 1e3:.1f} us "
+        f"-> {achieved:.0f} GB/s")
+
+    roofline = {"bound": "hbm", "kernel": "swiglu_bwd_kernel", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": load_traffic("swiglu_bwd_kernel"),
+                "algorithmic_bytes_per_launch": c2.swiglu_bwd_bytes, "avg_launch_us": round(sw_ms * 1e3, 2),
+                "launches": len(sw_events)}
+
+    ops = {}
+    if args.ops != "none":
+        flush = Flusher(dev)
+        log("per-op fwd+bwd (median, cache flushed between reps):")
+        ops.update(bench_c2_ops(c2, args.op_reps, flush))
+        if args.ops == "all":
+            ops["rms_norm"] = bench_c1(K, dev, args.op_reps, flush)
+        del flush
+
+    del c2
+    torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        cpu = cpu_baseline()
+        log(f"  CPU: {cpu['value']} GB/s on {cpu['cores']} cores")
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) inputs and upstream grads of BASELINE.json configs[1]",
+        "config": {"workload": "C2 Llama-3-8B layer ops fwd+bwd: FusedAddRMSNorm x,r[8192,4096]; "
+                               "RoPE q[4,2048,32,128] k[4,2048,8,128] theta=500000 ([B,T,H,D] storage); "
+                               "SwiGLU gate,up[8192,14336]",
+                   "bytes_per_step": total_bytes, "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": cpu, "ops": ops,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

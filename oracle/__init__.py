@@ -14,4 +14,3 @@ Pinning (what independently checks each function here) is listed in the
 docstring of ``oracle.reference``; every function is pinned.
 """
 from .reference import *  # noqa: F401,F403
-from . import configs  # noqa: F401

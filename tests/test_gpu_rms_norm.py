@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from oracle import configs
+import workloads as configs
 from _util import assert_close, rel_fro, tol, gpu
 
 from kernels import rms_norm as rn

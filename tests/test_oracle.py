@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as F
 
 import oracle
-from oracle import configs
+import workloads as configs
 
 torch.set_default_dtype(torch.float32)
 
@@ -283,7 +283,7 @@ def test_config_generators_small():
     c = configs.c3_cross_entropy(rows=4000, vocab=50)
     frac = (c["targets"] == -100).float().mean().item()
     assert 0.07 < frac < 0.13 and c["logits"].dtype == torch.bfloat16
-    c4 = configs.c4_grpo(B=4, T=300, vocab=40)
+    c4 = configs.c4_grpo(oracle.selective_log_softmax_ref, B=4, T=300, vocab=40)
     lens = c4["completion_mask"].sum(-1)
     assert c4["logits"].shape == (4, 300, 40) and c4["completion_ids"].shape == (4, 299)
     assert torch.all(lens >= 256) and torch.all(lens <= 299)

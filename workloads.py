@@ -1,7 +1,9 @@
-"""Seeded synthetic inputs of the benchmark configurations C1-C5 (test infrastructure).
+"""Seeded synthetic inputs of the benchmark configurations C1-C5.
 
-Every generator draws from ``torch.Generator(device).manual_seed(seed)`` in a
-fixed order, so the same call on the same device gives the same tensors.
+Shared by bench.py, the tests and smoke(); it holds workload definitions
+only (no reference arithmetic). Every generator draws from
+``torch.Generator(device).manual_seed(seed)`` in a fixed order, so the same
+call on the same device gives the same tensors.
 bf16 tensors are drawn in fp32 and then cast. Shapes default to the full
 configuration; tests pass smaller sizes. The draws follow the descriptions
 in BASELINE.json ``configs``.
@@ -10,9 +12,16 @@ from __future__ import annotations
 
 import torch
 
-from .reference import rope_tables, selective_log_softmax_ref
-
 SEEDS = {"c1": 1, "c2": 2, "c3": 3, "c4": 4, "c5": 5}
+
+
+def rope_tables(dim, max_position_embeddings=2048, base=10000.0):
+    """fp32 cos/sin tables (1, max_pos, dim//2) of RotaryEmbedding (kernels/rope.py:209-222)."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    t = torch.arange(max_position_embeddings, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos()[None, :, : dim // 2].contiguous(), emb.sin()[None, :, : dim // 2].contiguous()
 
 
 def _gen(device, seed):
@@ -59,9 +68,10 @@ def c2_rope(B=4, T=2048, Hq=32, Hk=8, D=128, theta=500000.0, device="cpu", seed=
     q = _randn(g, (B, T, Hq, D), device, dtype=bf).transpose(1, 2)
     k = _randn(g, (B, T, Hk, D), device, dtype=bf).transpose(1, 2)
     cos, sin = rope_tables(D, T, theta)
+    cos, sin = cos.to(device), sin.to(device)
     dq = _randn(g, (B, T, Hq, D), device, dtype=bf).transpose(1, 2)
     dk = _randn(g, (B, T, Hk, D), device, dtype=bf).transpose(1, 2)
-    return {"q": q, "k": k, "cos": cos.to(device), "sin": sin.to(device), "dq": dq, "dk": dk}
+    return {"q": q, "k": k, "cos": cos, "sin": sin, "dq": dq, "dk": dk}
 
 
 def c2_swiglu(rows=8192, inter=14336, device="cpu", seed=SEEDS["c2"] + 200):
@@ -84,15 +94,16 @@ def c3_cross_entropy(rows=8192, vocab=128256, ignore_frac=0.10, device="cpu", se
     return {"logits": logits, "targets": targets, "ignore_index": -100, "reduction": "mean"}
 
 
-def c4_grpo(B=16, T=1024, vocab=151936, device="cpu", seed=SEEDS["c4"], logp_fn=None):
+def c4_grpo(logp_fn, B=16, T=1024, vocab=151936, device="cpu", seed=SEEDS["c4"]):
     """C4: logits = (2 N(0,1)).bf16 [B, T, V] read as (B, L+1, V), L = T-1;
     ids uniform [0,V) (B,L); advantages N(0,1) (B,); valid lengths uniform in
     [256, T) clamped to L (prefix mask, int32); old = logp + 0.05 N, ref =
     logp + 0.1 N with logp the fp32 selective log-softmax of the logits;
     beta = 0.1, eps = 0.2, temperature = 1.
 
-    ``logp_fn(logits, ids)`` computes logp (defaults to the CPU oracle; the
-    GPU bench passes its own kernel to avoid a 10 GB host computation)."""
+    ``logp_fn(logits, ids)`` computes logp: the tests pass the CPU oracle,
+    the GPU bench passes the library's selective log-softmax (the values only
+    shape the synthetic old/ref log-probs)."""
     g = _gen(device, seed)
     L = T - 1
     logits = _randn(g, (B, T, vocab), device, 2.0, torch.bfloat16)
@@ -101,10 +112,7 @@ def c4_grpo(B=16, T=1024, vocab=151936, device="cpu", seed=SEEDS["c4"], logp_fn=
     lo = min(256, L)
     lengths = torch.randint(lo, max(T, lo + 1), (B,), generator=g, device=device).clamp(max=L)
     mask = (torch.arange(L, device=device)[None, :] < lengths[:, None]).to(torch.int32)
-    if logp_fn is None:
-        logp = selective_log_softmax_ref(logits, ids)
-    else:
-        logp = logp_fn(logits, ids)
+    logp = logp_fn(logits, ids).float()
     old = logp + _randn(g, (B, L), device, 0.05)
     ref = logp + _randn(g, (B, L), device, 0.1)
     return {"logits": logits, "completion_ids": ids, "advantages": adv, "old_logp": old, "ref_logp": ref,

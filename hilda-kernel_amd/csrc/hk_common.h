@@ -9,6 +9,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <type_traits>
+
 namespace hk {
 
 // ---------------------------------------------------------------------------
@@ -44,47 +46,149 @@ template <typename T> __device__ __forceinline__ float round_through(float v) {
 
 // ---------------------------------------------------------------------------
 // packed vectors: VEC elements of T moved as one global transaction
-// (16 bytes when VEC*sizeof(T) == 16).
+// (16 bytes when VEC*sizeof(T) == 16). The payload is kept as raw 32-bit
+// words so two 16-bit values share one VGPR; elements are widened to fp32 by
+// bit operations (bf16: shift/mask) or the hardware half->float convert.
 // ---------------------------------------------------------------------------
+template <typename T, int VEC, bool SUB_WORD = (sizeof(T) * VEC < 4)>
+struct Pack;
+
 template <typename T, int VEC>
-struct alignas(sizeof(T) * VEC) Pack {
-  T v[VEC];
+struct Pack<T, VEC, false> {
+  static constexpr int kWords = sizeof(T) * VEC / 4;
+  uint32_t w[kWords];
+};
+// a single 16-bit element
+template <typename T, int VEC>
+struct Pack<T, VEC, true> {
+  static_assert(sizeof(T) == 2 && VEC == 1, "sub-word packs hold one 16-bit element");
+  uint16_t h;
 };
 
 template <typename T, int VEC>
 __device__ __forceinline__ Pack<T, VEC> load_pack(const T* p) {
-  return *reinterpret_cast<const Pack<T, VEC>*>(p);
-}
-template <typename T, int VEC>
-__device__ __forceinline__ void store_pack(T* p, const Pack<T, VEC>& v) {
-  *reinterpret_cast<Pack<T, VEC>*>(p) = v;
-}
-// Streaming store for outputs that are not re-read by this kernel.
-template <typename T, int VEC>
-__device__ __forceinline__ void store_pack_nt(T* p, const Pack<T, VEC>& v) {
+  Pack<T, VEC> r;
   constexpr int B = sizeof(T) * VEC;
   if constexpr (B == 16) {
-    __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&v), reinterpret_cast<u32x4*>(p));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  } else if constexpr (B == 32) {
+    const u32x4 a = reinterpret_cast<const u32x4*>(p)[0];
+    const u32x4 b = reinterpret_cast<const u32x4*>(p)[1];
+    r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+    r.w[4] = b.x; r.w[5] = b.y; r.w[6] = b.z; r.w[7] = b.w;
   } else if constexpr (B == 8) {
-    __builtin_nontemporal_store(*reinterpret_cast<const u32x2*>(&v), reinterpret_cast<u32x2*>(p));
+    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    r.w[0] = v.x; r.w[1] = v.y;
   } else if constexpr (B == 4) {
-    __builtin_nontemporal_store(*reinterpret_cast<const uint32_t*>(&v), reinterpret_cast<uint32_t*>(p));
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
   } else {
-    *reinterpret_cast<Pack<T, VEC>*>(p) = v;
+    r.h = *reinterpret_cast<const uint16_t*>(p);
+  }
+  return r;
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_pack(T* p, const Pack<T, VEC>& r) {
+  constexpr int B = sizeof(T) * VEC;
+  if constexpr (B == 16) {
+    *reinterpret_cast<u32x4*>(p) = u32x4{r.w[0], r.w[1], r.w[2], r.w[3]};
+  } else if constexpr (B == 32) {
+    reinterpret_cast<u32x4*>(p)[0] = u32x4{r.w[0], r.w[1], r.w[2], r.w[3]};
+    reinterpret_cast<u32x4*>(p)[1] = u32x4{r.w[4], r.w[5], r.w[6], r.w[7]};
+  } else if constexpr (B == 8) {
+    *reinterpret_cast<u32x2*>(p) = u32x2{r.w[0], r.w[1]};
+  } else if constexpr (B == 4) {
+    *reinterpret_cast<uint32_t*>(p) = r.w[0];
+  } else {
+    *reinterpret_cast<uint16_t*>(p) = r.h;
+  }
+}
+
+// Streaming store for outputs that are not re-read by this kernel.
+template <typename T, int VEC>
+__device__ __forceinline__ void store_pack_nt(T* p, const Pack<T, VEC>& r) {
+  constexpr int B = sizeof(T) * VEC;
+  if constexpr (B == 16) {
+    __builtin_nontemporal_store(u32x4{r.w[0], r.w[1], r.w[2], r.w[3]}, reinterpret_cast<u32x4*>(p));
+  } else if constexpr (B == 8) {
+    __builtin_nontemporal_store(u32x2{r.w[0], r.w[1]}, reinterpret_cast<u32x2*>(p));
+  } else if constexpr (B == 4) {
+    __builtin_nontemporal_store(r.w[0], reinterpret_cast<uint32_t*>(p));
+  } else {
+    store_pack<T, VEC>(p, r);
+  }
+}
+
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+template <typename T, int VEC>
+__device__ __forceinline__ void unpack(const Pack<T, VEC>& r, float (&out)[VEC]) {
+  if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) out[i] = bits_f32(r.w[i]);
+  } else if constexpr (sizeof(T) * VEC < 4) {
+    out[0] = to_f32<T>(__builtin_bit_cast(T, r.h));
+  } else if constexpr (std::is_same<T, __bf16>::value) {
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) {
+      out[2 * k] = bits_f32(r.w[k] << 16);
+      out[2 * k + 1] = bits_f32(r.w[k] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) {
+      out[2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.w[k] & 0xffffu));
+      out[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.w[k] >> 16));
+    }
   }
 }
 
 template <typename T, int VEC>
-__device__ __forceinline__ void unpack(const Pack<T, VEC>& p, float (&out)[VEC]) {
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) out[i] = to_f32<T>(p.v[i]);
-}
-template <typename T, int VEC>
 __device__ __forceinline__ Pack<T, VEC> pack(const float (&in)[VEC]) {
-  Pack<T, VEC> p;
+  Pack<T, VEC> r;
+  if constexpr (std::is_same<T, float>::value) {
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) p.v[i] = from_f32<T>(in[i]);
-  return p;
+    for (int i = 0; i < VEC; ++i) r.w[i] = f32_bits(in[i]);
+  } else if constexpr (sizeof(T) * VEC < 4) {
+    r.h = __builtin_bit_cast(uint16_t, from_f32<T>(in[0]));
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) {
+      const uint32_t lo = __builtin_bit_cast(uint16_t, from_f32<T>(in[2 * k]));
+      const uint32_t hi = __builtin_bit_cast(uint16_t, from_f32<T>(in[2 * k + 1]));
+      r.w[k] = lo | (hi << 16);
+    }
+  }
+  return r;
+}
+
+// One element of a pack, widened to fp32.
+template <typename T, int VEC>
+__device__ __forceinline__ float pack_elem(const Pack<T, VEC>& r, int i) {
+  float x[VEC];
+  unpack(r, x);
+  return x[i];
+}
+
+// A pack with every element equal to `value` (rounded to T).
+template <typename T, int VEC>
+__device__ __forceinline__ Pack<T, VEC> splat_pack(float value) {
+  float x[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) x[i] = value;
+  return pack<T, VEC>(x);
+}
+
+// Keep the optimiser from reusing values derived from the pack across this
+// point (it re-derives them from the raw words instead of keeping copies live).
+template <typename T, int VEC>
+__device__ __forceinline__ void make_opaque(Pack<T, VEC>& r) {
+  if constexpr (sizeof(T) * VEC >= 4) {
+#pragma unroll
+    for (int k = 0; k < Pack<T, VEC>::kWords; ++k) asm volatile("" : "+v"(r.w[k]));
+  }
 }
 
 // ---------------------------------------------------------------------------

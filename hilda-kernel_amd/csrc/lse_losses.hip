@@ -1,0 +1,909 @@
+// Log-sum-exp loss family for gfx950: CrossEntropy (fused loss + gradient,
+// inference forward), selective log-softmax and the GRPO loss with its
+// gradient fused into the forward pass.
+//
+// Row engine. One workgroup owns one vocabulary row at a time (persistent
+// grid, rows strided by gridDim.x). When the row fits, it is held in VGPRs:
+// NCH packed 16-byte vectors per lane over a 256- or 1024-lane workgroup
+// (a 128256-entry bf16 row is 16 vectors per lane of 1024 lanes, 64 VGPRs),
+// so the row crosses HBM once: read, max, sum of 2^(x*c - m), then the
+// gradient (p - onehot) * g is written straight from the registers. Rows that
+// do not fit use a streaming variant that keeps a per-lane online (max, sum)
+// and reads the row a second time for the gradient.
+//
+// All exponentials run on v_exp_f32 (2^x) with log2(e)/T folded into one
+// multiply-add per element; log-sum-exp is kept in the log2 domain and
+// converted once per row.
+#include "hk_common.h"
+#include "../../include/hilda_kernel_amd.h"
+
+#include <math.h>
+#include <type_traits>
+
+namespace hk {
+namespace {
+
+// ---------------------------------------------------------------------------
+// register-resident row helpers
+// ---------------------------------------------------------------------------
+template <typename T, int VEC, int NCH, int BLOCK>
+struct RowRegs {
+  Pack<T, VEC> v[NCH];
+
+  // Addressing: vector j of lane t covers columns [j*BLOCK*VEC + t*VEC, +VEC).
+  // The j-dependent part is uniform (row pointer + constant) and the lane part
+  // is one 32-bit VGPR. Whether vector j is full, partial or absent depends
+  // only on the uniform remainder n - j*BLOCK*VEC, so those cases are scalar
+  // branches; only a partial vector needs a per-lane test. Column indices are
+  // 32-bit: the host rejects rows of 2^31 or more elements.
+  static constexpr int kSpan = BLOCK * VEC;
+  __device__ __forceinline__ static int lane_col() { return (int)threadIdx.x * VEC; }
+  // element offset of vector j for a lane at column tc, as an unsigned 32-bit
+  // value: the address is then one 64-bit base plus a zero-extended VGPR offset
+  // (the global_load saddr form) rather than one 64-bit base per vector.
+  __device__ __forceinline__ static uint32_t off(int j, int tc) { return (uint32_t)(j * kSpan) + (uint32_t)tc; }
+
+  // Elements past the row end hold -inf: they add nothing to the max or the
+  // sum, so the max/sum phases run without lane masks.
+  __device__ __forceinline__ void load(const T* __restrict__ row, int n) {
+    const int tc = lane_col();
+    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int lim = n - j * kSpan;  // uniform
+      if (lim >= kSpan) {
+        v[j] = load_pack<T, VEC>(row + off(j, tc));
+      } else if (lim > 0) {
+        const Pack<T, VEC> x = load_pack<T, VEC>(row + off(j, tc < lim ? tc : 0));  // in-bounds address
+        v[j] = tc < lim ? x : ninf;
+      } else {
+        v[j] = ninf;  // defined on every path, so no value flows in from the previous row
+      }
+    }
+  }
+
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) make_opaque(v[j]);
+  }
+
+  // max over the row of x * c (c > 0)
+  __device__ __forceinline__ float local_max(int n, float c) const {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j * kSpan < n) {  // uniform
+        float x[VEC];
+        unpack(v[j], x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) m = fmaxf(m, x[e]);
+      }
+    }
+    return m * c;
+  }
+
+  // sum over the row of 2^(x*c - m2)
+  __device__ __forceinline__ float local_sumexp(int n, float c, float m2) const {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j * kSpan < n) {
+        float x[VEC];
+        unpack(v[j], x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += exp2_fast(fmaf(x[e], c, -m2));
+      }
+    }
+    return s;
+  }
+
+  // out[j] = (2^(x*c - lse2) - [j == target]) * g   (target < 0: no one-hot)
+  __device__ __forceinline__ void store_grad(T* __restrict__ out, int n, float c, float lse2, int target,
+                                             float g) const {
+    const int tc = lane_col();
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int lim = n - j * kSpan;  // uniform
+      if (lim > 0) {
+        float x[VEC];
+        unpack(v[j], x);
+        const int rel = (target - j * kSpan) - tc;  // one compare base per vector
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float p = exp2_fast(fmaf(x[e], c, -lse2));
+          x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
+        }
+        if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
+      }
+    }
+  }
+};
+
+// The row length as a per-iteration scalar. Hiding it from loop-invariant
+// code motion keeps the per-vector bounds tests inside the row loop (a few
+// scalar ops per row) instead of hoisting 3*NCH 64-bit masks into SGPRs,
+// which spills them.
+__device__ __forceinline__ int row_len(int64_t v) {
+  int n = (int)v;
+  asm volatile("" : "+s"(n));
+  return n;
+}
+
+template <typename T, int VEC, int BLOCK>
+__device__ __forceinline__ void fill_row(T* __restrict__ out, int n, float value) {
+  const Pack<T, VEC> z = splat_pack<T, VEC>(value);
+  for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC)
+    store_pack_nt<T, VEC>(out + col, z);
+}
+
+// Row log-sum-exp in the log2 domain of (x * c), register-resident.
+template <typename T, int VEC, int NCH, int BLOCK>
+__device__ __forceinline__ float row_lse2(RowRegs<T, VEC, NCH, BLOCK>& r, int n, float c, float* red) {
+  const float m2 = block_max<BLOCK / kWave>(r.local_max(n, c), red);
+  r.opaque();
+  const float s = block_sum<BLOCK / kWave>(r.local_sumexp(n, c, m2), red);
+  r.opaque();
+  return m2 + log2_fast(s);
+}
+
+// Streaming row log-sum-exp (any length): per-lane online (max, sum), then a block combine.
+template <typename T, int VEC, int BLOCK>
+__device__ __forceinline__ float row_lse2_stream(const T* __restrict__ row, int n, float c, float* red) {
+  float m = -INFINITY, s = 0.f;
+  for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC) {
+    float x[VEC];
+    unpack(load_pack<T, VEC>(row + col), x);
+    float tm = x[0];
+#pragma unroll
+    for (int e = 1; e < VEC; ++e) tm = fmaxf(tm, x[e]);
+    const float mn = fmaxf(m, tm * c);
+    float add = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) add += exp2_fast(fmaf(x[e], c, -mn));
+    s = (m == -INFINITY ? 0.f : s * exp2_fast(m - mn)) + add;
+    m = mn;
+  }
+  const float M = block_max<BLOCK / kWave>(m, red);
+  const float sc = (m == -INFINITY) ? 0.f : s * exp2_fast(m - M);
+  const float S = block_sum<BLOCK / kWave>(sc, red);
+  return M + log2_fast(S);
+}
+
+template <typename T, int VEC, int BLOCK>
+__device__ __forceinline__ void store_grad_stream(T* __restrict__ out, const T* __restrict__ row, int n, float c,
+                                                  float lse2, int target, float g) {
+  for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC) {
+    float x[VEC];
+    unpack(load_pack<T, VEC>(row + col), x);
+    const int rel = target - col;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float p = exp2_fast(fmaf(x[e], c, -lse2));
+      x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
+    }
+    store_pack_nt<T, VEC>(out + col, pack<T, VEC>(x));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// CrossEntropy
+// ---------------------------------------------------------------------------
+struct CeArgs {
+  const int64_t* targets;
+  float* loss_rows;
+  float* lse_rows;  // inference path only
+  const int* n_valid;
+  int64_t rows, V, ld_in, ld_out, ignore_index;
+  int has_ignore;
+  int scale_by_n_valid;
+};
+
+__device__ __forceinline__ float ce_scale(const CeArgs& a) {
+  return a.scale_by_n_valid ? 1.f / fmaxf((float)*a.n_valid, 1.f) : 1.f;
+}
+
+// Training forward: loss_r = (lse - x_t) * s and dlogits = (softmax - onehot) * s
+// (kernels/cross_entropy.py:114-166). Ignored rows: loss 0 and a zero row.
+template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
+__global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
+                                                            CeArgs a) {
+  __shared__ float red[BLOCK / kWave];
+  const float scale = ce_scale(a);
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const int64_t t = a.targets[row];
+    T* out = dlogits + row * a.ld_out;
+    const T* in = logits + row * a.ld_in;
+    if (a.has_ignore && t == a.ignore_index) {
+      fill_row<T, VEC, BLOCK>(out, (int)a.V, 0.f);
+      if (threadIdx.x == 0) a.loss_rows[row] = 0.f;
+      continue;
+    }
+    if (t < 0 || t >= a.V) {  // out-of-range target: NaN loss and gradient, no out-of-bounds read
+      fill_row<T, VEC, BLOCK>(out, (int)a.V, NAN);
+      if (threadIdx.x == 0) a.loss_rows[row] = NAN;
+      continue;
+    }
+    const float xt = to_f32<T>(in[t]);
+    if constexpr (RESIDENT) {
+      const int n = row_len(a.V);
+      RowRegs<T, VEC, NCH, BLOCK> r;
+      r.load(in, n);
+      const float lse2 = row_lse2(r, n, kLog2e, red);
+      if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
+      r.store_grad(out, n, kLog2e, lse2, (int)t, scale);
+    } else {
+      const float lse2 = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red);
+      if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
+      store_grad_stream<T, VEC, BLOCK>(out, in, (int)a.V, kLog2e, lse2, (int)t, scale);
+    }
+  }
+}
+
+// Inference forward (kernels/cross_entropy.py:32-65): lse and lse - x_t (0 if ignored).
+template <typename T, int VEC, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void ce_fwd_kernel(const T* __restrict__ logits, CeArgs a) {
+  __shared__ float red[BLOCK / kWave];
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const T* in = logits + row * a.ld_in;
+    const float lse = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red) * kLn2;
+    if (threadIdx.x == 0) {
+      const int64_t t = a.targets[row];
+      float loss;
+      if (a.has_ignore && t == a.ignore_index) loss = 0.f;
+      else if (t < 0 || t >= a.V) loss = NAN;
+      else loss = lse - to_f32<T>(in[t]);
+      a.lse_rows[row] = lse;
+      a.loss_rows[row] = loss;
+    }
+  }
+}
+
+// n_valid = #targets != ignore_index (all rows when there is no ignore index)
+__global__ __launch_bounds__(1024) void count_valid_kernel(int* __restrict__ n_valid, const int64_t* __restrict__ t,
+                                                           int64_t rows, int64_t ignore_index, int has_ignore) {
+  __shared__ float red[16];
+  float c = 0.f;
+  for (int64_t i = threadIdx.x; i < rows; i += 1024) c += (!has_ignore || t[i] != ignore_index) ? 1.f : 0.f;
+  // counts up to 2^24 are exact in fp32; larger inputs use the int path below
+  c = block_sum<16>(c, red);
+  if (threadIdx.x == 0) *n_valid = rows < (1 << 24) ? (int)c : -1;
+  if (rows >= (1 << 24)) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int64_t n = 0;
+      for (int64_t i = 0; i < rows; ++i) n += (!has_ignore || t[i] != ignore_index);
+      *n_valid = (int)(n > 0x7fffffff ? 0x7fffffff : n);
+    }
+  }
+}
+
+// out[0] = sum(loss_rows) (fp64 accumulation), divided by max(n_valid, 1) when requested
+__global__ __launch_bounds__(1024) void sum_rows_kernel(float* __restrict__ out, const float* __restrict__ v,
+                                                        int64_t n, const int* __restrict__ n_valid, int divide) {
+  __shared__ double red[16];
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += (double)v[i];
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int i = 0; i < 16; ++i) t += red[i];
+    if (divide) t /= (double)(*n_valid > 1 ? *n_valid : 1);
+    out[0] = (float)t;
+  }
+}
+
+// out = in * g (g scalar or per row); with g_prev, out = in * g / g_prev (0 where g_prev = 0).
+// skip_if_one: a scalar g equal to 1 (and no g_prev) leaves the data untouched.
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void scale_rows_kernel(T* __restrict__ out, const T* __restrict__ in,
+                                                         const float* __restrict__ g, const float* __restrict__ g_prev,
+                                                         int per_row, int skip_if_one, int64_t rows, int64_t cols,
+                                                         int64_t ld_in, int64_t ld_out) {
+  if (!per_row && skip_if_one && g_prev == nullptr && g[0] == 1.f && out == in) return;
+  const int64_t nv = cols / VEC;
+  const int64_t total = rows * nv;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / nv, cv = (i - r * nv) * VEC;
+    float f = per_row ? g[r] : g[0];
+    if (g_prev) {
+      const float p = per_row ? g_prev[r] : g_prev[0];
+      f = p != 0.f ? f / p : 0.f;
+    }
+    float x[VEC];
+    unpack(load_pack<T, VEC>(in + r * ld_in + cv), x);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) x[e] *= f;
+    store_pack<T, VEC>(out + r * ld_out + cv, pack<T, VEC>(x));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// selective log-softmax and GRPO
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float load_mask(const void* m, int dt, int64_t off) {
+  switch (dt) {
+    case HK_F32: return ((const float*)m)[off];
+    case HK_F16: return (float)((const _Float16*)m)[off];
+    case HK_BF16: return (float)((const __bf16*)m)[off];
+    case HK_U8: return (float)((const uint8_t*)m)[off];
+    case HK_I32: return (float)((const int32_t*)m)[off];
+    case HK_I64: return (float)((const int64_t*)m)[off];
+  }
+  return 1.f;
+}
+
+struct GrpoArgs {
+  const int64_t* ids;
+  int64_t ids_sB, ids_sL;
+  const float* adv;
+  const float* old_logp;
+  int64_t old_sB, old_sL;
+  const float* ref_logp;
+  int64_t ref_sB, ref_sL;
+  const void* mask;
+  int mask_dt;
+  int64_t mask_sB, mask_sL;
+  int64_t B, L, V;
+  float inv_T, beta, eps_lo, eps_hi;
+  float* lse_rows;       // [B, L] outputs
+  float* loss_rows;
+  float* kl_rows;
+  float* clip_rows;
+  float* logp_out;       // selective log-softmax output [B, L]
+};
+
+// logp[b, l] = x[b, l, id] / T - logsumexp(x[b, l, :] / T) for unmasked l < L
+// (kernels/grpo_loss.py:29-62); logits are (B, L+1, V) contiguous.
+template <typename T, int VEC, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void selective_log_softmax_kernel(const T* __restrict__ logits, GrpoArgs a) {
+  __shared__ float red[BLOCK / kWave];
+  const int64_t rows = a.B * a.L;
+  const float c = kLog2e * a.inv_T;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const int64_t b = r / a.L, l = r - b * a.L;
+    if (a.mask && load_mask(a.mask, a.mask_dt, b * a.mask_sB + l * a.mask_sL) == 0.f) {
+      if (threadIdx.x == 0) a.logp_out[r] = 0.f;
+      continue;
+    }
+    const T* in = logits + (b * (a.L + 1) + l) * a.V;
+    const float lse = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, c, red) * kLn2;
+    if (threadIdx.x == 0) {
+      const int64_t id = a.ids[b * a.ids_sB + l * a.ids_sL];
+      a.logp_out[r] = (id >= 0 && id < a.V) ? to_f32<T>(in[id]) * a.inv_T - lse : NAN;
+    }
+  }
+}
+
+// Per-token inputs of the fused GRPO kernel, gathered by grpo_prep_kernel so
+// the hot kernel carries a handful of arguments instead of ~30 (its row loop
+// otherwise runs out of SGPRs and spills).
+struct alignas(16) GrpoTok {
+  int32_t id;   // completion token id (-1 if out of range)
+  float old;    // old policy log-prob (unused when the call has none)
+  float ref;    // reference log-prob (unused when beta == 0)
+  float adv;    // advantage of the sequence
+  float m;      // mask value (0: token skipped)
+  float gs;     // m / (max(len_b, 1) * B) / T: dloss / T at unit upstream gradient
+  float pad0, pad1;
+};
+struct alignas(16) GrpoOut {
+  float lse, loss, kl, clip;
+};
+
+struct GrpoHot {
+  const GrpoTok* tok;
+  GrpoOut* out;
+  int64_t B, L, V;
+  float inv_T, beta, eps_lo, eps_hi;
+  int has_old;
+};
+
+// GRPO forward with the gradient fused in (kernels/grpo_loss.py:87-159 forward,
+// :166-234 backward at unit upstream gradient). Rows are all B*(L+1) positions
+// of the logits; the last position and masked tokens get a zero gradient row.
+template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT, bool GRAD>
+__global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
+                                                     GrpoHot a) {
+  __shared__ float red[BLOCK / kWave];
+  const int64_t rows = a.B * (a.L + 1);
+  const float c = kLog2e * a.inv_T;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t b = row / (a.L + 1), l = row - b * (a.L + 1);
+    T* out = GRAD ? dlogits + row * a.V : nullptr;
+    const int64_t o = b * a.L + l;  // token index (valid when l < L)
+    GrpoTok tk{};
+    if (l < a.L) tk = a.tok[o];
+    if (l == a.L || tk.m == 0.f) {
+      if constexpr (GRAD) fill_row<T, VEC, BLOCK>(out, (int)a.V, 0.f);
+      if (l < a.L && threadIdx.x == 0) a.out[o] = GrpoOut{0.f, 0.f, 0.f, 0.f};
+      continue;
+    }
+    const T* in = logits + row * a.V;
+    const int n = row_len(a.V);
+    float lse2;
+    RowRegs<T, VEC, NCH, BLOCK> r;
+    if constexpr (RESIDENT) {
+      r.load(in, n);
+      lse2 = row_lse2(r, n, c, red);
+    } else {
+      lse2 = row_lse2_stream<T, VEC, BLOCK>(in, n, c, red);
+    }
+    const float lse = lse2 * kLn2;
+    const float logp = tk.id >= 0 ? to_f32<T>(in[tk.id]) * a.inv_T - lse : NAN;
+    const float old = a.has_old ? tk.old : logp;
+    const float coef1 = exp_fast(logp - old);
+    const float A = tk.adv;
+    const float coef2 = fminf(fmaxf(coef1, 1.f - a.eps_lo), 1.f + a.eps_hi);
+    const float l1 = coef1 * A, l2 = coef2 * A;
+    float loss = -fminf(l1, l2);
+    float kl = 0.f;
+    float dlogp = l2 >= l1 ? -coef1 * A : 0.f;
+    if (a.beta != 0.f) {
+      const float d = tk.ref - logp;
+      const float ed = exp_fast(d);
+      kl = ed - d - 1.f;
+      loss += a.beta * kl;
+      dlogp += a.beta * (1.f - ed);
+    }
+    if (threadIdx.x == 0) {
+      const bool clipped = (coef1 < 1.f - a.eps_lo && A < 0.f) || (coef1 > 1.f + a.eps_hi && A > 0.f);
+      a.out[o] = GrpoOut{lse, loss, kl, clipped ? 1.f : 0.f};
+    }
+    if constexpr (GRAD) {
+      // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
+      const float g = -dlogp * tk.gs;
+      if constexpr (RESIDENT) r.store_grad(out, n, c, lse2, tk.id, g);
+      else store_grad_stream<T, VEC, BLOCK>(out, in, n, c, lse2, tk.id, g);
+    }
+  }
+}
+
+// One block per sequence b: len_b = sum_l mask[b, l], then the token records.
+__global__ __launch_bounds__(1024) void grpo_prep_kernel(GrpoArgs a, GrpoTok* __restrict__ tok) {
+  __shared__ float red[16];
+  const int64_t b = blockIdx.x;
+  float s = 0.f;
+  for (int64_t l = threadIdx.x; l < a.L; l += 1024)
+    s += a.mask ? load_mask(a.mask, a.mask_dt, b * a.mask_sB + l * a.mask_sL) : 1.f;
+  s = block_sum<16>(s, red);
+  const float inv_len = 1.f / (fmaxf(s, 1.f) * (float)a.B);
+  const float A = a.adv[b];
+  for (int64_t l = threadIdx.x; l < a.L; l += 1024) {
+    GrpoTok t{};
+    const int64_t id = a.ids[b * a.ids_sB + l * a.ids_sL];
+    t.id = (id >= 0 && id < a.V) ? (int32_t)id : -1;
+    t.old = a.old_logp ? a.old_logp[b * a.old_sB + l * a.old_sL] : 0.f;
+    t.ref = a.ref_logp ? a.ref_logp[b * a.ref_sB + l * a.ref_sL] : 0.f;
+    t.adv = A;
+    t.m = a.mask ? load_mask(a.mask, a.mask_dt, b * a.mask_sB + l * a.mask_sL) : 1.f;
+    t.gs = t.m * inv_len * a.inv_T;
+    tok[b * a.L + l] = t;
+  }
+}
+
+// out = [mean_b(sum_l m*loss / max(len_b,1)), sum m*kl / max(sum m,1), sum m*clip / max(sum m,1)]
+// (kernels/grpo_loss.py:290-295); also scatters the per-token rows.
+__global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const GrpoTok* __restrict__ tok,
+                                                             const GrpoOut* __restrict__ res, float* __restrict__ loss_out,
+                                                             float* __restrict__ kl_out, float* __restrict__ clip_out) {
+  __shared__ double red[16];
+  auto bsum = [&](double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < 16; ++i) t += red[i];
+    __syncthreads();
+    return t;
+  };
+  double loss = 0.0, msum = 0.0, kls = 0.0, clips = 0.0;
+  for (int64_t b = 0; b < a.B; ++b) {
+    double ls = 0.0, ms = 0.0, ks = 0.0, cs = 0.0;
+    for (int64_t l = threadIdx.x; l < a.L; l += 1024) {
+      const int64_t o = b * a.L + l;
+      const double m = tok[o].m;
+      const GrpoOut r = res[o];
+      ls += m * r.loss;
+      ms += m;
+      ks += m * r.kl;
+      cs += m * r.clip;
+      a.lse_rows[o] = r.lse;
+      a.loss_rows[o] = r.loss;
+      a.kl_rows[o] = r.kl;
+      a.clip_rows[o] = r.clip;
+    }
+    ls = bsum(ls);
+    ms = bsum(ms);
+    ks = bsum(ks);
+    cs = bsum(cs);
+    loss += ls / (ms > 1.0 ? ms : 1.0);
+    msum += ms;
+    kls += ks;
+    clips += cs;
+  }
+  if (threadIdx.x == 0) {
+    const double d = msum > 1.0 ? msum : 1.0;
+    loss_out[0] = (float)(loss / (double)a.B);
+    if (kl_out) kl_out[0] = (float)(kls / d);
+    clip_out[0] = (float)(clips / d);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host-side configuration
+// ---------------------------------------------------------------------------
+template <typename T> struct Tag { using type = T; };
+
+template <typename F>
+int dispatch_t(int dt, F&& f) {
+  switch (dt) {
+    case HK_F32: return f(Tag<float>{});
+    case HK_F16: return f(Tag<_Float16>{});
+    case HK_BF16: return f(Tag<__bf16>{});
+  }
+  set_error("invalid logits dtype code %d", dt);
+  return HK_EINVAL;
+}
+
+// (block, vectors per lane) pairs with a register-resident instantiation
+struct RowCfg {
+  int block;
+  int nch;  // 0: streaming
+  int vec;  // elements per vector
+};
+
+RowCfg choose_row_cfg(int64_t V, int esize, bool vec_ok) {
+  RowCfg c{1024, 0, vec_ok ? 16 / esize : 1};
+  if (!vec_ok) return c;
+  const int64_t nv = V / c.vec;
+  static const int small[] = {1, 2, 4, 8};
+  for (int n : small)
+    if (nv <= 256LL * n) return RowCfg{256, n, c.vec};
+  static const int big[] = {12, 16, 20, 24};
+  for (int n : big)
+    if (nv <= 1024LL * n) return RowCfg{1024, n, c.vec};
+  return c;
+}
+
+template <typename F>
+int dispatch_cfg(const RowCfg& c, F&& f) {
+  using std::integral_constant;
+  if (c.nch == 0) return f(integral_constant<int, 1024>{}, integral_constant<int, 0>{});
+  if (c.block == 256) {
+    switch (c.nch) {
+      case 1: return f(integral_constant<int, 256>{}, integral_constant<int, 1>{});
+      case 2: return f(integral_constant<int, 256>{}, integral_constant<int, 2>{});
+      case 4: return f(integral_constant<int, 256>{}, integral_constant<int, 4>{});
+      case 8: return f(integral_constant<int, 256>{}, integral_constant<int, 8>{});
+    }
+  } else {
+    switch (c.nch) {
+      case 12: return f(integral_constant<int, 1024>{}, integral_constant<int, 12>{});
+      case 16: return f(integral_constant<int, 1024>{}, integral_constant<int, 16>{});
+      case 20: return f(integral_constant<int, 1024>{}, integral_constant<int, 20>{});
+      case 24: return f(integral_constant<int, 1024>{}, integral_constant<int, 24>{});
+    }
+  }
+  set_error("internal: bad row config (%d, %d)", c.block, c.nch);
+  return HK_EINVAL;
+}
+
+int64_t persistent_grid(int64_t rows, int block) {
+  const int dev = current_device();
+  const int cu = dev >= 0 ? cu_count(dev) : 256;
+  const int64_t per_cu = block >= 1024 ? 2 : 8;
+  const int64_t g = (int64_t)(cu > 0 ? cu : 256) * per_cu;
+  return rows < g ? (rows > 0 ? rows : 1) : g;
+}
+
+bool valid_float_dtype(int dt) { return dt == HK_F32 || dt == HK_F16 || dt == HK_BF16; }
+bool valid_mask_dtype(int dt) {
+  return dt == HK_F32 || dt == HK_F16 || dt == HK_BF16 || dt == HK_U8 || dt == HK_I32 || dt == HK_I64;
+}
+int esize(int dt) { return dt == HK_F32 ? 4 : 2; }
+
+}  // namespace
+}  // namespace hk
+
+using namespace hk;
+
+extern "C" {
+
+size_t hk_cross_entropy_workspace_size(int64_t rows) {
+  (void)rows;
+  return 256;
+}
+
+int hk_cross_entropy_fwd_grad(void* dlogits, float* loss_rows, float* loss_out, const void* logits,
+                              const int64_t* targets, int64_t rows, int64_t V, int64_t ld_logits, int64_t ld_dlogits,
+                              int64_t ignore_index, int reduction, int dtype, void* workspace, size_t workspace_bytes,
+                              hk_stream_t stream) {
+  HK_REQUIRE(valid_float_dtype(dtype), "invalid logits dtype code %d", dtype);
+  HK_REQUIRE(rows >= 0 && V > 0, "invalid shape rows=%lld V=%lld", (long long)rows, (long long)V);
+  HK_REQUIRE(ld_logits >= V && ld_dlogits >= V, "row stride smaller than V");
+  HK_REQUIRE(V < (1LL << 31) - 4096, "V=%lld too large", (long long)V);
+  HK_REQUIRE(reduction >= HK_REDUCTION_NONE && reduction <= HK_REDUCTION_SUM, "invalid reduction %d", reduction);
+  HK_REQUIRE(workspace && workspace_bytes >= 256, "workspace must hold at least 256 bytes");
+  HK_REQUIRE(rows == 0 || (dlogits && loss_rows && logits && targets), "null pointer argument");
+  const int es = esize(dtype);
+  hipStream_t st = (hipStream_t)stream;
+  CeArgs a{};
+  a.targets = targets;
+  a.loss_rows = loss_rows;
+  a.n_valid = (const int*)workspace;
+  a.rows = rows;
+  a.V = V;
+  a.ld_in = ld_logits;
+  a.ld_out = ld_dlogits;
+  a.ignore_index = ignore_index;
+  // ignore_index == -1 is the reference's "ignore nothing" sentinel (cross_entropy.py:197-198,219-225)
+  a.has_ignore = ignore_index != -1;
+  a.scale_by_n_valid = reduction == HK_REDUCTION_MEAN;
+  if (rows > 0) {
+    hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, (int*)workspace, targets, rows, ignore_index,
+                       a.has_ignore);
+    int rc = check_launch("count_valid_kernel");
+    if (rc) return rc;
+    const int vec = 16 / es;
+    const bool vec_ok = V % vec == 0 && aligned_to(logits, 16) && aligned_to(dlogits, 16) &&
+                        (ld_logits * es) % 16 == 0 && (ld_dlogits * es) % 16 == 0;
+    const RowCfg cfg = choose_row_cfg(V, es, vec_ok);
+    rc = dispatch_t(dtype, [&](auto tt) {
+      using T = typename decltype(tt)::type;
+      return dispatch_cfg(cfg, [&](auto blk, auto nch) {
+        constexpr int BLOCK = decltype(blk)::value;
+        constexpr int NCH = decltype(nch)::value;
+        const dim3 grid((unsigned)persistent_grid(rows, BLOCK));
+        if (cfg.vec == 1) {
+          hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 1, 1, 1024, false>), grid, dim3(1024), 0, st, (T*)dlogits,
+                             (const T*)logits, a);
+        } else if constexpr (NCH == 0) {
+          hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>), grid, dim3(BLOCK), 0, st,
+                             (T*)dlogits, (const T*)logits, a);
+        } else {
+          hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>), grid, dim3(BLOCK), 0, st,
+                             (T*)dlogits, (const T*)logits, a);
+        }
+        return check_launch("ce_fwd_grad_kernel");
+      });
+    });
+    if (rc) return rc;
+  }
+  if (loss_out) {
+    if (rows == 0) {
+      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, (int64_t)0,
+                         (const int*)nullptr, 0);
+    } else {
+      // the rows are already scaled by 1/max(n_valid, 1) for 'mean'
+      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, rows, (const int*)nullptr,
+                         0);
+    }
+    return check_launch("sum_rows_kernel");
+  }
+  return HK_OK;
+}
+
+int hk_cross_entropy_fwd(float* lse_rows, float* loss_rows, float* loss_out, const void* logits,
+                         const int64_t* targets, int64_t rows, int64_t V, int64_t ld_logits, int64_t ignore_index,
+                         int reduction, int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+  HK_REQUIRE(valid_float_dtype(dtype), "invalid logits dtype code %d", dtype);
+  HK_REQUIRE(rows >= 0 && V > 0, "invalid shape rows=%lld V=%lld", (long long)rows, (long long)V);
+  HK_REQUIRE(ld_logits >= V, "row stride smaller than V");
+  HK_REQUIRE(V < (1LL << 31) - 4096, "V=%lld too large", (long long)V);
+  HK_REQUIRE(reduction >= HK_REDUCTION_NONE && reduction <= HK_REDUCTION_SUM, "invalid reduction %d", reduction);
+  HK_REQUIRE(workspace && workspace_bytes >= 256, "workspace must hold at least 256 bytes");
+  HK_REQUIRE(rows == 0 || (lse_rows && loss_rows && logits && targets), "null pointer argument");
+  const int es = esize(dtype);
+  hipStream_t st = (hipStream_t)stream;
+  CeArgs a{};
+  a.targets = targets;
+  a.loss_rows = loss_rows;
+  a.lse_rows = lse_rows;
+  a.rows = rows;
+  a.V = V;
+  a.ld_in = ld_logits;
+  a.ignore_index = ignore_index;
+  a.has_ignore = ignore_index != -1;
+  if (rows > 0) {
+    hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, (int*)workspace, targets, rows, ignore_index,
+                       a.has_ignore);
+    int rc = check_launch("count_valid_kernel");
+    if (rc) return rc;
+    const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (ld_logits * es) % 16 == 0;
+    rc = dispatch_t(dtype, [&](auto tt) {
+      using T = typename decltype(tt)::type;
+      const dim3 grid((unsigned)persistent_grid(rows, 1024));
+      if (vec_ok)
+        hipLaunchKernelGGL((ce_fwd_kernel<T, 16 / sizeof(T), 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
+      else
+        hipLaunchKernelGGL((ce_fwd_kernel<T, 1, 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
+      return check_launch("ce_fwd_kernel");
+    });
+    if (rc) return rc;
+  }
+  if (loss_out) {
+    if (rows == 0) {
+      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, (int64_t)0,
+                         (const int*)nullptr, 0);
+    } else {
+      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, rows,
+                         (const int*)workspace, reduction == HK_REDUCTION_MEAN ? 1 : 0);
+    }
+    return check_launch("sum_rows_kernel");
+  }
+  return HK_OK;
+}
+
+int hk_scale_rows(void* out, const void* in, const float* g, const float* g_prev, int per_row, int skip_if_one,
+                  int64_t rows, int64_t cols, int64_t ld_in, int64_t ld_out, int dtype, hk_stream_t stream) {
+  HK_REQUIRE(valid_float_dtype(dtype), "invalid dtype code %d", dtype);
+  HK_REQUIRE(rows >= 0 && cols >= 0, "invalid shape");
+  HK_REQUIRE(ld_in >= cols && ld_out >= cols, "row stride smaller than cols");
+  if (rows == 0 || cols == 0) return HK_OK;
+  HK_REQUIRE(out && in && g, "null pointer argument");
+  const int es = esize(dtype);
+  const int vec = 16 / es;
+  const bool vec_ok = cols % vec == 0 && aligned_to(in, 16) && aligned_to(out, 16) && (ld_in * es) % 16 == 0 &&
+                      (ld_out * es) % 16 == 0;
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    const int64_t total = rows * (vec_ok ? cols / vec : cols);
+    const int64_t blocks = cdiv(total, 256 * 4);
+    const dim3 grid((unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536));
+    if (vec_ok)
+      hipLaunchKernelGGL((scale_rows_kernel<T, 16 / sizeof(T)>), grid, dim3(256), 0, st, (T*)out, (const T*)in, g,
+                         g_prev, per_row, skip_if_one, rows, cols, ld_in, ld_out);
+    else
+      hipLaunchKernelGGL((scale_rows_kernel<T, 1>), grid, dim3(256), 0, st, (T*)out, (const T*)in, g, g_prev, per_row,
+                         skip_if_one, rows, cols, ld_in, ld_out);
+    return check_launch("scale_rows_kernel");
+  });
+}
+
+int hk_selective_log_softmax(float* logp, const void* logits, const int64_t* ids, int64_t ids_sB, int64_t ids_sL,
+                             const void* mask, int mask_dtype, int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L,
+                             int64_t V, float temperature, int dtype, hk_stream_t stream) {
+  HK_REQUIRE(valid_float_dtype(dtype), "invalid logits dtype code %d", dtype);
+  HK_REQUIRE(B >= 0 && L >= 0 && V > 0, "invalid shape B=%lld L=%lld V=%lld", (long long)B, (long long)L,
+             (long long)V);
+  HK_REQUIRE(temperature > 0.f, "temperature must be positive");
+  HK_REQUIRE(!mask || valid_mask_dtype(mask_dtype), "invalid mask dtype code %d", mask_dtype);
+  HK_REQUIRE(V < (1LL << 31) - 4096, "V=%lld too large", (long long)V);
+  if (B * L == 0) return HK_OK;
+  HK_REQUIRE(logp && logits && ids, "null pointer argument");
+  GrpoArgs a{};
+  a.ids = ids;
+  a.ids_sB = ids_sB;
+  a.ids_sL = ids_sL;
+  a.mask = mask;
+  a.mask_dt = mask_dtype;
+  a.mask_sB = mask_sB;
+  a.mask_sL = mask_sL;
+  a.B = B;
+  a.L = L;
+  a.V = V;
+  a.inv_T = 1.f / temperature;
+  a.logp_out = logp;
+  const int es = esize(dtype);
+  const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16);
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    const dim3 grid((unsigned)persistent_grid(B * L, 1024));
+    if (vec_ok)
+      hipLaunchKernelGGL((selective_log_softmax_kernel<T, 16 / sizeof(T), 1024>), grid, dim3(1024), 0, st,
+                         (const T*)logits, a);
+    else
+      hipLaunchKernelGGL((selective_log_softmax_kernel<T, 1, 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
+    return check_launch("selective_log_softmax_kernel");
+  });
+}
+
+size_t hk_grpo_workspace_size(int64_t B, int64_t L) {
+  if (B < 0 || L < 0) return 0;
+  // token records then per-token results
+  return (size_t)(B * L) * (sizeof(GrpoTok) + sizeof(GrpoOut)) + 256;
+}
+
+int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_out, float* lse_rows,
+                     float* loss_rows, float* kl_rows, float* clip_rows, const void* logits, const int64_t* ids,
+                     int64_t ids_sB, int64_t ids_sL, const float* advantages, const float* old_logp, int64_t old_sB,
+                     int64_t old_sL, const float* ref_logp, int64_t ref_sB, int64_t ref_sL, const void* mask,
+                     int mask_dtype, int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t V,
+                     float temperature, float beta, float eps_low, float eps_high, int dtype, void* workspace,
+                     size_t workspace_bytes, hk_stream_t stream) {
+  HK_REQUIRE(valid_float_dtype(dtype), "invalid logits dtype code %d", dtype);
+  HK_REQUIRE(B > 0 && L >= 0 && V > 0, "invalid shape B=%lld L=%lld V=%lld", (long long)B, (long long)L,
+             (long long)V);
+  HK_REQUIRE(temperature > 0.f, "temperature must be positive");
+  HK_REQUIRE(!mask || valid_mask_dtype(mask_dtype), "invalid mask dtype code %d", mask_dtype);
+  HK_REQUIRE(beta == 0.f || ref_logp != nullptr, "beta != 0 needs ref_logp");
+  HK_REQUIRE(V < (1LL << 31) - 4096, "V=%lld too large", (long long)V);
+  HK_REQUIRE(workspace && workspace_bytes >= hk_grpo_workspace_size(B, L), "workspace too small");
+  HK_REQUIRE(loss_out && clip_out && logits && ids && advantages && (L == 0 || (lse_rows && loss_rows && kl_rows && clip_rows)),
+             "null pointer argument");
+  GrpoArgs a{};
+  a.ids = ids;
+  a.ids_sB = ids_sB;
+  a.ids_sL = ids_sL;
+  a.adv = advantages;
+  a.old_logp = old_logp;
+  a.old_sB = old_sB;
+  a.old_sL = old_sL;
+  a.ref_logp = ref_logp;
+  a.ref_sB = ref_sB;
+  a.ref_sL = ref_sL;
+  a.mask = mask;
+  a.mask_dt = mask_dtype;
+  a.mask_sB = mask_sB;
+  a.mask_sL = mask_sL;
+  a.B = B;
+  a.L = L;
+  a.V = V;
+  a.inv_T = 1.f / temperature;
+  a.beta = beta;
+  a.eps_lo = eps_low;
+  a.eps_hi = eps_high;
+  a.lse_rows = lse_rows;
+  a.loss_rows = loss_rows;
+  a.kl_rows = kl_rows;
+  a.clip_rows = clip_rows;
+  hipStream_t st = (hipStream_t)stream;
+  HK_REQUIRE(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
+  GrpoTok* tok = (GrpoTok*)workspace;
+  GrpoOut* res = (GrpoOut*)((char*)workspace + (size_t)(B * L) * sizeof(GrpoTok));
+  GrpoHot h{};
+  h.tok = tok;
+  h.out = res;
+  h.B = B;
+  h.L = L;
+  h.V = V;
+  h.inv_T = a.inv_T;
+  h.beta = beta;
+  h.eps_lo = eps_low;
+  h.eps_hi = eps_high;
+  h.has_old = old_logp != nullptr;
+  if (L > 0) {
+    hipLaunchKernelGGL(grpo_prep_kernel, dim3((unsigned)B), dim3(1024), 0, st, a, tok);
+    int rc = check_launch("grpo_prep_kernel");
+    if (rc) return rc;
+  }
+  int rc = HK_OK;
+  const int es = esize(dtype);
+  const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (!dlogits || aligned_to(dlogits, 16));
+  const RowCfg cfg = choose_row_cfg(V, es, vec_ok);
+  const int64_t rows = B * (L + 1);
+  rc = dispatch_t(dtype, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    return dispatch_cfg(cfg, [&](auto blk, auto nch) {
+      constexpr int BLOCK = decltype(blk)::value;
+      constexpr int NCH = decltype(nch)::value;
+      const dim3 grid((unsigned)persistent_grid(rows, BLOCK));
+      auto go = [&](auto grad_c) {
+        constexpr bool GRAD = decltype(grad_c)::value;
+        if (cfg.vec == 1) {
+          hipLaunchKernelGGL((grpo_kernel<T, 1, 1, 1024, false, GRAD>), grid, dim3(1024), 0, st, (T*)dlogits,
+                             (const T*)logits, h);
+        } else if constexpr (NCH == 0) {
+          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>), grid, dim3(BLOCK), 0, st,
+                             (T*)dlogits, (const T*)logits, h);
+        } else {
+          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>), grid, dim3(BLOCK), 0, st,
+                             (T*)dlogits, (const T*)logits, h);
+        }
+        return check_launch("grpo_kernel");
+      };
+      if (dlogits) return go(std::true_type{});
+      return go(std::false_type{});
+    });
+  });
+  if (rc) return rc;
+  hipLaunchKernelGGL(grpo_finalize_kernel, dim3(1), dim3(1024), 0, st, a, (const GrpoTok*)tok, (const GrpoOut*)res,
+                     loss_out, kl_out, clip_out);
+  return check_launch("grpo_finalize_kernel");
+}
+
+}  // extern "C"

@@ -85,9 +85,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_fwd_kernel(
     if (valid && col < cols) {
       float a[VEC];
       unpack(xv[j], a);
-      Pack<W, VEC> wv = load_pack<W, VEC>(w + col);
+      float wf[VEC];
+      unpack(load_pack<W, VEC>(w + col), wf);
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) a[i] = round_through<T>(a[i] * rstd) * to_f32<W>(wv.v[i]);
+      for (int i = 0; i < VEC; ++i) a[i] = round_through<T>(a[i] * rstd) * wf[i];
       store_pack<T, VEC>(y + row * ld_y + col, pack<T, VEC>(a));
     }
   }
@@ -115,11 +116,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_bwd_kernel(
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int col = (j * gl + lr) * VEC;
-    Pack<W, VEC> wv;
-    if (col < cols) wv = load_pack<W, VEC>(w + col);
+    float wv[VEC];
+    if (col < cols) unpack(load_pack<W, VEC>(w + col), wv);
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      wf[j][i] = col < cols ? to_f32<W>(wv.v[i]) : 0.f;
+      wf[j][i] = col < cols ? wv[i] : 0.f;
       acc[j][i] = 0.0;
     }
   }

@@ -9,11 +9,15 @@ with the reference.
 from .rms_norm import HildaRMSNormFunction, hilda_rms_norm, RMSNorm
 from .rope import HildaRopeFunction, hilda_rope, RotaryEmbedding
 from .swiglu import HildaSwiGLUFunction, hilda_swiglu, SwiGLU
+from .cross_entropy import HildaCrossEntropyFunction, hilda_cross_entropy, CrossEntropyLoss
 from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
+from .grpo_loss import HildaGRPOLossFunction, hilda_grpo_loss, GRPOLoss, fused_selective_log_softmax
 
 __all__ = [
     "HildaRMSNormFunction", "hilda_rms_norm", "RMSNorm",
     "HildaRopeFunction", "hilda_rope", "RotaryEmbedding",
     "HildaSwiGLUFunction", "hilda_swiglu", "SwiGLU",
+    "HildaCrossEntropyFunction", "hilda_cross_entropy", "CrossEntropyLoss",
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
+    "HildaGRPOLossFunction", "hilda_grpo_loss", "GRPOLoss", "fused_selective_log_softmax",
 ]

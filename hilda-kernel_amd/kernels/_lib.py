@@ -15,10 +15,13 @@ import torch
 LIB_NAME = "libhilda_kernel_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 DW_AUTO, DW_ATOMIC, DW_PARTIAL = 0, 1, 2
+REDUCTION = {"none": 0, "mean": 1, "sum": 2}
 
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+_MASK_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.bool: U8, torch.uint8: U8,
+              torch.int32: I32, torch.int64: I64}
 
 _i32, _i64, _f32, _p, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 
@@ -36,6 +39,15 @@ SIGNATURES = {
                        _i32, _i32, _i32, _p]),
     "hk_swiglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "hk_swiglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
+    "hk_cross_entropy_workspace_size": (_sz, [_i64]),
+    "hk_cross_entropy_fwd_grad": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
+    "hk_cross_entropy_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
+    "hk_scale_rows": (_i32, [_p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _i32, _p]),
+    "hk_selective_log_softmax": (_i32, [_p, _p, _p, _i64, _i64, _p, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
+                                        _p]),
+    "hk_grpo_workspace_size": (_sz, [_i64, _i64]),
+    "hk_grpo_loss_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _p,
+                                _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _i32, _p, _sz, _p]),
 }
 
 ABI_VERSION = 1
@@ -102,6 +114,13 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
         elif t.device != dev:
             raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
     return dev
+
+
+def mask_code(t: torch.Tensor) -> int:
+    try:
+        return _MASK_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported mask dtype {t.dtype}") from None
 
 
 def stream_of(device: torch.device) -> int:

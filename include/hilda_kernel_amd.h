@@ -32,6 +32,15 @@ extern "C" {
 #define HK_F32 0
 #define HK_F16 1
 #define HK_BF16 2
+/* integer codes, used for masks */
+#define HK_U8 3
+#define HK_I32 4
+#define HK_I64 5
+
+/* loss reductions */
+#define HK_REDUCTION_NONE 0
+#define HK_REDUCTION_MEAN 1
+#define HK_REDUCTION_SUM 2
 
 /* dW reduction path for the norm backward passes */
 #define HK_DW_AUTO 0    /* atomic when rows <= 8 * CU count, else partial */
@@ -112,6 +121,69 @@ int hk_swiglu_fwd(void* c, const void* a, const void* b, int64_t n, int dtype, h
  * db = dc * silu(a); da = dc * b * sig(a) * (1 + a * (1 - sig(a))). */
 int hk_swiglu_bwd(void* da, void* db, const void* a, const void* b, const void* dc, int64_t n, int dtype,
                   hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* CrossEntropy                                                            */
+/* ----------------------------------------------------------------------- */
+/* Bytes of device workspace the CrossEntropy entry points need (n_valid). */
+size_t hk_cross_entropy_workspace_size(int64_t rows);
+
+/* Replaces cross_entropy_forward's training path (cross_entropy.py:206-236:
+ * _n_valid_tensor :196-199, _ce_train_forward_kernel_ignore :114-166 and
+ * _ce_train_forward_kernel_no_ignore :72-111, per_token_loss.sum() :236).
+ * loss_rows[r] = (lse_r - x[r,t_r]) * s, dlogits[r,:] = (softmax_r - onehot_r) * s with
+ * s = 1/max(n_valid,1) for mean, 1 otherwise; ignored rows: 0 and a zero row.
+ * ignore_index == -1 means "ignore nothing". n_valid stays on the device.
+ * loss_out (nullable) receives sum(loss_rows). */
+int hk_cross_entropy_fwd_grad(void* dlogits, float* loss_rows, float* loss_out, const void* logits,
+                              const int64_t* targets, int64_t rows, int64_t V, int64_t ld_logits, int64_t ld_dlogits,
+                              int64_t ignore_index, int reduction, int dtype, void* workspace, size_t workspace_bytes,
+                              hk_stream_t stream);
+
+/* Replaces the inference path of cross_entropy_forward (cross_entropy.py:238-249,
+ * _ce_forward_kernel :32-65): lse_rows, loss_rows = lse - x_t (0 if ignored);
+ * loss_out (nullable) = sum, or sum / max(n_valid, 1) for mean. */
+int hk_cross_entropy_fwd(float* lse_rows, float* loss_rows, float* loss_out, const void* logits,
+                         const int64_t* targets, int64_t rows, int64_t V, int64_t ld_logits, int64_t ignore_index,
+                         int reduction, int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream);
+
+/* Replaces _ce_scale_grad_kernel (cross_entropy.py:173-189) and
+ * _element_mul_kernel (fused_linear_cross_entropy.py:84-96):
+ * out = in * g (g scalar or per row, read on the device), or in * g / g_prev
+ * when g_prev is given (0 where g_prev is 0). With skip_if_one, out == in and
+ * a scalar g == 1 the kernel returns without touching memory, which replaces
+ * the host-synchronising torch.equal test at cross_entropy.py:202-203. */
+int hk_scale_rows(void* out, const void* in, const float* g, const float* g_prev, int per_row, int skip_if_one,
+                  int64_t rows, int64_t cols, int64_t ld_in, int64_t ld_out, int dtype, hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* GRPO                                                                    */
+/* ----------------------------------------------------------------------- */
+/* Replaces fused_selective_log_softmax (grpo_loss.py:65-80, kernel :29-62).
+ * logits: (B, L+1, V) contiguous; logp[b,l] = x[b,l,id]/T - logsumexp(x[b,l,:]/T)
+ * for l < L with id = ids[b*ids_sB + l*ids_sL]; 0 where mask == 0 (mask
+ * nullable, dtype HK_F32/F16/BF16/U8/I32/I64, element strides). */
+int hk_selective_log_softmax(float* logp, const void* logits, const int64_t* ids, int64_t ids_sB, int64_t ids_sL,
+                             const void* mask, int mask_dtype, int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L,
+                             int64_t V, float temperature, int dtype, hk_stream_t stream);
+
+/* Bytes of device workspace hk_grpo_loss_fwd needs. */
+size_t hk_grpo_workspace_size(int64_t B, int64_t L);
+
+/* Replaces grpo_loss_forward (grpo_loss.py:241-297) and, fused into the same
+ * pass at unit upstream gradient, grpo_loss_backward (grpo_loss.py:300-330).
+ * Scalars loss_out, kl_out (nullable) and clip_out receive the reduced loss,
+ * kl_mean and clip_ratio (grpo_loss.py:290-295); per-token lse/loss/kl/clipped rows
+ * [B, L]; dlogits (nullable: forward only) is (B, L+1, V) with zero rows at
+ * masked tokens and at position L. old_logp (nullable: on-policy) and
+ * ref_logp (required when beta != 0) are fp32 with element strides. */
+int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_out, float* lse_rows,
+                     float* loss_rows, float* kl_rows, float* clip_rows, const void* logits, const int64_t* ids,
+                     int64_t ids_sB, int64_t ids_sL, const float* advantages, const float* old_logp, int64_t old_sB,
+                     int64_t old_sL, const float* ref_logp, int64_t ref_sB, int64_t ref_sL, const void* mask,
+                     int mask_dtype, int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t V,
+                     float temperature, float beta, float eps_low, float eps_high, int dtype, void* workspace,
+                     size_t workspace_bytes, hk_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,7 @@
 // multiply-add per element; log-sum-exp is kept in the log2 domain and
 // converted once per row.
 #include "hk_common.h"
+#include "hk_internal.h"
 #include "../../include/hilda_kernel_amd.h"
 
 #include <math.h>
@@ -193,6 +194,7 @@ struct CeArgs {
   float* loss_rows;
   float* lse_rows;  // inference path only
   const int* n_valid;
+  const float* row_scale;  // optional per-row gradient factor
   int64_t rows, V, ld_in, ld_out, ignore_index;
   int has_ignore;
   int scale_by_n_valid;
@@ -205,8 +207,9 @@ __device__ __forceinline__ float ce_scale(const CeArgs& a) {
 // Training forward: loss_r = (lse - x_t) * s and dlogits = (softmax - onehot) * s
 // (kernels/cross_entropy.py:114-166). Ignored rows: loss 0 and a zero row.
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
-__global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
-                                                            CeArgs a) {
+__global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T* logits, CeArgs a) {
+  // dlogits may alias logits (in-place use): every element is read before the
+  // same thread overwrites it, so the pointers are not declared __restrict__.
   __shared__ float red[BLOCK / kWave];
   const float scale = ce_scale(a);
   for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
@@ -224,17 +227,18 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* __restrict__ dlog
       continue;
     }
     const float xt = to_f32<T>(in[t]);
+    const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
     if constexpr (RESIDENT) {
       const int n = row_len(a.V);
       RowRegs<T, VEC, NCH, BLOCK> r;
       r.load(in, n);
       const float lse2 = row_lse2(r, n, kLog2e, red);
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
-      r.store_grad(out, n, kLog2e, lse2, (int)t, scale);
+      r.store_grad(out, n, kLog2e, lse2, (int)t, gscale);
     } else {
       const float lse2 = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red);
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
-      store_grad_stream<T, VEC, BLOCK>(out, in, (int)a.V, kLog2e, lse2, (int)t, scale);
+      store_grad_stream<T, VEC, BLOCK>(out, in, (int)a.V, kLog2e, lse2, (int)t, gscale);
     }
   }
 }
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_kernel(const T* __restrict__ log
       if (a.has_ignore && t == a.ignore_index) loss = 0.f;
       else if (t < 0 || t >= a.V) loss = NAN;
       else loss = lse - to_f32<T>(in[t]);
-      a.lse_rows[row] = lse;
+      if (a.lse_rows) a.lse_rows[row] = lse;
       a.loss_rows[row] = loss;
     }
   }
@@ -607,6 +611,76 @@ int esize(int dt) { return dt == HK_F32 ? 4 : 2; }
 }  // namespace
 }  // namespace hk
 
+namespace hk {
+
+int count_valid_launch(int* n_valid, const int64_t* targets, int64_t rows, int64_t ignore_index, int has_ignore,
+                       hipStream_t st) {
+  hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, n_valid, targets, rows, ignore_index,
+                     has_ignore);
+  return check_launch("count_valid_kernel");
+}
+
+int sum_rows_launch(float* out, const float* v, int64_t n, const int* n_valid, int divide, hipStream_t st) {
+  hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, out, v, n, n_valid, divide);
+  return check_launch("sum_rows_kernel");
+}
+
+int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const int64_t* targets, int64_t rows,
+                   int64_t V, int64_t ld_in, int64_t ld_out, int64_t ignore_index, int has_ignore, const int* n_valid,
+                   int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st) {
+  if (rows == 0) return HK_OK;
+  const int es = esize(dtype);
+  CeArgs a{};
+  a.targets = targets;
+  a.loss_rows = loss_rows;
+  a.n_valid = n_valid;
+  a.row_scale = row_scale;
+  a.rows = rows;
+  a.V = V;
+  a.ld_in = ld_in;
+  a.ld_out = ld_out;
+  a.ignore_index = ignore_index;
+  a.has_ignore = has_ignore;
+  a.scale_by_n_valid = scale_by_n_valid;
+  if (!dlogits) {  // loss rows only
+    const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (ld_in * es) % 16 == 0;
+    return dispatch_t(dtype, [&](auto tt) {
+      using T = typename decltype(tt)::type;
+      const dim3 grid((unsigned)persistent_grid(rows, 1024));
+      if (vec_ok)
+        hipLaunchKernelGGL((ce_fwd_kernel<T, 16 / sizeof(T), 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
+      else
+        hipLaunchKernelGGL((ce_fwd_kernel<T, 1, 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
+      return check_launch("ce_fwd_kernel");
+    });
+  }
+  const int vec = 16 / es;
+  const bool vec_ok = V % vec == 0 && aligned_to(logits, 16) && aligned_to(dlogits, 16) && (ld_in * es) % 16 == 0 &&
+                      (ld_out * es) % 16 == 0;
+  const RowCfg cfg = choose_row_cfg(V, es, vec_ok);
+  return dispatch_t(dtype, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    return dispatch_cfg(cfg, [&](auto blk, auto nch) {
+      constexpr int BLOCK = decltype(blk)::value;
+      constexpr int NCH = decltype(nch)::value;
+      const dim3 grid((unsigned)persistent_grid(rows, BLOCK));
+      if (cfg.vec == 1) {
+        hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 1, 1, 1024, false>), grid, dim3(1024), 0, st, (T*)dlogits,
+                           (const T*)logits, a);
+      } else if constexpr (NCH == 0) {
+        hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>), grid, dim3(BLOCK), 0, st,
+                           (T*)dlogits, (const T*)logits, a);
+      } else {
+        hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>), grid, dim3(BLOCK), 0, st,
+                           (T*)dlogits, (const T*)logits, a);
+      }
+      return check_launch("ce_fwd_grad_kernel");
+    });
+  });
+}
+
+}  // namespace hk
+
 using namespace hk;
 
 extern "C" {
@@ -627,61 +701,19 @@ int hk_cross_entropy_fwd_grad(void* dlogits, float* loss_rows, float* loss_out, 
   HK_REQUIRE(reduction >= HK_REDUCTION_NONE && reduction <= HK_REDUCTION_SUM, "invalid reduction %d", reduction);
   HK_REQUIRE(workspace && workspace_bytes >= 256, "workspace must hold at least 256 bytes");
   HK_REQUIRE(rows == 0 || (dlogits && loss_rows && logits && targets), "null pointer argument");
-  const int es = esize(dtype);
   hipStream_t st = (hipStream_t)stream;
-  CeArgs a{};
-  a.targets = targets;
-  a.loss_rows = loss_rows;
-  a.n_valid = (const int*)workspace;
-  a.rows = rows;
-  a.V = V;
-  a.ld_in = ld_logits;
-  a.ld_out = ld_dlogits;
-  a.ignore_index = ignore_index;
+  int* n_valid = (int*)workspace;
   // ignore_index == -1 is the reference's "ignore nothing" sentinel (cross_entropy.py:197-198,219-225)
-  a.has_ignore = ignore_index != -1;
-  a.scale_by_n_valid = reduction == HK_REDUCTION_MEAN;
+  const int has_ignore = ignore_index != -1;
   if (rows > 0) {
-    hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, (int*)workspace, targets, rows, ignore_index,
-                       a.has_ignore);
-    int rc = check_launch("count_valid_kernel");
+    int rc = count_valid_launch(n_valid, targets, rows, ignore_index, has_ignore, st);
     if (rc) return rc;
-    const int vec = 16 / es;
-    const bool vec_ok = V % vec == 0 && aligned_to(logits, 16) && aligned_to(dlogits, 16) &&
-                        (ld_logits * es) % 16 == 0 && (ld_dlogits * es) % 16 == 0;
-    const RowCfg cfg = choose_row_cfg(V, es, vec_ok);
-    rc = dispatch_t(dtype, [&](auto tt) {
-      using T = typename decltype(tt)::type;
-      return dispatch_cfg(cfg, [&](auto blk, auto nch) {
-        constexpr int BLOCK = decltype(blk)::value;
-        constexpr int NCH = decltype(nch)::value;
-        const dim3 grid((unsigned)persistent_grid(rows, BLOCK));
-        if (cfg.vec == 1) {
-          hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 1, 1, 1024, false>), grid, dim3(1024), 0, st, (T*)dlogits,
-                             (const T*)logits, a);
-        } else if constexpr (NCH == 0) {
-          hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>), grid, dim3(BLOCK), 0, st,
-                             (T*)dlogits, (const T*)logits, a);
-        } else {
-          hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>), grid, dim3(BLOCK), 0, st,
-                             (T*)dlogits, (const T*)logits, a);
-        }
-        return check_launch("ce_fwd_grad_kernel");
-      });
-    });
+    rc = ce_rows_launch(dlogits, loss_rows, logits, targets, rows, V, ld_logits, ld_dlogits, ignore_index, has_ignore,
+                        n_valid, reduction == HK_REDUCTION_MEAN, nullptr, dtype, st);
     if (rc) return rc;
   }
-  if (loss_out) {
-    if (rows == 0) {
-      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, (int64_t)0,
-                         (const int*)nullptr, 0);
-    } else {
-      // the rows are already scaled by 1/max(n_valid, 1) for 'mean'
-      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, rows, (const int*)nullptr,
-                         0);
-    }
-    return check_launch("sum_rows_kernel");
-  }
+  // the rows are already scaled by 1/max(n_valid, 1) for 'mean'
+  if (loss_out) return sum_rows_launch(loss_out, loss_rows, rows, nullptr, 0, st);
   return HK_OK;
 }
 
@@ -695,23 +727,23 @@ int hk_cross_entropy_fwd(float* lse_rows, float* loss_rows, float* loss_out, con
   HK_REQUIRE(reduction >= HK_REDUCTION_NONE && reduction <= HK_REDUCTION_SUM, "invalid reduction %d", reduction);
   HK_REQUIRE(workspace && workspace_bytes >= 256, "workspace must hold at least 256 bytes");
   HK_REQUIRE(rows == 0 || (lse_rows && loss_rows && logits && targets), "null pointer argument");
-  const int es = esize(dtype);
   hipStream_t st = (hipStream_t)stream;
-  CeArgs a{};
-  a.targets = targets;
-  a.loss_rows = loss_rows;
-  a.lse_rows = lse_rows;
-  a.rows = rows;
-  a.V = V;
-  a.ld_in = ld_logits;
-  a.ignore_index = ignore_index;
-  a.has_ignore = ignore_index != -1;
+  int* n_valid = (int*)workspace;
+  const int has_ignore = ignore_index != -1;
   if (rows > 0) {
-    hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, (int*)workspace, targets, rows, ignore_index,
-                       a.has_ignore);
-    int rc = check_launch("count_valid_kernel");
+    int rc = count_valid_launch(n_valid, targets, rows, ignore_index, has_ignore, st);
     if (rc) return rc;
+    const int es = esize(dtype);
     const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (ld_logits * es) % 16 == 0;
+    CeArgs a{};
+    a.targets = targets;
+    a.loss_rows = loss_rows;
+    a.lse_rows = lse_rows;
+    a.rows = rows;
+    a.V = V;
+    a.ld_in = ld_logits;
+    a.ignore_index = ignore_index;
+    a.has_ignore = has_ignore;
     rc = dispatch_t(dtype, [&](auto tt) {
       using T = typename decltype(tt)::type;
       const dim3 grid((unsigned)persistent_grid(rows, 1024));
@@ -723,16 +755,9 @@ int hk_cross_entropy_fwd(float* lse_rows, float* loss_rows, float* loss_out, con
     });
     if (rc) return rc;
   }
-  if (loss_out) {
-    if (rows == 0) {
-      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, (int64_t)0,
-                         (const int*)nullptr, 0);
-    } else {
-      hipLaunchKernelGGL(sum_rows_kernel, dim3(1), dim3(1024), 0, st, loss_out, loss_rows, rows,
-                         (const int*)workspace, reduction == HK_REDUCTION_MEAN ? 1 : 0);
-    }
-    return check_launch("sum_rows_kernel");
-  }
+  if (loss_out)
+    return sum_rows_launch(loss_out, loss_rows, rows, rows > 0 ? n_valid : nullptr,
+                           rows > 0 && reduction == HK_REDUCTION_MEAN, st);
   return HK_OK;
 }
 

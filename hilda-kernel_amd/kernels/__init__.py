@@ -11,6 +11,8 @@ from .rope import HildaRopeFunction, hilda_rope, RotaryEmbedding
 from .swiglu import HildaSwiGLUFunction, hilda_swiglu, SwiGLU
 from .cross_entropy import HildaCrossEntropyFunction, hilda_cross_entropy, CrossEntropyLoss
 from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
+from .fused_linear_cross_entropy import (HildaFusedLinearCrossEntropyFunction, hilda_fused_linear_cross_entropy,
+                                         FusedLinearCrossEntropyLoss)
 from .grpo_loss import HildaGRPOLossFunction, hilda_grpo_loss, GRPOLoss, fused_selective_log_softmax
 
 __all__ = [
@@ -19,5 +21,6 @@ __all__ = [
     "HildaSwiGLUFunction", "hilda_swiglu", "SwiGLU",
     "HildaCrossEntropyFunction", "hilda_cross_entropy", "CrossEntropyLoss",
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
+    "HildaFusedLinearCrossEntropyFunction", "hilda_fused_linear_cross_entropy", "FusedLinearCrossEntropyLoss",
     "HildaGRPOLossFunction", "hilda_grpo_loss", "GRPOLoss", "fused_selective_log_softmax",
 ]

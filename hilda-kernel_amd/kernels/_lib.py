@@ -46,6 +46,9 @@ SIGNATURES = {
     "hk_selective_log_softmax": (_i32, [_p, _p, _p, _i64, _i64, _p, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
                                         _p]),
     "hk_grpo_workspace_size": (_sz, [_i64, _i64]),
+    "hk_fused_linear_cross_entropy_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
+    "hk_fused_linear_cross_entropy": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32,
+                                             _i64, _p, _sz, _p]),
     "hk_grpo_loss_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _p,
                                 _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _i32, _p, _sz, _p]),
 }

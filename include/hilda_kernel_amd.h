@@ -185,6 +185,28 @@ int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_
                      float temperature, float beta, float eps_low, float eps_high, int dtype, void* workspace,
                      size_t workspace_bytes, hk_stream_t stream);
 
+/* ----------------------------------------------------------------------- */
+/* FusedLinearCrossEntropy                                                 */
+/* ----------------------------------------------------------------------- */
+/* Bytes of device workspace hk_fused_linear_cross_entropy needs (0 for an
+ * unsupported dtype). chunk <= 0 selects the default (4096 rows). */
+size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype,
+                                                    int with_grad);
+
+/* Replaces fused_linear_cross_entropy_forward (fused_linear_cross_entropy.py:103-171)
+ * and its backward scaling (:192-210). hidden [BT,H], weight [V,H] (bf16 or
+ * fp16, contiguous); targets [BT] int64; rows equal to ignore_index are ignored.
+ * loss_rows[r] = CE of row r (scaled by 1/max(n_valid,1) when gradients are
+ * computed with reduction mean); loss_out (nullable) = sum, or mean over valid
+ * rows. With dhidden/dweight (both or neither): the gradients of the reduced
+ * loss at unit upstream gradient, each row's gradient further multiplied by
+ * row_scale[r] when row_scale is given (reduction 'none' backward). Logits are
+ * produced `chunk` rows at a time on bf16/fp16 MFMA; dW accumulates in fp32. */
+int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
+                                  const void* weight, const int64_t* targets, const float* row_scale, int64_t BT,
+                                  int64_t H, int64_t V, int64_t ignore_index, int reduction, int dtype, int64_t chunk,
+                                  void* workspace, size_t workspace_bytes, hk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

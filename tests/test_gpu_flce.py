@@ -1,0 +1,140 @@
+"""GPU parity: FusedLinearCrossEntropy (bf16/fp16 MFMA GEMMs + CE) vs the CPU oracle.
+
+Follows benchmarks/bench_fused_linear_ce.py (loss, dH, dW against
+``hidden @ W.T`` + F.cross_entropy) with the fp64 oracle, adding ignored rows,
+multi-chunk runs with ragged chunk sizes (K not a multiple of 8), every
+reduction (including 'none', whose backward the reference gets wrong), the
+upstream gradient, and the C5 shape: per-row losses and dhidden rows of a row
+sample against the oracle, plus size-independent properties (ignored rows of
+dhidden exactly zero; the vocabulary sum of dW vanishes because every
+gradient row of the logits sums to zero).
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+import workloads
+from _util import assert_close, rel_fro, tol, gpu
+
+from kernels import hilda_fused_linear_cross_entropy, FusedLinearCrossEntropyLoss
+from kernels import fused_linear_cross_entropy as fl
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(BT, H, V, dtype, seed, ignore_frac=0.1):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(BT, H, generator=g).to(dtype)
+    w = (0.02 * torch.randn(V, H, generator=g)).to(dtype)
+    t = torch.randint(0, V, (BT,), generator=g)
+    t[torch.rand(BT, generator=g) < ignore_frac] = -100
+    return h, w, t
+
+
+def _oracle(h, w, t, reduction="mean", grads=None):
+    # logits in the compute dtype as the reference's GEMM returns them, CE in fp64
+    def f(a, b):
+        logits = (a.double() @ b.double().T).to(h.dtype).double()
+        return oracle.cross_entropy_ref(logits, t, -100, reduction)
+    return oracle.fwd_bwd(f, [h, w], grads, dtype=torch.float64)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape,chunk", [((96, 256, 1000), 4096), ((300, 128, 4096), 4096), ((200, 64, 520), 64),
+                                         ((513, 256, 2048), 128), ((64, 4096, 32000), 4096)])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_flce(dtype, shape, chunk, reduction):
+    BT, H, V = shape
+    h, w, t = _case(BT, H, V, dtype, BT + H + V)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, reduction)
+    dev = gpu()
+    hg = h.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    if chunk != 4096:
+        loss, gi, gw, _ = fl.fused_linear_cross_entropy_forward(hg.detach(), wg.detach(), t.to(dev), -100, reduction,
+                                                                compute_grad=True, chunk=chunk)
+        hg.grad, wg.grad = gi, gw
+    else:
+        loss = hilda_fused_linear_cross_entropy(hg, wg, t.to(dev), -100, reduction)
+        loss.backward()
+    n_valid = int((t != -100).sum())
+    s = n_valid if reduction == "mean" else 1
+    assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
+    tt = tol(dtype)
+    assert_close(hg.grad, dh_ref, name="dhidden", **tt)
+    assert_close(wg.grad, dw_ref, name="dweight", **tt)
+    assert_close(hg.grad.float() * s, dh_ref * s, name="dhidden*n_valid", **tt)
+    assert_close(wg.grad.float() * s, dw_ref * s, name="dweight*n_valid", **tt)
+    assert rel_fro(hg.grad, dh_ref) < 1e-2 and rel_fro(wg.grad, dw_ref) < 1e-2
+    assert torch.count_nonzero(hg.grad[(t == -100).to(dev)]).item() == 0
+
+
+def test_flce_reduction_none_and_upstream_grad():
+    dtype = torch.bfloat16
+    h, w, t = _case(130, 128, 3000, dtype, 21)
+    dev = gpu()
+    up = torch.randn(130)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, "none", [up])
+    hg = h.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    loss = FusedLinearCrossEntropyLoss(reduction="none")(hg, wg, t.to(dev))
+    assert loss.shape == (130,)
+    loss.backward(up.to(dev))
+    assert_close(loss, l_ref, name="loss rows", rtol=2e-3, atol=2e-3)
+    assert rel_fro(hg.grad, dh_ref) < 1e-2 and rel_fro(wg.grad, dw_ref) < 1e-2
+    # a scalar upstream gradient other than 1
+    (l2,), (dh2, dw2) = _oracle(h, w, t, "mean")
+    hg2 = h.to(dev).requires_grad_(True)
+    wg2 = w.to(dev).requires_grad_(True)
+    (2.5 * hilda_fused_linear_cross_entropy(hg2, wg2, t.to(dev))).backward()
+    assert rel_fro(hg2.grad, 2.5 * dh2) < 1e-2 and rel_fro(wg2.grad, 2.5 * dw2) < 1e-2
+
+
+def test_flce_all_ignored_and_no_grad():
+    dev = gpu()
+    h, w, t = _case(40, 64, 256, torch.bfloat16, 5)
+    hg = h.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    loss = hilda_fused_linear_cross_entropy(hg, wg, torch.full((40,), -100, device=dev))
+    loss.backward()
+    assert loss.item() == 0.0
+    assert torch.count_nonzero(hg.grad).item() == 0 and torch.count_nonzero(wg.grad).item() == 0
+    with torch.no_grad():
+        l_ng = hilda_fused_linear_cross_entropy(h.to(dev), w.to(dev), t.to(dev))
+    (l_ref,), _ = _oracle(h, w, t)
+    assert_close(l_ng, l_ref, name="no-grad loss", rtol=2e-3, atol=2e-3)
+
+
+def test_flce_c5_config():
+    """C5: hidden [16384, 4096], weight [128256, 4096] bf16, 5% ignored, mean; on the GPU."""
+    dev = gpu()
+    c = workloads.c5_fused_linear_ce(device=dev)
+    h, w, t = c["hidden"], c["weight"], c["targets"]
+    loss_rows, _, _, _ = fl.fused_linear_cross_entropy_forward(h, w, t, -100, "none", compute_grad=False)
+    hg = h.requires_grad_(True)
+    wg = w.requires_grad_(True)
+    loss = hilda_fused_linear_cross_entropy(hg, wg, t)
+    loss.backward()
+    valid = t != -100
+    n_valid = int(valid.sum())
+    assert torch.count_nonzero(hg.grad[~valid]).item() == 0
+    # mean of the per-row losses equals the reduced loss
+    assert math.isclose(loss.item(), loss_rows.double().sum().item() / n_valid, rel_tol=1e-5)
+    # sum over the vocabulary of dW vanishes (each logits-gradient row sums to zero),
+    # relative to the column's L1 mass; what remains is bf16 rounding of D and dW
+    gw = wg.grad.float()
+    ratio = gw.sum(0).abs() / gw.abs().sum(0)
+    assert ratio.max().item() < 1e-2
+    # a sample of rows against the oracle: per-row loss and dhidden rows
+    idx = torch.arange(0, 16384, 257, device=dev)[:64]
+    hs, ts = h[idx].detach().cpu(), t[idx].cpu()
+    wc = w.detach().cpu()
+    logits = (hs.double() @ wc.double().T).to(torch.bfloat16).double().requires_grad_(True)
+    per_row = oracle.cross_entropy_ref(logits, ts, -100, "none")
+    per_row.sum().backward()
+    assert_close(loss_rows[idx], per_row.detach(), name="loss rows", rtol=2e-3, atol=2e-3)
+    dh_ref = logits.grad.to(torch.bfloat16).double() @ wc.double()  # d(sum of rows) / dh for the sample
+    assert_close(hg.grad[idx].float() * n_valid, dh_ref, name="dhidden rows * n_valid", **tol(torch.bfloat16))
+    assert rel_fro(hg.grad[idx].float() * n_valid, dh_ref) < 1e-2

@@ -8,7 +8,8 @@ RoPE q[4,2048,32,128] + k[4,2048,8,128] ([B,T,H,D] storage), SwiGLU
 [8192,14336] — as algorithmic HBM GB/s. One step = one fwd+bwd of the three
 ops (inputs resident in HBM, grads via torch.autograd.grad so nothing is
 accumulated). ``ops`` adds each configuration's op on its own (C1-C5), timed
-with HIP events and a 512 MiB cache flush between reps. ``roofline`` is the
+with HIP events and a 512 MiB cache flush between reps; C5 (FusedLinearCE)
+is reported in TFLOP/s of 6*n_valid*H*V. ``roofline`` is the
 dominant kernel of the step (SwiGLU backward), timed per launch with HIP
 events on its stream inside the timed region. ``cpu_baseline`` times the CPU
 PyTorch reference path (the oracle) on a quarter-size C2 sample.
@@ -179,6 +180,68 @@ def bench_c1(K, dev, reps, flush):
     return e
 
 
+def bench_c3(K, dev, reps, flush):
+    c = workloads.c3_cross_entropy(device=dev)
+    logits = c["logits"].requires_grad_(True)
+    t = c["targets"]
+    N, V = logits.shape
+    n_valid = int((t != -100).sum())
+
+    def fn():
+        loss = K.hilda_cross_entropy(logits, t)
+        return torch.autograd.grad([loss], [logits])
+
+    # read the contributing rows once, write every gradient row, targets + per-row loss
+    work = 2 * V * n_valid + 2 * V * N + 12 * N
+    e = op_entry("C3", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
+    e["n_valid"] = n_valid
+    log(f"  cross_entropy (C3): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
+def bench_c4(K, dev, reps, flush):
+    sls = K.fused_selective_log_softmax
+    c = workloads.c4_grpo(lambda lg, ids: sls(lg, torch.cat([torch.zeros_like(ids[:, :1]), ids], 1)), device=dev)
+    logits = c["logits"].requires_grad_(True)
+    args = [c[k] for k in ("completion_ids", "advantages", "old_logp", "ref_logp", "completion_mask")]
+    B, L1, V = logits.shape
+    L = L1 - 1
+    n_valid = int(c["completion_mask"].sum())
+
+    def fn():
+        loss, _, _ = K.hilda_grpo_loss(logits, *args, c["temperature"], c["beta"], c["eps_low"], c["eps_high"])
+        return torch.autograd.grad([loss], [logits])
+
+    work = 2 * V * n_valid + 2 * V * B * (L + 1) + 36 * B * L
+    e = op_entry("C4", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
+    e["n_valid"] = n_valid
+    log(f"  grpo_loss (C4): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
+def bench_c5(K, dev, reps, flush):
+    c = workloads.c5_fused_linear_ce(device=dev)
+    h = c["hidden"].requires_grad_(True)
+    w = c["weight"].requires_grad_(True)
+    t = c["targets"]
+    BT, H = h.shape
+    V = w.shape[0]
+    n_valid = int((t != -100).sum())
+
+    def fn():
+        loss = K.hilda_fused_linear_cross_entropy(h, w, t)
+        return torch.autograd.grad([loss], [h, w])
+
+    work = 6 * n_valid * H * V  # conservative: ignored rows need no FLOPs
+    e = op_entry("C5", time_events(fn, reps, flush, warmup=1), work, "TFLOP/s", BF16_PEAK_TFLOPS)
+    dense = 6 * BT * H * V
+    e["dense_equivalent_tflops"] = round(dense / (e["ms"] * 1e-3) / 1e12, 2)
+    e["n_valid"] = n_valid
+    log(f"  fused_linear_cross_entropy (C5): {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  ({e['frac']:.1%}); "
+        f"dense-equivalent {e['dense_equivalent_tflops']} TFLOP/s")
+    return e
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (the reference's PyTorch path) on the host cores
 # ---------------------------------------------------------------------------
@@ -248,6 +311,9 @@ def main(argv=None):
     ap.add_argument("--ops", choices=["all", "c2", "none"], default="all")
     ap.add_argument("--op-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="finish with three plain 1 GiB device-to-device copies (reference kernel of known "
+                         "traffic for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -317,10 +383,25 @@ def main(argv=None):
         ops.update(bench_c2_ops(c2, args.op_reps, flush))
         if args.ops == "all":
             ops["rms_norm"] = bench_c1(K, dev, args.op_reps, flush)
+            del c2
+            torch.cuda.empty_cache()
+            c2 = None
+            for name, fn in (("cross_entropy", bench_c3), ("grpo_loss", bench_c4),
+                             ("fused_linear_cross_entropy", bench_c5)):
+                ops[name] = fn(K, dev, max(3, args.op_reps // 2), flush)
+                torch.cuda.empty_cache()
         del flush
 
     del c2
     torch.cuda.empty_cache()
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         log("CPU baseline ...")

@@ -2,25 +2,19 @@
 // cross-entropy gradient produced chunk by chunk, so the full (BT, V) logits
 // never exist.
 //
-// Every contraction is one "NT" GEMM, C[M,N] = A[M,K] * B[N,K]^T with both
-// operands K-contiguous, the layout the MFMA operand fetch wants:
+// Every contraction is one "NT" GEMM (gemm_nt.h), C[M,N] = A[M,K] * B[N,K]^T
+// with both operands K-contiguous, the layout the MFMA operand fetch wants:
 //   logits_c = X_c  * W^T          A = X_c  [C,H],  B = W   [V,H]
 //   dX_c     = D_c  * (W^T)^T      A = D_c  [C,V],  B = W^T [H,V]
 //   dW      += D_c^T * X_c          A = D_c^T[V,C],  B = X^T [H,C] (columns of X^T)
 // W^T and X^T are transposed once per call, D_c^T once per chunk (tiled LDS
 // transposes, HBM-bound and small next to the GEMMs). dW accumulates in fp32
-// across chunks; the last chunk's epilogue writes the bf16 result.
-//
-// GEMM kernel: 256x256 output tile per workgroup of 4 waves (2x2), each wave a
-// 128x128 sub-tile of 4x4 v_mfma_f32_32x32x16 tiles (256 fp32 accumulators per
-// lane). K advances 64 per stage; A and B stage tiles (2 x 32 KiB) are
-// double-buffered in LDS with a 16-byte-chunk XOR swizzle so the MFMA operand
-// reads (32 rows x 16 bytes per half-wave) are bank-conflict free. The next
-// stage's global loads are issued before the current stage's MFMAs. Workgroups
-// are renumbered so each XCD walks a contiguous band of output tiles (its L2
-// keeps the shared A/B panels), grouped by M within the band.
+// across chunks (the GEMM epilogue reads and writes the accumulator in
+// coalesced 16-byte chunks); the last chunk's epilogue writes the result in
+// the input dtype.
 #include "hk_common.h"
 #include "hk_internal.h"
+#include "gemm_nt.h"
 #include "../../include/hilda_kernel_amd.h"
 
 #include <algorithm>
@@ -29,165 +23,70 @@
 namespace hk {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+using gemm::f32x4_t;
+struct NoPrior {};
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kThreads = 256;
-constexpr int kTM = 4, kTN = 4;     // 32x32 MFMA tiles per wave in M and N
-constexpr int kStageElems = kBM * kBK;  // one operand tile (A or B) per stage
-constexpr int kXcds = 8;
-constexpr int kGroupM = 16;
-
+// C (T) = acc, in 16-byte chunks of 8 columns.
 template <typename T>
-__device__ __forceinline__ f32x16_t mfma32(const u32x4& a, const u32x4& b, const f32x16_t& c) {
-  if constexpr (std::is_same<T, __bf16>::value)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                  0, 0, 0);
-}
-
-// element offset of (row, 8-element chunk kc) in a swizzled [rows][64] stage tile
-__device__ __forceinline__ int swz(int row, int kc) { return row * kBK + ((kc ^ (row & 7)) << 3); }
-
-struct GemmShape {
-  int M, N, K;
-  int64_t lda, ldb;
-};
-
-// Output tile (tm, tn) of this workgroup: XCD-banded, then grouped by kGroupM.
-__device__ __forceinline__ void tile_of_block(int nbm, int nbn, int* tm, int* tn) {
-  const int total = nbm * nbn;
-  const int pid = blockIdx.x;
-  const int q = total / kXcds, r = total % kXcds;
-  const int xcd = pid % kXcds, local = pid / kXcds;
-  const int logical = xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
-  const int per_group = kGroupM * nbn;
-  const int group = logical / per_group;
-  const int first_m = group * kGroupM;
-  const int gsize = min(nbm - first_m, kGroupM);
-  const int in_group = logical - group * per_group;
-  *tm = first_m + in_group % gsize;
-  *tn = in_group / gsize;
-}
-
-// Epilogues receive each lane's 32x32 accumulator tile: element e of tile (i, j)
-// sits at row i*32 + (e/4)*8 + (lane/32)*4 + e%4 and column j*32 + lane%32 of
-// the wave's 128x128 sub-tile (the CDNA 32x32 accumulator layout).
-template <typename T>
-struct EpiStore {  // C (T) = acc
+struct EpiStore {
+  using Stage = T;
+  using Prior = NoPrior;
+  static constexpr bool kReads = false;
   T* C;
-  int64_t ldc;
-  __device__ __forceinline__ void operator()(int row, int col, float v) const { C[row * ldc + col] = from_f32<T>(v); }
+  int64_t ldc;  // a multiple of 8, so full chunks are 16-byte aligned
+  __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
+  __device__ __forceinline__ void store(int row, int col, const T* v, int n, const Prior&) const {
+    T* p = C + (int64_t)row * ldc + col;
+    if (n == 8) {
+      *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(v);
+    } else {
+      for (int e = 0; e < n; ++e) p[e] = v[e];
+    }
+  }
 };
 
-// fp32 accumulator across calls; the last call writes T.
-// MODE 0: acc = v; 1: acc += v; 2: out = acc + v; 3: out = v
+// fp32 accumulator across calls, 4 columns per chunk; the last call writes T.
+// MODE 0: acc = v; 1: acc += v; 2: out = acc + v
 template <typename T, int MODE>
 struct EpiAccum {
+  using Stage = float;
+  using Prior = f32x4_t;
+  static constexpr bool kReads = MODE != 0;
   float* acc;
   T* out;
-  int64_t ld;
-  __device__ __forceinline__ void operator()(int row, int col, float v) const {
-    const int64_t o = row * ld + col;
-    if constexpr (MODE == 0) acc[o] = v;
-    else if constexpr (MODE == 1) acc[o] += v;
-    else if constexpr (MODE == 2) out[o] = from_f32<T>(acc[o] + v);
-    else out[o] = from_f32<T>(v);
+  int64_t ld;  // a multiple of 8
+  __device__ __forceinline__ Prior load(int row, int col, int n) const {
+    const float* p = acc + (int64_t)row * ld + col;
+    if (n == 4) return *reinterpret_cast<const f32x4_t*>(p);
+    Prior x = {0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < n; ++e) x[e] = p[e];
+    return x;
+  }
+  __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior& x) const {
+    const int64_t o = (int64_t)row * ld + col;
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = MODE == 0 ? v[e] : x[e] + v[e];
+    if constexpr (MODE == 2) {
+      if (n == 4) {
+        *reinterpret_cast<u32x2*>(out + o) = u32x2{gemm::pack2<T>(r[0], r[1]), gemm::pack2<T>(r[2], r[3])};
+      } else {
+        for (int e = 0; e < n; ++e) out[o + e] = from_f32<T>(r[e]);
+      }
+    } else {
+      if (n == 4) {
+        *reinterpret_cast<f32x4_t*>(acc + o) = f32x4_t{r[0], r[1], r[2], r[3]};
+      } else {
+        for (int e = 0; e < n; ++e) acc[o + e] = r[e];
+      }
+    }
   }
 };
 
-template <typename T, class Epi>
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const T* __restrict__ A, const T* __restrict__ B,
-                                                           GemmShape g, Epi epi) {
-  __shared__ __attribute__((aligned(16))) T lds[2][2][kStageElems];  // [stage][A|B]: 128 KiB
-
-  const int nbm = (g.M + kBM - 1) / kBM, nbn = (g.N + kBN - 1) / kBN;
-  int tm, tn;
-  tile_of_block(nbm, nbn, &tm, &tn);
-  const int m0 = tm * kBM, n0 = tn * kBN;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // global -> LDS mapping: 8 chunks of 16 bytes per thread and operand,
-  // chunk c = tid + i*256 covers row c/8 (= tid/8 + 32i), k-chunk c%8 (= tid%8)
-  const int lrow = tid >> 3, lkc = tid & 7;
-
-  f32x16_t acc[kTM][kTN];
-#pragma unroll
-  for (int i = 0; i < kTM; ++i)
-#pragma unroll
-    for (int j = 0; j < kTN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-  u32x4 ra[8], rb[8];
-  auto gload = [&](int k0) {
-    const int gk = k0 + lkc * 8;
-    const bool kok = gk < g.K;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = lrow + i * 32;
-      const int gm = m0 + r, gn = n0 + r;
-      ra[i] = (kok && gm < g.M) ? *reinterpret_cast<const u32x4*>(A + (int64_t)gm * g.lda + gk) : u32x4{0, 0, 0, 0};
-      rb[i] = (kok && gn < g.N) ? *reinterpret_cast<const u32x4*>(B + (int64_t)gn * g.ldb + gk) : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto lstore = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = lrow + i * 32;
-      *reinterpret_cast<u32x4*>(&lds[s][0][swz(r, lkc)]) = ra[i];
-      *reinterpret_cast<u32x4*>(&lds[s][1][swz(r, lkc)]) = rb[i];
-    }
-  };
-
-  const int KT = (g.K + kBK - 1) / kBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  const int fr = lane & 31, fk = lane >> 5;  // MFMA operand lane -> (row, 8-wide k half)
-  for (int kt = 0; kt < KT; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      u32x4 af[kTM], bfr[kTN];
-#pragma unroll
-      for (int i = 0; i < kTM; ++i) {
-        const int r = wm * 128 + i * 32 + fr;
-        af[i] = *reinterpret_cast<const u32x4*>(&lds[s][0][swz(r, ks * 2 + fk)]);
-      }
-#pragma unroll
-      for (int j = 0; j < kTN; ++j) {
-        const int r = wn * 128 + j * 32 + fr;
-        bfr[j] = *reinterpret_cast<const u32x4*>(&lds[s][1][swz(r, ks * 2 + fk)]);
-      }
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j) acc[i][j] = mfma32<T>(af[i], bfr[j], acc[i][j]);
-    }
-    if (kt + 1 < KT) lstore(s ^ 1);
-    __syncthreads();
-  }
-
-  // epilogue
-#pragma unroll
-  for (int i = 0; i < kTM; ++i)
-#pragma unroll
-    for (int j = 0; j < kTN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        const int col = n0 + wn * 128 + j * 32 + (lane & 31);
-        if (row < g.M && col < g.N) epi(row, col, acc[i][j][e]);
-      }
+// n16 16-byte words of zeros
+__global__ __launch_bounds__(256) void zero16_kernel(u32x4* __restrict__ p, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0, 0, 0, 0};
 }
 
 // out[c, r] = in[r, c] for a rows x cols matrix (row strides ld_in, ld_out);
@@ -218,11 +117,7 @@ template <typename T> struct Tag { using type = T; };
 
 template <typename T, class Epi>
 int launch_gemm(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st) {
-  if (M == 0 || N == 0) return HK_OK;
-  GemmShape g{M, N, K, lda, ldb};
-  const int64_t blocks = (int64_t)((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, Epi>), dim3((unsigned)blocks), dim3(kThreads), 0, st, A, B, g, epi);
-  return check_launch("gemm_nt_kernel");
+  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st);
 }
 
 template <typename T>
@@ -351,20 +246,22 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
       const int64_t csp = pad8(cs);
       rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, csp, st);
       if (rc) return rc;
-      const int mode = nchunks == 1 ? 3 : ci == 0 ? 0 : ci + 1 == nchunks ? 2 : 1;
       auto dw_gemm = [&](auto epi) {
         return launch_gemm<T>(Dt, Xt + r0, (int)V, (int)H, (int)csp, csp, BTp, epi, st);
       };
       T* dWo = (T*)dweight;
-      if (mode == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
-      else if (mode == 1) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
-      else if (mode == 2) rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
-      else rc = dw_gemm(EpiAccum<T, 3>{dwacc, dWo, H});
+      if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
+      else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
+      else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
+      else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
       if (rc) return rc;
     }
     if (grad && nchunks == 0) {
-      // no rows: zero gradients
-      rc = launch_gemm<T>(Dt, Xt, (int)V, (int)H, 0, 0, 0, EpiAccum<T, 3>{dwacc, (T*)dweight, H}, st);
+      // no rows: the weight gradient is zero (dhidden is empty)
+      const int64_t n16 = V * H * (int64_t)sizeof(T) / 16;
+      hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n16, 256), 4096)), dim3(256), 0, st,
+                         (u32x4*)dweight, n16);
+      rc = check_launch("zero16_kernel");
       if (rc) return rc;
     }
     if (loss_out) {

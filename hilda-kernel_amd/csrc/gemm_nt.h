@@ -1,15 +1,30 @@
 // bf16/fp16 "NT" GEMM on gfx950 MFMA: C[M,N] = A[M,K] * B[N,K]^T, both operands
-// K-contiguous, fp32 accumulation, result handed to an epilogue functor.
+// K-contiguous, fp32 accumulation, result handed to an epilogue functor in
+// 16-byte row chunks.
 //
-// One workgroup computes a BM x BN tile with WGM x WGN waves; each wave owns a
-// (BM/WGM) x (BN/WGN) sub-tile made of 32x32 v_mfma_f32_32x32x16 tiles. K
-// advances BK per stage through two LDS buffers (A and B stage tiles side by
-// side). Stage tiles are [rows][BK] with the 16-byte chunk index XOR-swizzled
-// by the row, so a half-wave reading 32 consecutive rows at one k-chunk hits
-// distinct bank groups. The next stage's global loads are issued into
-// registers before the current stage's MFMAs and written to the other LDS
-// buffer after them (one barrier per stage). With FRAG_PIPE the MFMA operands
-// of sub-step ks+1 are read from LDS while sub-step ks computes.
+// Layout of the work:
+// * One workgroup computes a BM x BN tile with WGM x WGN waves; each wave owns a
+//   (BM/WGM) x (BN/WGN) sub-tile of 32x32 v_mfma_f32_32x32x16 tiles, its
+//   accumulators held in AGPRs.
+// * K advances BK per stage through STAGES LDS buffers. Stage tiles are
+//   [rows][BK] with the 16-byte chunk index XOR-swizzled by the row, so the
+//   lanes a ds_read_b128 serves together hit distinct banks.
+// * Stage tiles are filled by buffer_load_dwordx4 ... lds (no VGPR round
+//   trip): each lane's 16 bytes land at LDS base + 16*lane, so the swizzle is
+//   applied to the global offset each lane fetches. The buffer resource covers
+//   only this block's rows of A (B), so rows past M (N) read as zero; columns
+//   past K (the last, partial stage) are redirected past the end of the buffer
+//   and read as zero too. Nothing is clamped and nothing is read out of bounds.
+// * The loads of stage kt+STAGES are issued as soon as every wave has finished
+//   reading stage kt. One barrier per stage, with no memory fence (a fence
+//   would drain the loads of the later stages too); vmcnt is counted by hand.
+// * MFMA operands are double-buffered in registers, and the LDS reads (and the
+//   global loads) are interleaved one-for-one with the MFMAs of the previous
+//   sub-step by scheduling-group barriers.
+// * Epilogue: the accumulators are staged through LDS (one wave row at a time)
+//   and read back as 16-byte row chunks, so global stores (and the
+//   read-modify-write of an fp32 accumulator) are full, coalesced 16-byte
+//   accesses; all loads of a batch of chunks are issued before its stores.
 //
 // Workgroups are renumbered so each of the 8 XCDs walks a contiguous band of
 // output tiles (grouped by GROUP_M rows of tiles), keeping the shared A/B
@@ -26,27 +41,37 @@ namespace gemm {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_, bool FRAG_PIPE_ = false, int GROUP_M_ = 16>
-struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_;
-  static constexpr bool FRAG_PIPE = FRAG_PIPE_;
-  static constexpr int GROUP_M = GROUP_M_;
-  static constexpr int NT = WGM * WGN * 64;       // threads per workgroup
-  static constexpr int WTM = BM / WGM, WTN = BN / WGN;  // wave tile
-  static constexpr int TM = WTM / 32, TN = WTN / 32;    // MFMA tiles per wave
-  static constexpr int CPR = BK / 8;              // 16-byte chunks per stage row
-  static constexpr int LA = BM * CPR / NT, LB = BN * CPR / NT;  // chunks per thread per stage
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-  static_assert(BK % 16 == 0 && (CPR == 2 || CPR == 4 || CPR == 8), "BK must be 16, 32 or 64");
-  static_assert(BM * CPR % NT == 0 && BN * CPR % NT == 0, "stage tile must split evenly over the threads");
-  static constexpr int STAGE = (BM + BN) * BK;    // elements per LDS stage
-};
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 struct Shape {
   int M, N, K;
   int64_t lda, ldb;
 };
+
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int GROUP_M_ = 16>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
+  static constexpr int GROUP_M = GROUP_M_;
+  static constexpr int NW = WGM * WGN, NT = NW * 64;
+  static constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  static constexpr int CPR = BK / 8, RPI = 64 / CPR;  // chunks per row, rows per load instruction
+  static constexpr int IA = BM / RPI / NW, IB = BN / RPI / NW;  // load instructions per wave per stage
+  static constexpr int NI = IA + IB;
+  static constexpr int NKS = BK / 16;              // MFMA sub-steps per stage
+  static constexpr int NR = TM + TN;               // LDS reads per sub-step
+  static constexpr int STAGE = (BM + BN) * BK;     // elements per stage
+  static_assert(IA * RPI * NW == BM && IB * RPI * NW == BN, "stage tile must split in 1 KiB loads");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
+  static_assert(CPR == 4 || CPR == 8, "BK must be 32 or 64");
+  static_assert(STAGES >= 2 && (STAGES - 1) * NI <= 63, "outstanding loads must fit vmcnt");
+  static_assert(TM * TN >= NR + 4, "sub-step must hold enough MFMAs to cover its reads");
+};
+
+// The configuration every caller uses: 256x256 tiles, 4 waves of 128x128,
+// BK=64 in two stages (128 KiB of LDS); measured fastest on the FusedLinearCE
+// shapes (M, N, K in {4096, 128256}).
+using DefaultCfg = Cfg<256, 256, 64, 2, 2, 2>;
 
 template <typename T>
 __device__ __forceinline__ f32x16_t mfma32(const u32x4& a, const u32x4& b, const f32x16_t& c) {
@@ -58,15 +83,26 @@ __device__ __forceinline__ f32x16_t mfma32(const u32x4& a, const u32x4& b, const
                                                   0, 0, 0);
 }
 
-// element offset of (row, 16-byte chunk kc) in a swizzled [rows][BK] stage tile
+// two values rounded to the 16-bit type T, packed low-first into one word
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(lo)) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(hi)) << 16);
+}
+
+// XOR applied to the 16-byte chunk index of a stage row, chosen (by measuring
+// ds_read_b128 rates over candidate patterns on gfx950) so that the rows read
+// together at one logical chunk fall in distinct banks.
+template <int BK>
+__device__ __forceinline__ int swz_xor(int row) {
+  constexpr int CPR = BK / 8;
+  if constexpr (CPR == 8) return (row ^ (row >> 3)) & 7;
+  else return (row ^ (row >> 2)) & 3;
+}
+
 template <int BK>
 __device__ __forceinline__ int swz(int row, int kc) {
-  constexpr int CPR = BK / 8;
-  int s;
-  if constexpr (CPR == 8) s = row & 7;
-  else if constexpr (CPR == 4) s = (row >> 1) & 3;
-  else s = (row >> 2) & 1;
-  return row * BK + ((kc ^ s) << 3);
+  return row * BK + ((kc ^ swz_xor<BK>(row)) << 3);
 }
 
 template <int GROUP_M>
@@ -86,22 +122,54 @@ __device__ __forceinline__ void tile_of_block(int nbm, int nbn, int* tm, int* tn
   *tn = in_group / gsize;
 }
 
-// Epilogue contract: epi(row, col, value) for every in-range element. Element
-// e of 32x32 tile (i, j) of a wave sits at row i*32 + (e/4)*8 + (lane/32)*4 + e%4
-// and column j*32 + lane%32 of the wave tile (the CDNA 32x32 accumulator layout).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// word 3 of a raw buffer descriptor on gfx9-family parts (32-bit data format, no swizzle)
+constexpr int kRsrcWord3 = 0x00020000;
+// A buffer offset past the end of any buffer this kernel builds (the launcher
+// keeps them below it) that cannot wrap when the scalar offset is added.
+constexpr uint32_t kOobOffset = 0x7ff00000u;
+
+// ---------------------------------------------------------------------------
+// Epilogue contract. An epilogue functor declares
+//   using Stage = float or the input type;   // how values are staged in LDS
+//   using Prior = what load() returns;       // (an empty struct if kReads is false)
+//   static constexpr bool kReads;            // does it read memory per chunk?
+//   Prior load(row, col, n) const;           // (kReads) prior data of the chunk
+//   void store(row, col, const Stage* v, n, const Prior&) const;
+// and is called once per 16-byte chunk of a row: v holds 16/sizeof(Stage)
+// consecutive columns starting at col, of which the first n are inside the
+// matrix (n is the full chunk unless the chunk straddles column N).
+// ---------------------------------------------------------------------------
+
 template <typename T, class C, class Epi>
 __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A, const T* __restrict__ B, Shape g,
                                                         Epi epi) {
-  __shared__ __attribute__((aligned(16))) T lds[2][C::STAGE];
+  using S = typename Epi::Stage;
+  constexpr int EPC = 16 / sizeof(S);           // elements per 16-byte chunk
+  constexpr int LDR = C::BN + EPC;              // padded LDS row of the staged tile
+  constexpr int kStageBytes = C::STAGES * C::STAGE * (int)sizeof(T);
+  constexpr int kEpiBytes = C::WTM * LDR * (int)sizeof(S);
+  constexpr int kLdsBytes = kStageBytes > kEpiBytes ? kStageBytes : kEpiBytes;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[kLdsBytes];
+  T* const lds = reinterpret_cast<T*>(lds_raw);
 
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
   int tm, tn;
   tile_of_block<C::GROUP_M>(nbm, nbn, &tm, &tn);
   const int m0 = tm * C::BM, n0 = tn * C::BN;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the LDS base of a load lives in M0
   const int wm = wave / C::WGN, wn = wave % C::WGN;
 
+  // acc[i][j] holds the transposed 32x32 tile (the MFMA is fed B then A), so
+  // element e of a lane is row i*32 + lane%32, column j*32 + (e/4)*8 + (lane/32)*4 + e%4:
+  // four consecutive columns per group of four elements.
   f32x16_t acc[C::TM][C::TN];
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
@@ -110,100 +178,201 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // global -> LDS: chunk c = tid + i*NT covers row c / CPR, k-chunk c % CPR
-  u32x4 ra[C::LA], rb[C::LB];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < C::LA; ++i) {
-      const int c = tid + i * C::NT, r = c / C::CPR, kc = c % C::CPR;
-      const int gm = m0 + r, gk = k0 + kc * 8;
-      ra[i] = (gm < g.M && gk < g.K) ? *reinterpret_cast<const u32x4*>(A + (int64_t)gm * g.lda + gk)
-                                     : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < C::LB; ++i) {
-      const int c = tid + i * C::NT, r = c / C::CPR, kc = c % C::CPR;
-      const int gn = n0 + r, gk = k0 + kc * 8;
-      rb[i] = (gn < g.N && gk < g.K) ? *reinterpret_cast<const u32x4*>(B + (int64_t)gn * g.ldb + gk)
-                                     : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto lstore = [&](int s) {
-#pragma unroll
-    for (int i = 0; i < C::LA; ++i) {
-      const int c = tid + i * C::NT, r = c / C::CPR, kc = c % C::CPR;
-      *reinterpret_cast<u32x4*>(&lds[s][swz<C::BK>(r, kc)]) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < C::LB; ++i) {
-      const int c = tid + i * C::NT, r = c / C::CPR, kc = c % C::CPR;
-      *reinterpret_cast<u32x4*>(&lds[s][C::BM * C::BK + swz<C::BK>(r, kc)]) = rb[i];
-    }
-  };
+  const int KT = (g.K + C::BK - 1) / C::BK;  // >= 1 (checked by the launcher)
+  const int fr = lane & 31, fk = lane >> 5;
 
-  const int fr = lane & 31, fk = lane >> 5;  // operand lane -> (row in tile, 8-wide k half)
-  auto frag = [&](int s, int ks, u32x4 (&af)[C::TM], u32x4 (&bf)[C::TN]) {
+  // The buffer builtins exist only for the device target; the host pass still
+  // instantiates this body to emit the launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int rows_a = min(C::BM, g.M - m0), rows_b = min(C::BN, g.N - n0);
+  T* const pa = const_cast<T*>(A + (int64_t)m0 * g.lda);
+  T* const pb = const_cast<T*>(B + (int64_t)n0 * g.ldb);
+  const int nrec_a = (int)(rows_a * g.lda * (int64_t)sizeof(T));
+  const int nrec_b = (int)(rows_b * g.ldb * (int64_t)sizeof(T));
+  // Load instruction i of this wave covers stage chunks p = (wave*I + i)*64 + lane:
+  // row p / CPR, stored chunk p % CPR, which holds logical k-chunk (p % CPR) ^ swz_xor(row).
+  uint32_t voffA[C::IA], voffB[C::IB];
+  int kcA[C::IA], kcB[C::IB];  // first column of the chunk within the stage
+  const int lr = lane / C::CPR, lc = lane % C::CPR;
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      const int r = wm * C::WTM + i * 32 + fr;
-      af[i] = *reinterpret_cast<const u32x4*>(&lds[s][swz<C::BK>(r, ks * 2 + fk)]);
-    }
+  for (int i = 0; i < C::IA; ++i) {
+    const int r = (wave * C::IA + i) * C::RPI + lr;
+    kcA[i] = (lc ^ swz_xor<C::BK>(r)) << 3;
+    voffA[i] = (uint32_t)(r * g.lda + kcA[i]) * sizeof(T);
+  }
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int r = wn * C::WTN + j * 32 + fr;
-      bf[j] = *reinterpret_cast<const u32x4*>(&lds[s][C::BM * C::BK + swz<C::BK>(r, ks * 2 + fk)]);
-    }
+  for (int i = 0; i < C::IB; ++i) {
+    const int r = (wave * C::IB + i) * C::RPI + lr;
+    kcB[i] = (lc ^ swz_xor<C::BK>(r)) << 3;
+    voffB[i] = (uint32_t)(r * g.ldb + kcB[i]) * sizeof(T);
+  }
+  // Stage kst into LDS buffer `stage`. Every call issues the same NI loads, so
+  // the vmcnt arithmetic never depends on the position in the loop: a stage
+  // past the end goes through a zero-length buffer, whose loads return zeros
+  // without touching memory (and land in a buffer nobody reads again). Chunks
+  // at or past column K read zeros through an offset past the buffer's end.
+  auto issue = [&](int stage, int kst) {
+    const bool live = kst < KT;
+    const int k0 = live ? kst * C::BK : 0;
+    const int lim = g.K - k0;  // columns of this stage inside the matrix
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(pa, 0, live ? nrec_a : 0, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(pb, 0, live ? nrec_b : 0, kRsrcWord3);
+    T* la = lds + stage * C::STAGE;
+    T* lb = la + C::BM * C::BK;
+#pragma unroll
+    for (int i = 0; i < C::IA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, la + (wave * C::IA + i) * 512, 16,
+                                               kcA[i] < lim ? voffA[i] : kOobOffset, k0 * sizeof(T), 0, 0);
+#pragma unroll
+    for (int i = 0; i < C::IB; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, lb + (wave * C::IB + i) * 512, 16,
+                                               kcB[i] < lim ? voffB[i] : kOobOffset, k0 * sizeof(T), 0, 0);
   };
-  auto mma = [&](const u32x4 (&af)[C::TM], const u32x4 (&bf)[C::TN]) {
+#else
+  auto issue = [&](int, int) {};
+#endif
+
+  u32x4 fa[2][C::TM], fb[2][C::TN];
+  auto frag = [&](int stage, int ks, u32x4* a, u32x4* b) {
+    const T* la = lds + stage * C::STAGE;
+    const T* lb = la + C::BM * C::BK;
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma32<T>(af[i], bf[j], acc[i][j]);
-  };
-
-  const int KT = (g.K + C::BK - 1) / C::BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * C::BK);
-    if constexpr (C::FRAG_PIPE) {
-      u32x4 af[2][C::TM], bf[2][C::TN];
-      frag(s, 0, af[0], bf[0]);
-#pragma unroll
-      for (int ks = 0; ks < C::BK / 16; ++ks) {
-        if (ks + 1 < C::BK / 16) frag(s, ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
-        mma(af[ks & 1], bf[ks & 1]);
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < C::BK / 16; ++ks) {
-        u32x4 af[C::TM], bf[C::TN];
-        frag(s, ks, af, bf);
-        mma(af, bf);
-      }
-    }
-    if (kt + 1 < KT) lstore(s ^ 1);
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+      a[i] = *reinterpret_cast<const u32x4*>(la + swz<C::BK>(wm * C::WTM + i * 32 + fr, ks * 2 + fk));
 #pragma unroll
     for (int j = 0; j < C::TN; ++j)
+      b[j] = *reinterpret_cast<const u32x4*>(lb + swz<C::BK>(wn * C::WTN + j * 32 + fr, ks * 2 + fk));
+  };
+  auto mma = [&](int buf, int first, int count) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * C::WTM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        const int col = n0 + wn * C::WTN + j * 32 + (lane & 31);
-        if (row < g.M && col < g.N) epi(row, col, acc[i][j][e]);
+    for (int t = first; t < first + count; ++t) {
+      const int i = t / C::TN, j = t % C::TN;
+      acc[i][j] = mfma32<T>(fb[buf][j], fa[buf][i], acc[i][j]);
+    }
+  };
+  auto barrier = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // sub-steps 0 .. NKS-2 of the stage in buffer cur
+  auto inner = [&](int cur) {
+#pragma unroll
+    for (int ks = 0; ks < C::NKS - 1; ++ks) {
+      frag(cur, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      mma(ks & 1, 0, C::TM * C::TN);
+#pragma unroll
+      for (int t = 0; t < C::NR; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
       }
+      __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - C::NR, 0);
+    }
+  };
+  constexpr int LB = (C::NKS - 1) & 1;  // register buffer of a stage's last sub-step
+  constexpr int Q = 4;                  // MFMAs issued before the per-stage barrier
+
+  // prologue: every buffer gets a stage
+#pragma unroll
+  for (int s = 0; s < C::STAGES; ++s) issue(s, s);
+  wait_vmcnt<(C::STAGES - 1) * C::NI>();
+  barrier();
+  frag(0, 0, fa[0], fb[0]);
+
+  // Straight-line body: no branch may split the MFMA chain, or the compiler
+  // permutes the accumulators across the back-edge.
+  for (int kt = 0; kt < KT - 1; ++kt) {
+    const int cur = kt % C::STAGES;
+    inner(cur);
+    mma(LB, 0, Q);
+    wait_vmcnt<(C::STAGES - 2) * C::NI>();  // stage kt+1 has landed
+    barrier();                              // every wave is done reading stage kt
+    frag((kt + 1) % C::STAGES, 0, fa[0], fb[0]);
+    issue(cur, kt + C::STAGES);
+    mma(LB, Q, C::TM * C::TN - Q);
+#pragma unroll
+    for (int t = 0; t < C::NR; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+    }
+#pragma unroll
+    for (int t = 0; t < C::NI; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
+      if (t < C::TM * C::TN - Q - C::NR) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    }
+    if constexpr (C::TM * C::TN - Q - C::NR > C::NI)
+      __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - Q - C::NR - C::NI, 1);
+  }
+  inner((KT - 1) % C::STAGES);
+  mma(LB, 0, C::TM * C::TN);
+  wait_vmcnt<0>();  // the dummy loads of the tail target LDS: drain them before LDS is reused
+  barrier();
+
+  // ---- epilogue: one wave row (WTM rows x BN columns) at a time through LDS ----
+  S* const st = reinterpret_cast<S*>(lds_raw);
+  constexpr int CPRO = C::BN / EPC;                  // chunks per staged row
+  constexpr int PER_T = C::WTM * CPRO / C::NT;       // chunks per thread per pass
+  constexpr int BATCH = PER_T < 8 ? PER_T : 8;
+  static_assert(C::WTM * CPRO % C::NT == 0 && PER_T % BATCH == 0, "epilogue split");
+#pragma unroll 1
+  for (int p = 0; p < C::WGM; ++p) {
+    if (wm == p) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            S* dst = st + (i * 32 + fr) * LDR + wn * C::WTN + j * 32 + q * 8 + fk * 4;
+            if constexpr (sizeof(S) == 4) {
+              *reinterpret_cast<f32x4_t*>(dst) =
+                  f32x4_t{acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]};
+            } else {
+              u32x2 w;
+              w.x = pack2<S>(acc[i][j][q * 4], acc[i][j][q * 4 + 1]);
+              w.y = pack2<S>(acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+              *reinterpret_cast<u32x2*>(dst) = w;
+            }
+          }
+    }
+    barrier();
+    const int rbase = m0 + p * C::WTM;
+#pragma unroll
+    for (int b0 = 0; b0 < PER_T; b0 += BATCH) {
+      typename Epi::Prior prior[BATCH];
+      if constexpr (Epi::kReads) {
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+          const int c = (b0 + u) * C::NT + tid, r = c / CPRO, col = n0 + (c % CPRO) * EPC;
+          if (rbase + r < g.M && col < g.N) prior[u] = epi.load(rbase + r, col, min(EPC, g.N - col));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int c = (b0 + u) * C::NT + tid, r = c / CPRO, cc = c % CPRO, col = n0 + cc * EPC;
+        if (rbase + r < g.M && col < g.N) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * LDR + cc * EPC);
+          epi.store(rbase + r, col, reinterpret_cast<const S*>(&v), min(EPC, g.N - col), prior[u]);
+        }
+      }
+    }
+    if (p + 1 < C::WGM) barrier();
+  }
 }
 
-template <typename T, class C, class Epi>
+// Returns 0, or -1 with the error set for shapes the kernel does not take.
+template <typename T, class C = DefaultCfg, class Epi>
 int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st) {
   if (M == 0 || N == 0) return 0;
+  if (K <= 0 || K % 8 != 0 || lda % 8 != 0 || ldb % 8 != 0 || lda < K || ldb < K) {
+    set_error("gemm_nt: K (%d) must be a positive multiple of 8, lda/ldb multiples of 8 and >= K", K);
+    return -1;
+  }
+  if ((int64_t)C::BM * lda * (int64_t)sizeof(T) >= (int64_t)kOobOffset ||
+      (int64_t)C::BN * ldb * (int64_t)sizeof(T) >= (int64_t)kOobOffset) {
+    set_error("gemm_nt: a %d-row panel of A or B exceeds the 2 GiB buffer range", C::BM);
+    return -1;
+  }
   Shape g{M, N, K, lda, ldb};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
   hipLaunchKernelGGL((gemm_nt_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);

@@ -4,8 +4,7 @@
 //
 // Layout of the work:
 // * One workgroup computes a BM x BN tile with WGM x WGN waves; each wave owns a
-//   (BM/WGM) x (BN/WGN) sub-tile of 32x32 v_mfma_f32_32x32x16 tiles, its
-//   accumulators held in AGPRs.
+//   (BM/WGM) x (BN/WGN) sub-tile of 32x32 v_mfma_f32_32x32x16 tiles.
 // * K advances BK per stage through STAGES LDS buffers. Stage tiles are
 //   [rows][BK] with the 16-byte chunk index XOR-swizzled by the row, so the
 //   lanes a ds_read_b128 serves together hit distinct banks.
@@ -65,13 +64,17 @@ struct Cfg {
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(CPR == 4 || CPR == 8, "BK must be 32 or 64");
   static_assert(STAGES >= 2 && (STAGES - 1) * NI <= 63, "outstanding loads must fit vmcnt");
-  static_assert(TM * TN >= NR + 4, "sub-step must hold enough MFMAs to cover its reads");
+  static_assert(TM * TN >= NR, "sub-step must hold enough MFMAs to cover its reads");
+  static constexpr int Q = NW >= 8 ? 2 : 4;        // MFMAs of a stage's last sub-step issued before its barrier
+  static_assert(TM * TN > Q, "last sub-step split");
 };
 
-// The configuration every caller uses: 256x256 tiles, 4 waves of 128x128,
-// BK=64 in two stages (128 KiB of LDS); measured fastest on the FusedLinearCE
-// shapes (M, N, K in {4096, 128256}).
-using DefaultCfg = Cfg<256, 256, 64, 2, 2, 2>;
+// The configuration every caller uses: 256x256 tiles, 8 waves of 128x64 (two
+// per SIMD, so one wave's barrier and LDS waits overlap the other's MFMAs),
+// BK=64 in two stages (128 KiB of LDS). Measured fastest on the FusedLinearCE
+// shapes (M, N, K in {4096, 128256}) against 4 waves of 128x128 and against
+// BK=32 with 4 or 5 stages.
+using DefaultCfg = Cfg<256, 256, 64, 2, 4, 2>;
 
 template <typename T>
 __device__ __forceinline__ f32x16_t mfma32(const u32x4& a, const u32x4& b, const f32x16_t& c) {
@@ -270,7 +273,8 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
     }
   };
   constexpr int LB = (C::NKS - 1) & 1;  // register buffer of a stage's last sub-step
-  constexpr int Q = 4;                  // MFMAs issued before the per-stage barrier
+  constexpr int Q = C::Q;               // MFMAs issued before the per-stage barrier
+  constexpr int R = C::TM * C::TN - Q;  // MFMAs after it
 
   // prologue: every buffer gets a stage
 #pragma unroll
@@ -289,19 +293,15 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
     barrier();                              // every wave is done reading stage kt
     frag((kt + 1) % C::STAGES, 0, fa[0], fb[0]);
     issue(cur, kt + C::STAGES);
-    mma(LB, Q, C::TM * C::TN - Q);
+    mma(LB, Q, R);
+    // after the barrier: the next stage's first operand reads, then its loads,
+    // each slotted behind one of the R remaining MFMAs while they last
 #pragma unroll
-    for (int t = 0; t < C::NR; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // LDS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+    for (int t = 0; t < C::NR + C::NI || t < R; ++t) {
+      if (t < C::NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);             // LDS read
+      else if (t < C::NR + C::NI) __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
+      if (t < R) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                   // MFMA
     }
-#pragma unroll
-    for (int t = 0; t < C::NI; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
-      if (t < C::TM * C::TN - Q - C::NR) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    }
-    if constexpr (C::TM * C::TN - Q - C::NR > C::NI)
-      __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - Q - C::NR - C::NI, 1);
   }
   inner((KT - 1) % C::STAGES);
   mma(LB, 0, C::TM * C::TN);

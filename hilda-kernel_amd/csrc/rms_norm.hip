@@ -7,19 +7,22 @@
 // LDS exchange between the row group's waves when wpr > 1. Vector j of lane l
 // covers elements [(j*64*wpr + l)*VEC, +VEC), so every load instruction of a
 // wave touches one contiguous 64*VEC*sizeof(T)-byte span (1 KiB for 16-byte
-// vectors).
+// vectors). The weight is loaded together with the row, so a row costs one
+// memory latency, not two.
 //
 // Backward saves only rstd (the forward's [rows] fp32 output) and recomputes
-// the normalised row. dW is reduced either by atomics into one [cols]
-// accumulator or by per-row-group partial rows plus a reduction pass; the
-// choice follows the reference rule "atomic when rows <= 8 * CU count"
-// (rms_norm.py:325-326). dW is accumulated in fp64 (registers, partial rows
-// and atomics alike): a sum over thousands of rows in fp32 drifts by ~1e-4,
-// more than the 1e-5 fp32 tolerance allows, and the fp64 VALU rate is far
-// above what this HBM-bound kernel needs.
+// the normalised row. Each row group walks a run of R consecutive rows (about
+// two groups per CU), accumulating its dW contribution in registers: fp32 for
+// 16-bit inputs, fp64 for fp32 inputs (a sum over thousands of rows in fp32
+// drifts by ~1e-4, more than the 1e-5 fp32 tolerance allows). The groups'
+// accumulators then go either into fp64 atomics on one [cols] accumulator or
+// into one partial row per group, summed by a two-level reduction; the choice
+// follows the reference rule "atomic when rows <= 8 * CU count"
+// (rms_norm.py:325-326).
 #include "hk_common.h"
 #include "../../include/hilda_kernel_amd.h"
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -31,8 +34,8 @@ constexpr int kMaxWaves = 16;  // 1024-thread blocks at most
 // ------------------------------------------------------------------------
 // forward
 // ------------------------------------------------------------------------
-template <typename T, typename W, int VEC, int NCH, bool ADD>
-__global__ __launch_bounds__(1024) void rmsnorm_fwd_kernel(
+template <typename T, typename W, int VEC, int NCH, bool ADD, int LB>
+__global__ __launch_bounds__(LB) void rmsnorm_fwd_kernel(
     T* __restrict__ y, T* __restrict__ s_out, float* __restrict__ rstd_out, const T* __restrict__ x,
     const T* __restrict__ r, const W* __restrict__ w, int64_t rows, int cols, int64_t ld_x, int64_t ld_r,
     int64_t ld_y, int64_t ld_s, int wpr, float eps) {
@@ -46,10 +49,11 @@ __global__ __launch_bounds__(1024) void rmsnorm_fwd_kernel(
   const bool valid = row < rows;
 
   Pack<T, VEC> xv[NCH];
-  float ss = 0.f;
+  Pack<W, VEC> wv[NCH];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int col = (j * gl + lr) * VEC;
+    if (col < cols) wv[j] = load_pack<W, VEC>(w + col);
     if (valid && col < cols) {
       xv[j] = load_pack<T, VEC>(x + row * ld_x + col);
       if constexpr (ADD) {
@@ -63,6 +67,13 @@ __global__ __launch_bounds__(1024) void rmsnorm_fwd_kernel(
         xv[j] = pack<T, VEC>(a);
         store_pack<T, VEC>(s_out + row * ld_s + col, xv[j]);
       }
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int col = (j * gl + lr) * VEC;
+    if (valid && col < cols) {
       float a[VEC];
       unpack(xv[j], a);
 #pragma unroll
@@ -86,7 +97,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_fwd_kernel(
       float a[VEC];
       unpack(xv[j], a);
       float wf[VEC];
-      unpack(load_pack<W, VEC>(w + col), wf);
+      unpack(wv[j], wf);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) a[i] = round_through<T>(a[i] * rstd) * wf[i];
       store_pack<T, VEC>(y + row * ld_y + col, pack<T, VEC>(a));
@@ -95,100 +106,111 @@ __global__ __launch_bounds__(1024) void rmsnorm_fwd_kernel(
 }
 
 // ------------------------------------------------------------------------
-// backward: dx per row, dW accumulated per row group in registers
+// backward: dx per row; dW accumulated per row group over R consecutive rows
 // ------------------------------------------------------------------------
-template <typename T, typename W, int VEC, int NCH, bool HAS_DS, bool ATOMIC>
-__global__ __launch_bounds__(1024) void rmsnorm_bwd_kernel(
-    T* __restrict__ dx, double* __restrict__ dw_ws, const T* __restrict__ dy, const T* __restrict__ ds,
-    const T* __restrict__ x, const W* __restrict__ w, const float* __restrict__ rstd, int64_t rows, int cols,
-    int64_t ld_dy, int64_t ld_ds, int64_t ld_x, int64_t ld_dx, int wpr) {
-  __shared__ float red[kMaxWaves];
+template <typename T, typename W, typename A, int VEC, int NCH, bool HAS_DS, int LB>
+__global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
+    T* __restrict__ dx, void* __restrict__ dw_ws, int atomic,
+    const T* __restrict__ dy, const T* __restrict__ ds, const T* __restrict__ x, const W* __restrict__ w,
+    const float* __restrict__ rstd, int64_t rows, int cols, int64_t ld_dy, int64_t ld_ds, int64_t ld_x,
+    int64_t ld_dx, int wpr, int64_t rows_per_group) {
+  __shared__ float red[2][kMaxWaves];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int rpb = blockDim.x / (kWave * wpr);
   const int rib = wave / wpr;
   const int lr = (wave % wpr) * kWave + lane;
   const int gl = wpr * kWave;
-  const int64_t groups = (int64_t)gridDim.x * rpb;
-  const float n = (float)cols;
-
-  float wf[NCH][VEC];
-  double acc[NCH][VEC];
+  const int64_t group = (int64_t)blockIdx.x * rpb + rib;
+  const int64_t row0 = group * rows_per_group;
+  const float inv_n = 1.f / (float)cols;
+  Pack<W, VEC> wv[NCH];
+  A acc[NCH][VEC];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int col = (j * gl + lr) * VEC;
-    float wv[VEC];
-    if (col < cols) unpack(load_pack<W, VEC>(w + col), wv);
+    if (col < cols) wv[j] = load_pack<W, VEC>(w + col);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      wf[j][i] = col < cols ? wv[i] : 0.f;
-      acc[j][i] = 0.0;
-    }
+    for (int i = 0; i < VEC; ++i) acc[j][i] = A(0);
   }
 
   // The trip count is uniform over the block so every thread meets the barriers.
-  for (int64_t base = (int64_t)blockIdx.x * rpb; base < rows; base += groups) {
-    const int64_t row = base + rib;
+#pragma unroll 1
+  for (int64_t t = 0; t < rows_per_group; ++t) {
+    const int64_t row = row0 + t;
     const bool valid = row < rows;
-    Pack<T, VEC> dyv[NCH], xv[NCH];
-    float dot = 0.f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int col = (j * gl + lr) * VEC;
-      if (valid && col < cols) {
-        dyv[j] = load_pack<T, VEC>(dy + row * ld_dy + col);
-        xv[j] = load_pack<T, VEC>(x + row * ld_x + col);
-        float g[VEC], a[VEC];
-        unpack(dyv[j], g);
-        unpack(xv[j], a);
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) dot = fmaf(g[i] * wf[j][i], a[i], dot);
-      }
-    }
-    dot = wave_sum(dot);
-    if (wpr > 1) {
-      if (lane == 0) red[wave] = dot;
-      __syncthreads();
-      dot = 0.f;
-      for (int i = 0; i < wpr; ++i) dot += red[rib * wpr + i];
-      __syncthreads();
-    }
-    if (!valid) continue;
-    const float rs = rstd[row];
-    const float c = rs * rs * rs * (dot / n);
+    const int64_t rr = valid ? row : rows - 1;  // loads stay unconditional
+    const float rs = rstd[rr];
+    Pack<T, VEC> gv[NCH], xv[NCH], dv[NCH];
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int col = (j * gl + lr) * VEC;
       if (col < cols) {
-        float g[VEC], a[VEC], o[VEC];
-        unpack(dyv[j], g);
+        gv[j] = load_pack<T, VEC>(dy + rr * ld_dy + col);
+        xv[j] = load_pack<T, VEC>(x + rr * ld_x + col);
+        if constexpr (HAS_DS) dv[j] = load_pack<T, VEC>(ds + rr * ld_ds + col);
+      }
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int col = (j * gl + lr) * VEC;
+      if (col < cols) {
+        float g[VEC], a[VEC], wf[VEC];
+        unpack(gv[j], g);
         unpack(xv[j], a);
-        if constexpr (HAS_DS) {
-          Pack<T, VEC> dsv = load_pack<T, VEC>(ds + row * ld_ds + col);
-          unpack(dsv, o);
-        }
+        unpack(wv[j], wf);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) dot = fmaf(g[i] * wf[i], a[i], dot);
+      }
+    }
+    dot = wave_sum(dot);
+    if (wpr > 1) {
+      const int b = (int)(t & 1);  // two slots: no second barrier before the next row's write
+      if (lane == 0) red[b][wave] = dot;
+      __syncthreads();
+      dot = 0.f;
+      for (int i = 0; i < wpr; ++i) dot += red[b][rib * wpr + i];
+    }
+    // unpack again below rather than keep the floats live across the barrier
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      make_opaque(gv[j]);
+      make_opaque(xv[j]);
+      make_opaque(wv[j]);
+    }
+    const float c = rs * rs * rs * (dot * inv_n);
+    const float vf = valid ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int col = (j * gl + lr) * VEC;
+      if (col < cols) {
+        float g[VEC], a[VEC], wf[VEC], o[VEC];
+        unpack(gv[j], g);
+        unpack(xv[j], a);
+        unpack(wv[j], wf);
+        if constexpr (HAS_DS) unpack(dv[j], o);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          float v = rs * (g[i] * wf[j][i]) - c * a[i];
+          float v = rs * (g[i] * wf[i]) - c * a[i];
           if constexpr (HAS_DS) v += o[i];
           o[i] = v;
-          acc[j][i] += (double)g[i] * (double)(a[i] * rs);
+          acc[j][i] += A(g[i] * vf) * A(a[i] * rs);
         }
-        store_pack<T, VEC>(dx + row * ld_dx + col, pack<T, VEC>(o));
+        if (valid) store_pack<T, VEC>(dx + row * ld_dx + col, pack<T, VEC>(o));
       }
     }
   }
 
-  const int64_t g = (int64_t)blockIdx.x * rpb + rib;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int col = (j * gl + lr) * VEC;
     if (col < cols) {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
-        if constexpr (ATOMIC) {
-          if (g < rows) unsafeAtomicAdd(dw_ws + col + i, acc[j][i]);
+        if (atomic) {
+          if (row0 < rows) unsafeAtomicAdd(static_cast<double*>(dw_ws) + col + i, (double)acc[j][i]);
         } else {
-          dw_ws[g * cols + col + i] = acc[j][i];
+          static_cast<A*>(dw_ws)[group * cols + col + i] = acc[j][i];
         }
       }
     }
@@ -206,20 +228,31 @@ __global__ __launch_bounds__(256) void cast_f64_kernel(W* __restrict__ out, cons
     out[i] = from_f32<W>((float)in[i]);
 }
 
-// out[c] = sum_g part[g*cols + c]; block = 64 columns x 16 group slices
-template <typename W>
-__global__ __launch_bounds__(1024) void reduce_partial_kernel(W* __restrict__ out, const double* __restrict__ part,
+// out[c] = sum_g part[g*cols + c]: a block of 64 columns x 16 group slices,
+// four independent partial sums per thread so its loads overlap. (A two-level
+// variant with an arrival ticket needs a device-scope fence per block, which
+// writes back the XCD's L2 and was an order of magnitude slower.)
+template <typename A, typename W>
+__global__ __launch_bounds__(1024) void reduce_partial_kernel(W* __restrict__ out, const A* __restrict__ part,
                                                               int64_t groups, int cols) {
-  __shared__ double red[16][65];
+  __shared__ A red[16][65];
   const int c = threadIdx.x % 64, s = threadIdx.x / 64;
   const int col = blockIdx.x * 64 + c;
-  double t = 0.0;
-  if (col < cols)
-    for (int64_t g = s; g < groups; g += 16) t += part[g * cols + col];
-  red[s][c] = t;
+  A t0 = A(0), t1 = A(0), t2 = A(0), t3 = A(0);
+  if (col < cols) {
+    int64_t g = s;
+    for (; g + 48 < groups; g += 64) {
+      t0 += part[g * cols + col];
+      t1 += part[(g + 16) * cols + col];
+      t2 += part[(g + 32) * cols + col];
+      t3 += part[(g + 48) * cols + col];
+    }
+    for (; g < groups; g += 16) t0 += part[g * cols + col];
+  }
+  red[s][c] = (t0 + t1) + (t2 + t3);
   __syncthreads();
   if (s == 0 && col < cols) {
-    double u = 0.0;
+    A u = A(0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) u += red[i][c];
     out[col] = from_f32<W>((float)u);
@@ -269,14 +302,16 @@ struct Geom {
 
 // Pick the row-group geometry: full 16-byte vectors when every row start and
 // the weight are 16-byte aligned, and the fewest waves per row that keep at
-// most `max_elems` elements of one tensor per lane.
-bool choose_geom(int64_t cols, int esize, bool vec_ok, int max_elems, Geom* g) {
+// most 16 elements of one tensor per lane (4 waves of 2 vectors for a
+// 4096-wide bf16 row: measured fastest for both passes).
+bool choose_geom(int64_t cols, int esize, bool vec_ok, Geom* g) {
+  constexpr int kMaxElems = 16;
   g->vec = vec_ok ? 16 / esize : 1;
-  const int64_t nv = cols / g->vec;
+  const int64_t nv = cdiv(cols, (int64_t)g->vec);
   for (int wpr = 1; wpr <= kMaxWaves; wpr *= 2) {
     int64_t nch = cdiv(nv, (int64_t)kWave * wpr);
     int n = nch <= 1 ? 1 : nch <= 2 ? 2 : nch <= 4 ? 4 : nch <= 8 ? 8 : 16;
-    if (n <= 8 && (n * g->vec <= max_elems || wpr == kMaxWaves)) {
+    if (n <= 8 && (n * g->vec <= kMaxElems || wpr == kMaxWaves)) {
       g->nch = n;
       g->wpr = wpr;
       g->block = wpr >= 4 ? wpr * kWave : 256;
@@ -289,6 +324,13 @@ bool choose_geom(int64_t cols, int esize, bool vec_ok, int max_elems, Geom* g) {
 
 bool rows_aligned(const void* p, int64_t ld, int esize) {
   return aligned_to(p, 16) && ((ld * esize) % 16 == 0);
+}
+
+// f(integral_constant<LB>) with LB the launch bound matching the block size
+template <typename F>
+int dispatch_lb(int block, F&& f) {
+  if (block <= 256) return f(std::integral_constant<int, 256>{});
+  return f(std::integral_constant<int, 1024>{});
 }
 
 int fwd_impl(void* y, void* s, float* rstd, const void* x, const void* r, const void* w, int64_t rows,
@@ -307,8 +349,7 @@ int fwd_impl(void* y, void* s, float* rstd, const void* x, const void* r, const 
                 aligned_to(w, (size_t)ws * vec);
   if (add) vec_ok = vec_ok && rows_aligned(r, ld_r, es) && rows_aligned(s, ld_s, es);
   Geom g;
-  HK_REQUIRE(choose_geom(cols, es, vec_ok, 32, &g), "cols=%lld exceeds the supported row length",
-             (long long)cols);
+  HK_REQUIRE(choose_geom(cols, es, vec_ok, &g), "cols=%lld exceeds the supported row length", (long long)cols);
   const int64_t grid = cdiv(rows, g.rpb);
   hipStream_t st = (hipStream_t)stream;
   int rc = dispatch_xw(dt_x, dt_w, [&](auto tx, auto tw) {
@@ -316,42 +357,54 @@ int fwd_impl(void* y, void* s, float* rstd, const void* x, const void* r, const 
     using W = typename decltype(tw)::type;
     return dispatch_nch(g.nch, [&](auto nch_c) {
       constexpr int NCH = decltype(nch_c)::value;
-      auto launch = [&](auto vec_c) {
-        constexpr int VEC = decltype(vec_c)::value;
-        if (add)
-          hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, W, VEC, NCH, true>), dim3(grid), dim3(g.block), 0, st,
-                             (T*)y, (T*)s, rstd, (const T*)x, (const T*)r, (const W*)w, rows, (int)cols, ld_x,
-                             ld_r, ld_y, ld_s, g.wpr, eps);
-        else
-          hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, W, VEC, NCH, false>), dim3(grid), dim3(g.block), 0, st,
-                             (T*)y, (T*)nullptr, rstd, (const T*)x, (const T*)nullptr, (const W*)w, rows,
-                             (int)cols, ld_x, ld_x, ld_y, ld_y, g.wpr, eps);
-        return check_launch("rmsnorm_fwd_kernel");
-      };
-      if (g.vec == 1) return launch(std::integral_constant<int, 1>{});
-      return launch(std::integral_constant<int, 16 / sizeof(T)>{});
+      return dispatch_lb(g.block, [&](auto lb_c) {
+        constexpr int LB = decltype(lb_c)::value;
+        auto launch = [&](auto vec_c) {
+          constexpr int VEC = decltype(vec_c)::value;
+          if (add)
+            hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, W, VEC, NCH, true, LB>), dim3(grid), dim3(g.block), 0, st,
+                               (T*)y, (T*)s, rstd, (const T*)x, (const T*)r, (const W*)w, rows, (int)cols, ld_x,
+                               ld_r, ld_y, ld_s, g.wpr, eps);
+          else
+            hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, W, VEC, NCH, false, LB>), dim3(grid), dim3(g.block), 0, st,
+                               (T*)y, (T*)nullptr, rstd, (const T*)x, (const T*)nullptr, (const W*)w, rows,
+                               (int)cols, ld_x, ld_x, ld_y, ld_y, g.wpr, eps);
+          return check_launch("rmsnorm_fwd_kernel");
+        };
+        if (g.vec == 1) return launch(std::integral_constant<int, 1>{});
+        return launch(std::integral_constant<int, 16 / sizeof(T)>{});
+      });
     });
   });
   return rc;
 }
 
-// Geometry and grid of the backward launch, shared by the workspace query.
+// Geometry, grid and workspace layout of the backward launch, shared by the
+// workspace query.
 struct BwdPlan {
   Geom g;
-  int64_t grid;
+  int64_t groups;     // row groups (one accumulator row each)
+  int64_t rpg;        // rows per group
+  int64_t grid;       // blocks
   bool atomic;
-  int64_t ws_elems;  // fp64 accumulators
+  int acc_bytes;      // 4 (fp32 accumulators) or 8 (fp64)
+  size_t total;
 };
 
 bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int cu, BwdPlan* p) {
-  if (!choose_geom(cols, es, vec_ok, 16, &p->g)) return false;
-  const int64_t needed = cdiv(rows, p->g.rpb);
-  // enough resident waves per CU to cover HBM latency, but few partial rows
-  const int64_t target = (int64_t)(cu > 0 ? cu : 256) * (p->g.block >= 1024 ? 2 : p->g.block >= 512 ? 4 : 8) / 2;
-  p->grid = needed < target ? needed : target;
-  if (p->grid < 1) p->grid = 1;
-  p->atomic = dw_mode == HK_DW_ATOMIC || (dw_mode == HK_DW_AUTO && rows <= 8LL * (cu > 0 ? cu : 256));
-  p->ws_elems = p->atomic ? cols : p->grid * p->g.rpb * cols;
+  if (!choose_geom(cols, es, vec_ok, &p->g)) return false;
+  const int64_t ncu = cu > 0 ? cu : 256;
+  p->atomic = dw_mode == HK_DW_ATOMIC || (dw_mode == HK_DW_AUTO && rows <= 8 * ncu);
+  p->acc_bytes = es == 4 ? 8 : 4;
+  // about two row groups per CU: long runs of rows keep the accumulator rows
+  // (partials or atomics) few; more groups were not faster
+  const int64_t target = (p->atomic ? 1 : 2) * ncu * p->g.rpb;
+  p->groups = std::max<int64_t>(1, std::min<int64_t>(rows, target));
+  p->rpg = rows > 0 ? cdiv(rows, p->groups) : 0;
+  p->groups = rows > 0 ? cdiv(rows, p->rpg) : 1;
+  p->grid = cdiv(p->groups, (int64_t)p->g.rpb);
+  p->groups = p->grid * p->g.rpb;  // every launched group owns an accumulator row
+  p->total = p->atomic ? (size_t)cols * 8 : (size_t)p->groups * cols * p->acc_bytes;
   return true;
 }
 
@@ -376,49 +429,52 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
   BwdPlan p;
   HK_REQUIRE(plan_bwd(rows, cols, es, vec_ok, dw_mode, cu_count(dev), &p),
              "cols=%lld exceeds the supported row length", (long long)cols);
-  HK_REQUIRE(workspace != nullptr && ws_bytes >= (size_t)p.ws_elems * sizeof(double),
-             "workspace too small: need %zu bytes, got %zu", (size_t)p.ws_elems * sizeof(double), ws_bytes);
+  HK_REQUIRE(workspace != nullptr && ws_bytes >= p.total, "workspace too small: need %zu bytes, got %zu", p.total,
+             ws_bytes);
   HK_REQUIRE(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
-  double* wsf = (double*)workspace;
+  void* part = workspace;
 
   return dispatch_xw(dt_x, dt_w, [&](auto tx, auto tw) {
     using T = typename decltype(tx)::type;
     using W = typename decltype(tw)::type;
+    using A = typename std::conditional<std::is_same<T, float>::value, double, float>::type;
     if (p.atomic) {
-      hipLaunchKernelGGL(fill_zero_f64, dim3((unsigned)cdiv(cols, 256)), dim3(256), 0, st, wsf, cols);
+      hipLaunchKernelGGL(fill_zero_f64, dim3((unsigned)cdiv(cols, 256)), dim3(256), 0, st, (double*)part, cols);
       int rc = check_launch("fill_zero_f64");
       if (rc) return rc;
     }
     if (rows > 0) {
       int rc = dispatch_nch(p.g.nch, [&](auto nch_c) {
         constexpr int NCH = decltype(nch_c)::value;
-        auto launch = [&](auto vec_c) {
-          constexpr int VEC = decltype(vec_c)::value;
-#define HK_BWD_LAUNCH(HDS, AT)                                                                               \
-  hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, W, VEC, NCH, HDS, AT>), dim3(p.grid), dim3(p.g.block), 0, st,     \
-                     (T*)dx, wsf, (const T*)dy, (const T*)ds, (const T*)x, (const W*)w, rstd, rows, (int)cols, \
-                     ld_dy, ld_ds, ld_x, ld_dx, p.g.wpr)
-          if (ds) {
-            if (p.atomic) HK_BWD_LAUNCH(true, true); else HK_BWD_LAUNCH(true, false);
-          } else {
-            if (p.atomic) HK_BWD_LAUNCH(false, true); else HK_BWD_LAUNCH(false, false);
-          }
-#undef HK_BWD_LAUNCH
-          return check_launch("rmsnorm_bwd_kernel");
-        };
-        if (p.g.vec == 1) return launch(std::integral_constant<int, 1>{});
-        return launch(std::integral_constant<int, 16 / sizeof(T)>{});
+        return dispatch_lb(p.g.block, [&](auto lb_c) {
+          constexpr int LB = decltype(lb_c)::value;
+          auto launch = [&](auto vec_c) {
+            constexpr int VEC = decltype(vec_c)::value;
+            auto go = [&](auto hds_c) {
+              constexpr bool HDS = decltype(hds_c)::value;
+              hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, W, A, VEC, NCH, HDS, LB>), dim3((unsigned)p.grid),
+                                 dim3(p.g.block), 0, st, (T*)dx, part, (int)p.atomic, (const T*)dy, (const T*)ds, (const T*)x, (const W*)w, rstd, rows,
+                                 (int)cols, ld_dy, ld_ds, ld_x, ld_dx, p.g.wpr, p.rpg);
+              return check_launch("rmsnorm_bwd_kernel");
+            };
+            if (ds) return go(std::true_type{});
+            return go(std::false_type{});
+          };
+          if (p.g.vec == 1) return launch(std::integral_constant<int, 1>{});
+          return launch(std::integral_constant<int, 16 / sizeof(T)>{});
+        });
       });
       if (rc) return rc;
     }
     if (p.atomic) {
-      hipLaunchKernelGGL((cast_f64_kernel<W>), dim3((unsigned)cdiv(cols, 256)), dim3(256), 0, st, (W*)dw, wsf,
-                         cols);
+      hipLaunchKernelGGL((cast_f64_kernel<W>), dim3((unsigned)cdiv(cols, 256)), dim3(256), 0, st, (W*)dw,
+                         (const double*)part, cols);
       return check_launch("cast_f64_kernel");
     }
-    hipLaunchKernelGGL((reduce_partial_kernel<W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw, wsf,
-                       p.grid * p.g.rpb, (int)cols);
+    // (no rows: zero groups are summed and dW comes out zero)
+    hipLaunchKernelGGL((reduce_partial_kernel<A, W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
+                       (const A*)part, rows > 0 ? p.groups : 0, (int)cols);
     return check_launch("reduce_partial_kernel");
   });
 }
@@ -447,15 +503,11 @@ size_t hk_rms_norm_bwd_workspace_size(int64_t rows, int64_t cols, int dtype_x, i
   (void)dtype_w;
   if (rows < 0 || cols <= 0 || !valid_dtype(dtype_x)) return 0;
   BwdPlan p;
-  // The vector width can only shrink the geometry's group count, so plan
-  // with full vectors and the widest alternative and take the larger.
+  // The vector width only changes the geometry, so plan with full vectors
+  // and with scalars and take the larger.
   size_t best = 0;
-  for (int v = 0; v < 2; ++v) {
-    if (plan_bwd(rows, cols, dtype_size(dtype_x), v == 0, dw_mode, cu_count(device), &p)) {
-      size_t b = (size_t)p.ws_elems * sizeof(double);
-      if (b > best) best = b;
-    }
-  }
+  for (int v = 0; v < 2; ++v)
+    if (plan_bwd(rows, cols, dtype_size(dtype_x), v == 0, dw_mode, cu_count(device), &p)) best = std::max(best, p.total);
   return best;
 }
 

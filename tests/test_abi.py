@@ -68,11 +68,14 @@ def test_argument_validation_without_gpu():
 @needs_lib
 def test_workspace_query_is_pure():
     lib = _lib.load()
-    # partial path: one fp64 row per row group; atomic path: one [cols] fp64 row
+    # atomic path: one [cols] fp64 row; partial path (bf16 -> fp32 accumulators): one row per row group
     part = lib.hk_rms_norm_bwd_workspace_size(8192, 4096, 2, 2, _lib.DW_PARTIAL, 0)
     atom = lib.hk_rms_norm_bwd_workspace_size(8192, 4096, 2, 2, _lib.DW_ATOMIC, 0)
     assert atom == 4096 * 8
-    assert part >= 4096 * 8 and part % (4096 * 8) == 0
+    assert part >= 4096 * 4 and part % (4096 * 4) == 0
+    # fp32 inputs accumulate in fp64
+    part32 = lib.hk_rms_norm_bwd_workspace_size(8192, 4096, 0, 0, _lib.DW_PARTIAL, 0)
+    assert part32 > part
     assert lib.hk_rms_norm_bwd_workspace_size(-1, 4096, 2, 2, 0, 0) == 0
 
 

@@ -126,13 +126,19 @@ class C2Step:
 # per-op timing with HIP events and a cache flush between reps
 # ---------------------------------------------------------------------------
 class Flusher:
-    """Writes a 512 MiB buffer so MI355X's 256 MB MALL and the L2s hold none of the op's data."""
+    """Reads a 512 MiB buffer so MI355X's 256 MB MALL and the L2s hold none of the op's data.
+
+    A read, not a write: a written flush buffer leaves up to 256 MB of dirty lines in the
+    caches, and writing them back would be charged to the timed op (it halves the apparent
+    bandwidth of a 64 MB copy). Earlier dirty lines are written back during the flush itself.
+    """
 
     def __init__(self, dev):
-        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        # fp32, so the sum reads the buffer directly (an integer sum widens it through a copy first)
+        self.buf = torch.ones(128 << 20, dtype=torch.float32, device=dev)
 
     def __call__(self):
-        self.buf.zero_()
+        self.sink = torch.sum(self.buf)
 
 
 def time_events(fn, reps, flush=None, warmup=2):

@@ -27,6 +27,46 @@ namespace {
 // ---------------------------------------------------------------------------
 // register-resident row helpers
 // ---------------------------------------------------------------------------
+// max(a, b, c) in one instruction (fmaxf would add a canonicalising max per operand)
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Storage of exp values in a row's registers: fp32 stays fp32; for 16-bit rows
+// the values (all in [0, 1]) are kept as fp16, whose 11-bit significand is
+// finer than the bf16 the gradient is finally rounded to.
+template <typename T, int VEC>
+__device__ __forceinline__ Pack<T, VEC> pack_e(const float (&x)[VEC]) {
+  if constexpr (sizeof(T) == 4) {
+    return pack<T, VEC>(x);
+  } else {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    Pack<T, VEC> r;
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k)
+      r.w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x[2 * k], x[2 * k + 1]}), h2));
+    return r;
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void unpack_e(const Pack<T, VEC>& p, float (&x)[VEC]) {
+  if constexpr (sizeof(T) == 4) {
+    unpack(p, x);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) {
+      const h2 h = __builtin_bit_cast(h2, p.w[k]);
+      x[2 * k] = (float)h.x;
+      x[2 * k + 1] = (float)h.y;
+    }
+  }
+}
+
 template <typename T, int VEC, int NCH, int BLOCK>
 struct RowRegs {
   Pack<T, VEC> v[NCH];
@@ -98,6 +138,102 @@ struct RowRegs {
     return s;
   }
 
+  // This lane's (max, sum) of x*c in the log2 domain, m = max and
+  // s = sum 2^(x*c - m); the registers are overwritten with e = 2^(x*c - m)
+  // (see pack_e), so the gradient needs one multiply per element, not a
+  // second exponential. Padding (-inf) becomes 0.
+  __device__ __forceinline__ void lse2_to_exp(int n, float c, float* m_out, float* s_out) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j * kSpan < n) {
+        float x[VEC];
+        unpack(v[j], x);
+#pragma unroll
+        for (int e = 0; e + 1 < VEC; e += 2) m = max3(m, x[e], x[e + 1]);
+        if constexpr (VEC & 1) m = fmaxf(m, x[VEC - 1]);
+      }
+    }
+    m *= c;
+    opaque();  // unpack again below rather than keep all the floats of the max pass live
+    const float mo = m == -INFINITY ? 0.f : m;  // an all-padding lane: every e is 2^-inf = 0
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j * kSpan < n) {
+        float x[VEC];
+        unpack(v[j], x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          x[e] = exp2_fast(fmaf(x[e], c, -mo));
+          s += x[e];
+        }
+        v[j] = pack_e<T, VEC>(x);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one vector's floats live at a time
+    }
+    *m_out = m;
+    *s_out = s;
+  }
+
+  // Gradient from the exp registers, (e * f) with f = 2^(m_lane - lse2) * g,
+  // without the one-hot term (the caller patches the target element), then
+  // the row at `next` loaded into the same registers vector by vector, so the
+  // row's stores and the next row's loads are in flight together.
+  __device__ __forceinline__ void store_exp_grad_then_load(T* out, int n, float f, const T* next) {
+    const int tc = lane_col();
+    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int lim = n - j * kSpan;  // uniform
+      if (lim > 0) {
+        float x[VEC];
+        unpack_e<T, VEC>(v[j], x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[e] *= f;
+        if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
+        if (lim >= kSpan) {
+          v[j] = load_pack<T, VEC>(next + off(j, tc));
+        } else {
+          const Pack<T, VEC> y = load_pack<T, VEC>(next + off(j, tc < lim ? tc : 0));
+          v[j] = tc < lim ? y : ninf;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Gradient of this row, then the row at `next` loaded into the same
+  // registers vector by vector: each vector is refilled right after its
+  // gradient is stored, so the row's stores and the next row's loads are in
+  // flight together.
+  __device__ __forceinline__ void store_grad_then_load(T* out, int n, float c, float lse2, int target, float g,
+                                                       const T* next) {
+    const int tc = lane_col();
+    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int lim = n - j * kSpan;  // uniform
+      if (lim > 0) {
+        float x[VEC];
+        unpack(v[j], x);
+        const int rel = (target - j * kSpan) - tc;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float p = exp2_fast(fmaf(x[e], c, -lse2));
+          x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
+        }
+        if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
+        if (lim >= kSpan) {
+          v[j] = load_pack<T, VEC>(next + off(j, tc));
+        } else {
+          const Pack<T, VEC> y = load_pack<T, VEC>(next + off(j, tc < lim ? tc : 0));
+          v[j] = tc < lim ? y : ninf;
+        }
+      }
+    }
+  }
+
   // out[j] = (2^(x*c - lse2) - [j == target]) * g   (target < 0: no one-hot)
   __device__ __forceinline__ void store_grad(T* __restrict__ out, int n, float c, float lse2, int target,
                                              float g) const {
@@ -135,6 +271,38 @@ __device__ __forceinline__ void fill_row(T* __restrict__ out, int n, float value
   const Pack<T, VEC> z = splat_pack<T, VEC>(value);
   for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC)
     store_pack_nt<T, VEC>(out + col, z);
+}
+
+// (m, s) <- merge with (m2, s2), where s is a sum of 2^(v - m)
+__device__ __forceinline__ void lse2_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  const float a = m == -INFINITY ? 0.f : s * exp2_fast(m - M);
+  const float b = m2 == -INFINITY ? 0.f : s2 * exp2_fast(m2 - M);
+  m = M;
+  s = a + b;
+}
+
+// Block-wide log2-sum-exp from per-lane (m, s) pairs: one LDS exchange. `red`
+// holds 2*NW floats per parity; alternating `parity` between consecutive calls
+// lets the exchange go without a trailing barrier.
+template <int NW>
+__device__ __forceinline__ float block_lse2(float m, float s, float* red, int parity) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) lse2_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
+  if constexpr (NW > 1) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    float* r = red + parity * 2 * NW;
+    if (lane == 0) {
+      r[wave] = m;
+      r[NW + wave] = s;
+    }
+    __syncthreads();
+    m = r[0];
+    s = r[NW];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) lse2_merge(m, s, r[i], r[NW + i]);
+  }
+  return m + log2_fast(s);
 }
 
 // Row log-sum-exp in the log2 domain of (x * c), register-resident.
@@ -205,38 +373,79 @@ __device__ __forceinline__ float ce_scale(const CeArgs& a) {
 }
 
 // Training forward: loss_r = (lse - x_t) * s and dlogits = (softmax - onehot) * s
-// (kernels/cross_entropy.py:114-166). Ignored rows: loss 0 and a zero row.
+// (kernels/cross_entropy.py:114-166). Ignored rows: loss 0 and a zero row,
+// never read.
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T* logits, CeArgs a) {
   // dlogits may alias logits (in-place use): every element is read before the
-  // same thread overwrites it, so the pointers are not declared __restrict__.
-  __shared__ float red[BLOCK / kWave];
+  // same thread overwrites it, and a row's stores are issued before the next
+  // row's loads of the same vector, so the pointers are not declared __restrict__.
+  __shared__ float red[4 * (BLOCK / kWave)];
   const float scale = ce_scale(a);
-  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
-    const int64_t t = a.targets[row];
-    T* out = dlogits + row * a.ld_out;
-    const T* in = logits + row * a.ld_in;
-    if (a.has_ignore && t == a.ignore_index) {
-      fill_row<T, VEC, BLOCK>(out, (int)a.V, 0.f);
-      if (threadIdx.x == 0) a.loss_rows[row] = 0.f;
-      continue;
+  const int64_t G = gridDim.x;
+  auto is_live = [&](int64_t t) { return !(a.has_ignore && t == a.ignore_index) && t >= 0 && t < a.V; };
+  if constexpr (RESIDENT) {
+    const int n = row_len(a.V);
+    // dead rows (ignored or out of range) first: a zero (NaN) row, never read
+    for (int64_t row = blockIdx.x; row < a.rows; row += G) {
+      const int64_t t = a.targets[row];
+      if (!is_live(t)) {
+        const bool ignored = a.has_ignore && t == a.ignore_index;
+        fill_row<T, VEC, BLOCK>(dlogits + row * a.ld_out, n, ignored ? 0.f : NAN);
+        if (threadIdx.x == 0) a.loss_rows[row] = ignored ? 0.f : NAN;
+      }
     }
-    if (t < 0 || t >= a.V) {  // out-of-range target: NaN loss and gradient, no out-of-bounds read
-      fill_row<T, VEC, BLOCK>(out, (int)a.V, NAN);
-      if (threadIdx.x == 0) a.loss_rows[row] = NAN;
-      continue;
-    }
-    const float xt = to_f32<T>(in[t]);
-    const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
-    if constexpr (RESIDENT) {
-      const int n = row_len(a.V);
-      RowRegs<T, VEC, NCH, BLOCK> r;
-      r.load(in, n);
-      const float lse2 = row_lse2(r, n, kLog2e, red);
+    // then the live rows, each one's gradient stores overlapped with the next one's loads
+    auto next_live = [&](int64_t from) {
+      int64_t q = from;
+      while (q < a.rows && !is_live(a.targets[q])) q += G;
+      return q;
+    };
+    int64_t row = next_live(blockIdx.x);
+    if (row >= a.rows) return;
+    RowRegs<T, VEC, NCH, BLOCK> r;
+    r.load(logits + row * a.ld_in, n);
+    int parity = 0;
+    for (;;) {
+      const int64_t t = a.targets[row];
+      const T* in = logits + row * a.ld_in;
+      const int64_t next = next_live(row + G);
+      const float xt = to_f32<T>(in[t]);
+      const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
+      float m, s;
+      r.lse2_to_exp(n, kLog2e, &m, &s);
+      const float lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+      parity ^= 1;
+      r.opaque();
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
-      r.store_grad(out, n, kLog2e, lse2, (int)t, gscale);
-    } else {
-      const float lse2 = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red);
+      // the refill is unconditional (the last row re-reads itself, from L2) so the
+      // registers carry one definition around the loop
+      const T* src = next < a.rows ? logits + next * a.ld_in : in;
+      T* out = dlogits + row * a.ld_out;
+      const float f = m == -INFINITY ? 0.f : exp2_fast(m - lse2) * gscale;
+      r.store_exp_grad_then_load(out, n, f, src);
+      // the target element: (p_t - 1) * g, from x_t in fp32, stored after (and
+      // over) the vector store of the same thread
+      if ((int)threadIdx.x == (int)(t % RowRegs<T, VEC, NCH, BLOCK>::kSpan) / VEC)
+        out[t] = from_f32<T>((exp2_fast(fmaf(xt, kLog2e, -lse2)) - 1.f) * gscale);
+      if (next >= a.rows) break;
+      row = next;
+    }
+  } else {
+    __shared__ float red1[BLOCK / kWave];
+    for (int64_t row = blockIdx.x; row < a.rows; row += G) {
+      const int64_t t = a.targets[row];
+      T* out = dlogits + row * a.ld_out;
+      const T* in = logits + row * a.ld_in;
+      if (!is_live(t)) {
+        const bool ignored = a.has_ignore && t == a.ignore_index;
+        fill_row<T, VEC, BLOCK>(out, (int)a.V, ignored ? 0.f : NAN);
+        if (threadIdx.x == 0) a.loss_rows[row] = ignored ? 0.f : NAN;
+        continue;
+      }
+      const float xt = to_f32<T>(in[t]);
+      const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
+      const float lse2 = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red1);
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
       store_grad_stream<T, VEC, BLOCK>(out, in, (int)a.V, kLog2e, lse2, (int)t, gscale);
     }

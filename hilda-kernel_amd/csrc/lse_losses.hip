@@ -18,6 +18,7 @@
 #include "hk_internal.h"
 #include "../../include/hilda_kernel_amd.h"
 
+#include <algorithm>
 #include <math.h>
 #include <type_traits>
 
@@ -616,59 +617,129 @@ struct GrpoHot {
 // GRPO forward with the gradient fused in (kernels/grpo_loss.py:87-159 forward,
 // :166-234 backward at unit upstream gradient). Rows are all B*(L+1) positions
 // of the logits; the last position and masked tokens get a zero gradient row.
+// The per-token loss terms from logp (kernels/grpo_loss.py:103-133): the
+// result row and d loss / d logp.
+__device__ __forceinline__ GrpoOut grpo_terms(const GrpoHot& a, const GrpoTok& tk, float lse, float logp,
+                                             float* dlogp_out) {
+  const float old = a.has_old ? tk.old : logp;
+  const float coef1 = exp_fast(logp - old);
+  const float A = tk.adv;
+  const float coef2 = fminf(fmaxf(coef1, 1.f - a.eps_lo), 1.f + a.eps_hi);
+  const float l1 = coef1 * A, l2 = coef2 * A;
+  float loss = -fminf(l1, l2);
+  float kl = 0.f;
+  float dlogp = l2 >= l1 ? -coef1 * A : 0.f;
+  if (a.beta != 0.f) {
+    const float d = tk.ref - logp;
+    const float ed = exp_fast(d);
+    kl = ed - d - 1.f;
+    loss += a.beta * kl;
+    dlogp += a.beta * (1.f - ed);
+  }
+  *dlogp_out = dlogp;
+  const bool clipped = (coef1 < 1.f - a.eps_lo && A < 0.f) || (coef1 > 1.f + a.eps_hi && A > 0.f);
+  return GrpoOut{lse, loss, kl, clipped ? 1.f : 0.f};
+}
+
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT, bool GRAD>
 __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
                                                      GrpoHot a) {
-  __shared__ float red[BLOCK / kWave];
+  __shared__ float red[4 * (BLOCK / kWave)];
   const int64_t rows = a.B * (a.L + 1);
+  const int64_t G = gridDim.x;
   const float c = kLog2e * a.inv_T;
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+  // a row is live when it is a token position (l < L) with a nonzero mask
+  auto live = [&](int64_t row, GrpoTok* tk) {
     const int64_t b = row / (a.L + 1), l = row - b * (a.L + 1);
-    T* out = GRAD ? dlogits + row * a.V : nullptr;
-    const int64_t o = b * a.L + l;  // token index (valid when l < L)
+    if (l == a.L) return false;
+    *tk = a.tok[b * a.L + l];
+    return tk->m != 0.f;
+  };
+  auto token = [&](int64_t row) {
+    const int64_t b = row / (a.L + 1);
+    return row - b;  // b * L + l
+  };
+  // dead rows: a zero gradient row (never read) and zero results
+  for (int64_t row = blockIdx.x; row < rows; row += G) {
     GrpoTok tk{};
-    if (l < a.L) tk = a.tok[o];
-    if (l == a.L || tk.m == 0.f) {
-      if constexpr (GRAD) fill_row<T, VEC, BLOCK>(out, (int)a.V, 0.f);
-      if (l < a.L && threadIdx.x == 0) a.out[o] = GrpoOut{0.f, 0.f, 0.f, 0.f};
-      continue;
+    if (!live(row, &tk)) {
+      if constexpr (GRAD) fill_row<T, VEC, BLOCK>(dlogits + row * a.V, (int)a.V, 0.f);
+      const int64_t b = row / (a.L + 1), l = row - b * (a.L + 1);
+      if (l < a.L && threadIdx.x == 0) a.out[b * a.L + l] = GrpoOut{0.f, 0.f, 0.f, 0.f};
     }
-    const T* in = logits + row * a.V;
+  }
+  if constexpr (RESIDENT && GRAD) {
+    // live rows, each one's gradient stores overlapped with the next one's loads
     const int n = row_len(a.V);
-    float lse2;
+    auto next_live = [&](int64_t from) {
+      int64_t q = from;
+      GrpoTok t{};
+      while (q < rows && !live(q, &t)) q += G;
+      return q;
+    };
+    int64_t row = next_live(blockIdx.x);
+    if (row >= rows) return;
     RowRegs<T, VEC, NCH, BLOCK> r;
-    if constexpr (RESIDENT) {
-      r.load(in, n);
-      lse2 = row_lse2(r, n, c, red);
-    } else {
-      lse2 = row_lse2_stream<T, VEC, BLOCK>(in, n, c, red);
-    }
-    const float lse = lse2 * kLn2;
-    const float logp = tk.id >= 0 ? to_f32<T>(in[tk.id]) * a.inv_T - lse : NAN;
-    const float old = a.has_old ? tk.old : logp;
-    const float coef1 = exp_fast(logp - old);
-    const float A = tk.adv;
-    const float coef2 = fminf(fmaxf(coef1, 1.f - a.eps_lo), 1.f + a.eps_hi);
-    const float l1 = coef1 * A, l2 = coef2 * A;
-    float loss = -fminf(l1, l2);
-    float kl = 0.f;
-    float dlogp = l2 >= l1 ? -coef1 * A : 0.f;
-    if (a.beta != 0.f) {
-      const float d = tk.ref - logp;
-      const float ed = exp_fast(d);
-      kl = ed - d - 1.f;
-      loss += a.beta * kl;
-      dlogp += a.beta * (1.f - ed);
-    }
-    if (threadIdx.x == 0) {
-      const bool clipped = (coef1 < 1.f - a.eps_lo && A < 0.f) || (coef1 > 1.f + a.eps_hi && A > 0.f);
-      a.out[o] = GrpoOut{lse, loss, kl, clipped ? 1.f : 0.f};
-    }
-    if constexpr (GRAD) {
+    r.load(logits + row * a.V, n);
+    int parity = 0;
+    for (;;) {
+      const T* in = logits + row * a.V;
+      // the token record is uniform: keep it in scalar registers, off the row's VGPR budget
+      GrpoTok tk = a.tok[token(row)];
+      tk.id = __builtin_amdgcn_readfirstlane(tk.id);
+      tk.old = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.old)));
+      tk.ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.ref)));
+      tk.adv = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.adv)));
+      tk.gs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.gs)));
+      const int64_t next = next_live(row + G);
+      const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
+      float m, s;
+      r.lse2_to_exp(n, c, &m, &s);
+      const float lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+      parity ^= 1;
+      r.opaque();
+      const float lse = lse2 * kLn2;
+      const float logp = tk.id >= 0 ? xid * a.inv_T - lse : NAN;
+      float dlogp;
+      const GrpoOut res = grpo_terms(a, tk, lse, logp, &dlogp);
+      if (threadIdx.x == 0) a.out[token(row)] = res;
       // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
       const float g = -dlogp * tk.gs;
-      if constexpr (RESIDENT) r.store_grad(out, n, c, lse2, tk.id, g);
-      else store_grad_stream<T, VEC, BLOCK>(out, in, n, c, lse2, tk.id, g);
+      T* out = dlogits + row * a.V;
+      const T* src = next < rows ? logits + next * a.V : in;  // unconditional refill (see the CE kernel)
+      const float f = m == -INFINITY ? 0.f : exp2_fast(m - lse2) * g;
+      r.store_exp_grad_then_load(out, n, f, src);
+      if (tk.id >= 0 && (int)threadIdx.x == (tk.id % RowRegs<T, VEC, NCH, BLOCK>::kSpan) / VEC)
+        out[tk.id] = from_f32<T>((exp2_fast(fmaf(xid, c, -lse2)) - 1.f) * g);
+      if (next >= rows) break;
+      row = next;
+    }
+  } else {
+    int parity = 0;
+    for (int64_t row = blockIdx.x; row < rows; row += G) {
+      GrpoTok tk{};
+      if (!live(row, &tk)) continue;
+      T* out = GRAD ? dlogits + row * a.V : nullptr;
+      const T* in = logits + row * a.V;
+      const int n = row_len(a.V);
+      float lse2;
+      if constexpr (RESIDENT) {
+        // the same reduction as the gradient path, so both give bitwise equal results
+        RowRegs<T, VEC, NCH, BLOCK> r;
+        r.load(in, n);
+        float m, s;
+        r.lse2_to_exp(n, c, &m, &s);
+        lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+        parity ^= 1;
+      } else {
+        lse2 = row_lse2_stream<T, VEC, BLOCK>(in, n, c, red);
+      }
+      const float lse = lse2 * kLn2;
+      const float logp = tk.id >= 0 ? to_f32<T>(in[tk.id]) * a.inv_T - lse : NAN;
+      float dlogp;
+      const GrpoOut res = grpo_terms(a, tk, lse, logp, &dlogp);
+      if (threadIdx.x == 0) a.out[token(row)] = res;
+      if constexpr (GRAD) store_grad_stream<T, VEC, BLOCK>(out, in, n, c, lse2, tk.id, -dlogp * tk.gs);
     }
   }
 }
@@ -697,24 +768,22 @@ __global__ __launch_bounds__(1024) void grpo_prep_kernel(GrpoArgs a, GrpoTok* __
 }
 
 // out = [mean_b(sum_l m*loss / max(len_b,1)), sum m*kl / max(sum m,1), sum m*clip / max(sum m,1)]
-// (kernels/grpo_loss.py:290-295); also scatters the per-token rows.
+// (kernels/grpo_loss.py:290-295); also scatters the per-token rows. Each wave
+// owns whole sequences (b = wave, wave + 16, ...) and reduces them with
+// shuffles; one block-wide combine at the end.
 __global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const GrpoTok* __restrict__ tok,
                                                              const GrpoOut* __restrict__ res, float* __restrict__ loss_out,
                                                              float* __restrict__ kl_out, float* __restrict__ clip_out) {
-  __shared__ double red[16];
-  auto bsum = [&](double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = v;
-    __syncthreads();
-    double t = 0.0;
-    for (int i = 0; i < 16; ++i) t += red[i];
-    __syncthreads();
-    return t;
+  __shared__ double red[4][16];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  auto wsum = [](double v) {
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
   };
   double loss = 0.0, msum = 0.0, kls = 0.0, clips = 0.0;
-  for (int64_t b = 0; b < a.B; ++b) {
+  for (int64_t b = wave; b < a.B; b += 16) {
     double ls = 0.0, ms = 0.0, ks = 0.0, cs = 0.0;
-    for (int64_t l = threadIdx.x; l < a.L; l += 1024) {
+    for (int64_t l = lane; l < a.L; l += kWave) {
       const int64_t o = b * a.L + l;
       const double m = tok[o].m;
       const GrpoOut r = res[o];
@@ -727,20 +796,28 @@ __global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const G
       a.kl_rows[o] = r.kl;
       a.clip_rows[o] = r.clip;
     }
-    ls = bsum(ls);
-    ms = bsum(ms);
-    ks = bsum(ks);
-    cs = bsum(cs);
+    ls = wsum(ls);
+    ms = wsum(ms);
     loss += ls / (ms > 1.0 ? ms : 1.0);
     msum += ms;
-    kls += ks;
-    clips += cs;
+    kls += wsum(ks);
+    clips += wsum(cs);
   }
+  if (lane == 0) {
+    red[0][wave] = loss;
+    red[1][wave] = msum;
+    red[2][wave] = kls;
+    red[3][wave] = clips;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const double d = msum > 1.0 ? msum : 1.0;
-    loss_out[0] = (float)(loss / (double)a.B);
-    if (kl_out) kl_out[0] = (float)(kls / d);
-    clip_out[0] = (float)(clips / d);
+    double t[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int i = 0; i < 16; ++i)
+      for (int k = 0; k < 4; ++k) t[k] += red[k][i];
+    const double d = t[1] > 1.0 ? t[1] : 1.0;
+    loss_out[0] = (float)(t[0] / (double)a.B);
+    if (kl_out) kl_out[0] = (float)(t[2] / d);
+    clip_out[0] = (float)(t[3] / d);
   }
 }
 
@@ -985,8 +1062,13 @@ int hk_scale_rows(void* out, const void* in, const float* g, const float* g_prev
   return dispatch_t(dtype, [&](auto tt) {
     using T = typename decltype(tt)::type;
     const int64_t total = rows * (vec_ok ? cols / vec : cols);
-    const int64_t blocks = cdiv(total, 256 * 4);
-    const dim3 grid((unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536));
+    // grid-stride over a few blocks per CU: a call that turns out to be a no-op
+    // (g == 1, decided on the device) then costs one short launch, not 64K blocks
+    const int dev = current_device();
+    if (dev < 0) return (int)hipErrorNoDevice;
+    const int64_t cap = (int64_t)cu_count(dev) * 8;
+    const int64_t blocks = std::min<int64_t>(std::max<int64_t>(cdiv(total, 256 * 4), 1), cap);
+    const dim3 grid((unsigned)blocks);
     if (vec_ok)
       hipLaunchKernelGGL((scale_rows_kernel<T, 16 / sizeof(T)>), grid, dim3(256), 0, st, (T*)out, (const T*)in, g,
                          g_prev, per_row, skip_if_one, rows, cols, ld_in, ld_out);

@@ -159,7 +159,7 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
 
 // Rows per chunk: a multiple of 8 (chunk starts stay 16-byte aligned in X^T), at most BT.
 int64_t flce_chunk(int64_t BT, int64_t chunk) {
-  if (chunk <= 0) chunk = 4096;
+  if (chunk <= 0) chunk = 8192;
   chunk = std::max<int64_t>(8, chunk & ~(int64_t)7);
   return std::min<int64_t>(chunk, BT > 0 ? BT : 1);
 }

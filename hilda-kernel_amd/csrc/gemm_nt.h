@@ -1,6 +1,9 @@
-// bf16/fp16 "NT" GEMM on gfx950 MFMA: C[M,N] = A[M,K] * B[N,K]^T, both operands
-// K-contiguous, fp32 accumulation, result handed to an epilogue functor in
-// 16-byte row chunks.
+// bf16/fp16 GEMM on gfx950 MFMA: C[M,N] = sum_k A(m,k) * B(n,k), fp32
+// accumulation, result handed to an epilogue functor in 16-byte row chunks.
+// Each operand is stored either K-contiguous (A[m][k], the "NT" layout) or
+// MN-contiguous (A[k][m]); the stage tiles keep that orientation in LDS and
+// the MN-contiguous ones are read with the transposing ds_read_b64_tr_b16, so
+// no operand is ever transposed in memory.
 //
 // Layout of the work:
 // * One workgroup computes a BM x BN tile with WGM x WGN waves; each wave owns a
@@ -11,9 +14,9 @@
 // * Stage tiles are filled by buffer_load_dwordx4 ... lds (no VGPR round
 //   trip): each lane's 16 bytes land at LDS base + 16*lane, so the swizzle is
 //   applied to the global offset each lane fetches. The buffer resource covers
-//   only this block's rows of A (B), so rows past M (N) read as zero; columns
-//   past K (the last, partial stage) are redirected past the end of the buffer
-//   and read as zero too. Nothing is clamped and nothing is read out of bounds.
+//   only what the tile may read; elements past M, N or K read as zero, either
+//   because they lie past the buffer's end or because the lane's offset is
+//   redirected there. Nothing is clamped and nothing is read out of bounds.
 // * The loads of stage kt+STAGES are issued as soon as every wave has finished
 //   reading stage kt. One barrier per stage, with no memory fence (a fence
 //   would drain the loads of the later stages too); vmcnt is counted by hand.
@@ -137,6 +140,120 @@ constexpr int kRsrcWord3 = 0x00020000;
 constexpr uint32_t kOobOffset = 0x7ff00000u;
 
 // ---------------------------------------------------------------------------
+// One operand panel: ROWS rows (of M or N) by the K range, stored K-contiguous
+// (element (r, k) at p[r*ld + k]) or MN-contiguous (at p[k*ld + r]).
+//
+// K-contiguous stage tile: [ROWS][BK], 16-byte chunk index XOR swz_xor(row).
+// A 1 KiB load instruction covers 64/CPR rows. The buffer spans the panel's
+// rows (rows past the matrix read zero); chunks at or past column K are
+// redirected out of the buffer.
+//
+// MN-contiguous stage tile: [BK][ROWS], 16-byte chunk index XOR 4*(k%4), which
+// keeps the 4 k-rows x 4 chunks a 32-lane ds_read_b64_tr_b16 touches in
+// distinct banks. A 1 KiB load covers 1024/(2*ROWS) k-rows. The buffer starts
+// at the stage's first k-row and ends at the matrix's last element, so k-rows
+// past K read zero; chunks at or past the matrix's last row are redirected.
+// A fragment (32 rows x 16 k of the MFMA operand layout: lane l holds row
+// l%32, k = 8*(l/32) .. +7) is two tr16 reads: within each 16-lane group the
+// read returns out[j][q] = in[4q + j/4][j%4], so lane 16g+i points at k-row
+// 8*(g/2) + 4h + i/4 and row 16*(g%2) + 4*(i%4).
+// ---------------------------------------------------------------------------
+template <typename T, class C, int ROWS, bool MN>
+struct Operand {
+  static constexpr int I = ROWS * C::BK * (int)sizeof(T) / 1024 / C::NW;  // 1 KiB loads per wave per stage
+  static_assert(I * 1024 * C::NW == ROWS * C::BK * (int)sizeof(T), "stage tile must split in 1 KiB loads");
+  static_assert(!MN || ROWS / 8 >= 16, "MN-contiguous tiles need at least 16 chunks per k-row");
+  uint32_t voff[I];
+  int key[I];  // K-contiguous: first column of the chunk in the stage; MN: first row of the chunk
+  const T* p;
+  int64_t ld;
+  int r0, rows_valid, K;
+
+  __device__ __forceinline__ void init(const T* ptr, int64_t ld_, int r0_, int nrows, int K_, int wave, int lane) {
+    p = ptr;
+    ld = ld_;
+    r0 = r0_;
+    rows_valid = min(ROWS, nrows - r0_);
+    K = K_;
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const int q = (wave * I + i) * 64 + lane;  // chunk index in the stage tile
+      if constexpr (!MN) {
+        constexpr int CPR = C::BK / 8;
+        const int r = q / CPR;
+        key[i] = ((q % CPR) ^ swz_xor<C::BK>(r)) << 3;
+        voff[i] = (uint32_t)(r * ld + key[i]) * sizeof(T);
+      } else {
+        constexpr int CPR = ROWS / 8;
+        const int k = q / CPR;
+        key[i] = ((q % CPR) ^ (4 * (k & 3))) << 3;
+        voff[i] = (uint32_t)(k * ld + key[i]) * sizeof(T);
+      }
+    }
+  }
+
+  // Stage kst (a stage at or past KT is a zero-length buffer: the loads
+  // return zeros without touching memory) into `tile`.
+  __device__ __forceinline__ void issue(T* tile, int kst, int KT, int wave) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const bool live = kst < KT;
+    const int k0 = live ? kst * C::BK : 0;
+    if constexpr (!MN) {
+      const int lim = K - k0;  // columns of this stage inside the matrix
+      const int nrec = live ? (int)(rows_valid * ld * (int64_t)sizeof(T)) : 0;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(p + (int64_t)r0 * ld), 0, nrec, kRsrcWord3);
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * 512, 16,
+                                                 key[i] < lim ? voff[i] : kOobOffset, k0 * sizeof(T), 0, 0);
+    } else {
+      // from the stage's first k-row to the matrix's last element
+      const int64_t span = live ? ((int64_t)(K - k0 - 1) * ld + (rows_valid > 0 ? rows_valid : 0)) * sizeof(T) : 0;
+      const int nrec = (int)(span < (int64_t)kOobOffset ? span : (int64_t)kOobOffset);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<T*>(p + (int64_t)k0 * ld + r0), 0, nrec, kRsrcWord3);
+#pragma unroll
+      for (int i = 0; i < I; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * 512, 16,
+                                                 key[i] < rows_valid ? voff[i] : kOobOffset, 0, 0, 0);
+    }
+#endif
+  }
+
+  // CNT fragments for sub-step ks, rows R, R+32, ... of the tile
+  template <int CNT>
+  __device__ __forceinline__ void frag(const T* tile, int ks, int R, int lane, u32x4* out) const {
+    if constexpr (!MN) {
+      const int fr = lane & 31, fk = lane >> 5;
+#pragma unroll
+      for (int t = 0; t < CNT; ++t)
+        out[t] = *reinterpret_cast<const u32x4*>(tile + swz<C::BK>(R + t * 32 + fr, ks * 2 + fk));
+    } else {
+#if defined(__HIP_DEVICE_COMPILE__)
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+      const int g = lane >> 4, i = lane & 15;
+      const int kq = i >> 2;  // k % 4 of this lane's k-row
+#pragma unroll
+      for (int t = 0; t < CNT; ++t) {
+        const int r = R + t * 32 + 16 * (g & 1) + 4 * (i & 3);
+        v4i16 h[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int k = ks * 16 + 8 * (g >> 1) + 4 * hh + kq;
+          const int e = k * ROWS + (((r >> 3) ^ (4 * kq)) << 3) + (r & 7);
+          h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(tile + e));
+        }
+        const u32x2 lo = __builtin_bit_cast(u32x2, h[0]), hi = __builtin_bit_cast(u32x2, h[1]);
+        out[t] = u32x4{lo.x, lo.y, hi.x, hi.y};
+      }
+#endif
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Epilogue contract. An epilogue functor declares
 //   using Stage = float or the input type;   // how values are staged in LDS
 //   using Prior = what load() returns;       // (an empty struct if kReads is false)
@@ -148,7 +265,7 @@ constexpr uint32_t kOobOffset = 0x7ff00000u;
 // matrix (n is the full chunk unless the chunk straddles column N).
 // ---------------------------------------------------------------------------
 
-template <typename T, class C, class Epi>
+template <typename T, class C, bool AMN, bool BMN, class Epi>
 __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A, const T* __restrict__ B, Shape g,
                                                         Epi epi) {
   using S = typename Epi::Stage;
@@ -184,67 +301,21 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
   const int KT = (g.K + C::BK - 1) / C::BK;  // >= 1 (checked by the launcher)
   const int fr = lane & 31, fk = lane >> 5;
 
-  // The buffer builtins exist only for the device target; the host pass still
-  // instantiates this body to emit the launch stub.
-#if defined(__HIP_DEVICE_COMPILE__)
-  const int rows_a = min(C::BM, g.M - m0), rows_b = min(C::BN, g.N - n0);
-  T* const pa = const_cast<T*>(A + (int64_t)m0 * g.lda);
-  T* const pb = const_cast<T*>(B + (int64_t)n0 * g.ldb);
-  const int nrec_a = (int)(rows_a * g.lda * (int64_t)sizeof(T));
-  const int nrec_b = (int)(rows_b * g.ldb * (int64_t)sizeof(T));
-  // Load instruction i of this wave covers stage chunks p = (wave*I + i)*64 + lane:
-  // row p / CPR, stored chunk p % CPR, which holds logical k-chunk (p % CPR) ^ swz_xor(row).
-  uint32_t voffA[C::IA], voffB[C::IB];
-  int kcA[C::IA], kcB[C::IB];  // first column of the chunk within the stage
-  const int lr = lane / C::CPR, lc = lane % C::CPR;
-#pragma unroll
-  for (int i = 0; i < C::IA; ++i) {
-    const int r = (wave * C::IA + i) * C::RPI + lr;
-    kcA[i] = (lc ^ swz_xor<C::BK>(r)) << 3;
-    voffA[i] = (uint32_t)(r * g.lda + kcA[i]) * sizeof(T);
-  }
-#pragma unroll
-  for (int i = 0; i < C::IB; ++i) {
-    const int r = (wave * C::IB + i) * C::RPI + lr;
-    kcB[i] = (lc ^ swz_xor<C::BK>(r)) << 3;
-    voffB[i] = (uint32_t)(r * g.ldb + kcB[i]) * sizeof(T);
-  }
-  // Stage kst into LDS buffer `stage`. Every call issues the same NI loads, so
-  // the vmcnt arithmetic never depends on the position in the loop: a stage
-  // past the end goes through a zero-length buffer, whose loads return zeros
-  // without touching memory (and land in a buffer nobody reads again). Chunks
-  // at or past column K read zeros through an offset past the buffer's end.
+  Operand<T, C, C::BM, AMN> opa;
+  Operand<T, C, C::BN, BMN> opb;
+  opa.init(A, g.lda, m0, g.M, g.K, wave, lane);
+  opb.init(B, g.ldb, n0, g.N, g.K, wave, lane);
   auto issue = [&](int stage, int kst) {
-    const bool live = kst < KT;
-    const int k0 = live ? kst * C::BK : 0;
-    const int lim = g.K - k0;  // columns of this stage inside the matrix
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(pa, 0, live ? nrec_a : 0, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(pb, 0, live ? nrec_b : 0, kRsrcWord3);
     T* la = lds + stage * C::STAGE;
-    T* lb = la + C::BM * C::BK;
-#pragma unroll
-    for (int i = 0; i < C::IA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, la + (wave * C::IA + i) * 512, 16,
-                                               kcA[i] < lim ? voffA[i] : kOobOffset, k0 * sizeof(T), 0, 0);
-#pragma unroll
-    for (int i = 0; i < C::IB; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, lb + (wave * C::IB + i) * 512, 16,
-                                               kcB[i] < lim ? voffB[i] : kOobOffset, k0 * sizeof(T), 0, 0);
+    opa.issue(la, kst, KT, wave);
+    opb.issue(la + C::BM * C::BK, kst, KT, wave);
   };
-#else
-  auto issue = [&](int, int) {};
-#endif
 
   u32x4 fa[2][C::TM], fb[2][C::TN];
   auto frag = [&](int stage, int ks, u32x4* a, u32x4* b) {
     const T* la = lds + stage * C::STAGE;
-    const T* lb = la + C::BM * C::BK;
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-      a[i] = *reinterpret_cast<const u32x4*>(la + swz<C::BK>(wm * C::WTM + i * 32 + fr, ks * 2 + fk));
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-      b[j] = *reinterpret_cast<const u32x4*>(lb + swz<C::BK>(wn * C::WTN + j * 32 + fr, ks * 2 + fk));
+    opa.template frag<C::TM>(la, ks, wm * C::WTM, lane, a);
+    opb.template frag<C::TN>(la + C::BM * C::BK, ks, wn * C::WTN, lane, b);
   };
   auto mma = [&](int buf, int first, int count) {
 #pragma unroll
@@ -361,21 +432,44 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 }
 
 // Returns 0, or -1 with the error set for shapes the kernel does not take.
-template <typename T, class C = DefaultCfg, class Epi>
+// AMN / BMN: the operand is stored MN-contiguous (A[k][m], B[k][n]) instead of
+// K-contiguous (A[m][k], B[n][k]); lda / ldb are the leading dimensions of
+// whichever layout is used.
+template <typename T, class C = DefaultCfg, bool AMN = false, bool BMN = false, class Epi>
 int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st) {
   if (M == 0 || N == 0) return 0;
-  if (K <= 0 || K % 8 != 0 || lda % 8 != 0 || ldb % 8 != 0 || lda < K || ldb < K) {
-    set_error("gemm_nt: K (%d) must be a positive multiple of 8, lda/ldb multiples of 8 and >= K", K);
+  if (K <= 0) {
+    set_error("gemm: K (%d) must be positive", K);
     return -1;
   }
-  if ((int64_t)C::BM * lda * (int64_t)sizeof(T) >= (int64_t)kOobOffset ||
-      (int64_t)C::BN * ldb * (int64_t)sizeof(T) >= (int64_t)kOobOffset) {
-    set_error("gemm_nt: a %d-row panel of A or B exceeds the 2 GiB buffer range", C::BM);
-    return -1;
-  }
+  auto check = [&](bool mn, int rows, int64_t ld, const char* name) {
+    if (mn) {
+      if (rows % 8 != 0 || ld % 8 != 0 || ld < rows) {
+        set_error("gemm: MN-contiguous %s needs rows (%d) and ld (%lld) multiples of 8, ld >= rows", name, rows,
+                  (long long)ld);
+        return false;
+      }
+      if ((int64_t)C::BK * ld * (int64_t)sizeof(T) >= (int64_t)kOobOffset) {
+        set_error("gemm: a %d-row stage of %s exceeds the 2 GiB buffer range", C::BK, name);
+        return false;
+      }
+    } else {
+      if (K % 8 != 0 || ld % 8 != 0 || ld < K) {
+        set_error("gemm: K-contiguous %s needs K (%d) and ld (%lld) multiples of 8, ld >= K", name, K, (long long)ld);
+        return false;
+      }
+      if ((int64_t)C::BM * ld * (int64_t)sizeof(T) >= (int64_t)kOobOffset) {
+        set_error("gemm: a %d-row panel of %s exceeds the 2 GiB buffer range", C::BM, name);
+        return false;
+      }
+    }
+    return true;
+  };
+  if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
   Shape g{M, N, K, lda, ldb};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, C, AMN, BMN, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g,
+                     epi);
   return check_launch("gemm_nt_kernel");
 }
 

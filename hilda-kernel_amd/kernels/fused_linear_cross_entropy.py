@@ -24,7 +24,7 @@ import torch
 from . import _lib
 from .cross_entropy import scale_rows_
 
-DEFAULT_CHUNK = 4096
+DEFAULT_CHUNK = 8192
 
 
 def fused_linear_cross_entropy_forward(hidden_states, weight, targets, ignore_index=-100, reduction='mean',

@@ -189,7 +189,7 @@ int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_
 /* FusedLinearCrossEntropy                                                 */
 /* ----------------------------------------------------------------------- */
 /* Bytes of device workspace hk_fused_linear_cross_entropy needs (0 for an
- * unsupported dtype). chunk <= 0 selects the default (4096 rows). */
+ * unsupported dtype). chunk <= 0 selects the default (8192 rows). */
 size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype,
                                                     int with_grad);
 

@@ -89,27 +89,44 @@ __global__ __launch_bounds__(256) void zero16_kernel(u32x4* __restrict__ p, int6
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0, 0, 0, 0};
 }
 
-// out[c, r] = in[r, c] for a rows x cols matrix (row strides ld_in, ld_out);
-// output columns r in [rows, rows_pad) are written as zeros. 64x64 tiles through LDS.
+// out[c, r] = in[r, c] for a rows x cols matrix of a 16-bit type (row strides
+// ld_in, ld_out, both multiples of 8; cols a multiple of 8); output columns r
+// in [rows, rows_pad) are written as zeros (rows_pad a multiple of 8). 64x64
+// tiles: 16-byte global loads and stores, the tile staged in LDS with a pitch
+// of 66 elements (33 dwords), so the column-gathering 2-byte reads of a wave
+// fall in distinct banks.
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, const T* __restrict__ in, int64_t rows,
                                                         int64_t rows_pad, int64_t cols, int64_t ld_in,
                                                         int64_t ld_out) {
-  __shared__ T tile[64][65];
+  constexpr int P = 66;
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * P];
+  const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int y = ty + i * 4;
-    const int64_t r = r0 + y, c = c0 + tx;
-    tile[y][tx] = (r < rows && c < cols) ? in[r * ld_in + c] : from_f32<T>(0.f);
+  for (int k = 0; k < 2; ++k) {
+    const int rr = t / 8 + 32 * k, cc = (t % 8) * 8;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < rows && c < cols) v = *reinterpret_cast<const u32x4*>(in + r * ld_in + c);
+    uint32_t* tp = reinterpret_cast<uint32_t*>(tile + rr * P + cc);
+    tp[0] = v.x;
+    tp[1] = v.y;
+    tp[2] = v.z;
+    tp[3] = v.w;
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int y = ty + i * 4;
-    const int64_t c = c0 + y, r = r0 + tx;
-    if (r < rows_pad && c < cols) out[c * ld_out + r] = tile[tx][y];
+  for (int k = 0; k < 2; ++k) {
+    const int oc = t / 8 + 32 * k, oq = (t % 8) * 8;
+    const int64_t c = c0 + oc, r = r0 + oq;
+    if (c < cols && r < rows_pad) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)tile[(oq + 2 * i) * P + oc] | ((uint32_t)tile[(oq + 2 * i + 1) * P + oc] << 16);
+      *reinterpret_cast<u32x4*>(out + c * ld_out + r) = u32x4{w[0], w[1], w[2], w[3]};
+    }
   }
 }
 
@@ -124,6 +141,9 @@ template <typename T>
 int launch_transpose(T* out, const T* in, int64_t rows, int64_t rows_pad, int64_t cols, int64_t ld_in,
                      int64_t ld_out, hipStream_t st) {
   if (rows_pad == 0 || cols == 0) return HK_OK;
+  HK_REQUIRE(cols % 8 == 0 && rows_pad % 8 == 0 && ld_in % 8 == 0 && ld_out % 8 == 0 && aligned_to(in, 16) &&
+                 aligned_to(out, 16),
+             "transpose: 16-byte rows and chunks expected");
   const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows_pad, 64));
   hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out);
   return check_launch("transpose_kernel");

@@ -37,6 +37,7 @@ SIGNATURES = {
     "hk_fused_add_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
     "hk_rope": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                        _i32, _i32, _i32, _p]),
+    "hk_rope_qk": (_i32, [_p, _p] + [_i64] * 7 + [_p, _p] + [_i64] * 7 + [_p, _p] + [_i64] * 6 + [_i32, _i32, _i32, _p]),
     "hk_swiglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "hk_swiglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
     "hk_cross_entropy_workspace_size": (_sz, [_i64]),

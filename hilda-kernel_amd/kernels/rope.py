@@ -34,6 +34,29 @@ def _launch(x_in, x_out, cos, sin, inverse):
               _lib.dtype_code(x_in), _lib.dtype_code(cos), int(inverse), _lib.stream_of(x_in.device))
 
 
+def _launch_qk(q_in, q_out, k_in, k_out, cos, sin, inverse):
+    """q and k in one launch when they share batch, positions, head_dim and dtype."""
+    bsz, hq, seq_len, hd = q_in.shape
+    same = (k_in.shape[0] == bsz and k_in.shape[2] == seq_len and k_in.shape[3] == hd and k_in.dtype == q_in.dtype
+            and q_in.stride(-1) == 1 and k_in.stride(-1) == 1)
+    if not same or q_in.numel() == 0 or k_in.numel() == 0:
+        _launch(q_in, q_out, cos, sin, inverse)
+        _launch(k_in, k_out, cos, sin, inverse)
+        return
+    assert q_out.stride(-1) == 1 and k_out.stride(-1) == 1
+    assert cos.shape == sin.shape and cos.dim() == 3 and cos.shape[-1] == hd // 2, \
+        f"cos/sin must be (1 or bsz, seq, head_dim/2); got {tuple(cos.shape)}"
+    assert cos.shape[1] >= seq_len, f"cos/sin cover {cos.shape[1]} positions, need {seq_len}"
+    assert cos.shape[0] in (1, bsz)
+    assert cos.dtype == sin.dtype and cos.stride() == sin.stride()
+    _lib.call("hk_rope_qk", q_out.data_ptr(), q_in.data_ptr(), hq,
+              q_in.stride(0), q_in.stride(1), q_in.stride(2), q_out.stride(0), q_out.stride(1), q_out.stride(2),
+              k_out.data_ptr(), k_in.data_ptr(), k_in.shape[1],
+              k_in.stride(0), k_in.stride(1), k_in.stride(2), k_out.stride(0), k_out.stride(1), k_out.stride(2),
+              cos.data_ptr(), sin.data_ptr(), bsz, seq_len, hd, cos.shape[0], cos.stride(0), cos.stride(1),
+              _lib.dtype_code(q_in), _lib.dtype_code(cos), int(inverse), _lib.stream_of(q_in.device))
+
+
 def _tables(cos, sin):
     if cos.stride(-1) != 1:
         cos = cos.contiguous()
@@ -49,8 +72,7 @@ def rope_forward(q, k, cos, sin):
     cos, sin = _tables(cos, sin)
     q_out = torch.empty_like(q)
     k_out = torch.empty_like(k)
-    _launch(q, q_out, cos, sin, inverse=False)
-    _launch(k, k_out, cos, sin, inverse=False)
+    _launch_qk(q, q_out, k, k_out, cos, sin, inverse=False)
     return q_out, k_out, cos, sin
 
 
@@ -61,8 +83,7 @@ def rope_backward(dq, dk, cos, sin):
     # empty_like keeps a dense input's layout and is contiguous for broadcast (zero-stride) grads
     dq_out = torch.empty_like(dq)
     dk_out = torch.empty_like(dk)
-    _launch(dq, dq_out, cos, sin, inverse=True)
-    _launch(dk, dk_out, cos, sin, inverse=True)
+    _launch_qk(dq, dq_out, dk, dk_out, cos, sin, inverse=True)
     return dq_out, dk_out
 
 

@@ -109,6 +109,16 @@ int hk_rope(void* out, const void* in, const void* cos, const void* sin, int64_t
             int64_t cos_B, int64_t cos_sB, int64_t cos_sT, int dtype_x, int dtype_cs, int inverse,
             hk_stream_t stream);
 
+/* Replaces the pair of _launch calls in rope_forward (rope.py:133-134) and
+ * rope_backward (rope.py:169-170): q (B, Hq, T, D) and k (B, Hk, T, D), each
+ * with its own input/output strides, rotated by the same cos/sin in one
+ * launch. Arguments as for hk_rope. */
+int hk_rope_qk(void* q_out, const void* q_in, int64_t Hq, int64_t q_in_sB, int64_t q_in_sH, int64_t q_in_sT,
+               int64_t q_out_sB, int64_t q_out_sH, int64_t q_out_sT, void* k_out, const void* k_in, int64_t Hk,
+               int64_t k_in_sB, int64_t k_in_sH, int64_t k_in_sT, int64_t k_out_sB, int64_t k_out_sH,
+               int64_t k_out_sT, const void* cos, const void* sin, int64_t B, int64_t T, int64_t D, int64_t cos_B,
+               int64_t cos_sB, int64_t cos_sT, int dtype_x, int dtype_cs, int inverse, hk_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* SwiGLU                                                                  */
 /* ----------------------------------------------------------------------- */

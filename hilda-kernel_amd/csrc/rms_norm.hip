@@ -16,9 +16,9 @@
 // 16-bit inputs, fp64 for fp32 inputs (a sum over thousands of rows in fp32
 // drifts by ~1e-4, more than the 1e-5 fp32 tolerance allows). The groups'
 // accumulators then go either into fp64 atomics on one [cols] accumulator or
-// into one partial row per group, summed by a two-level reduction; the choice
-// follows the reference rule "atomic when rows <= 8 * CU count"
-// (rms_norm.py:325-326).
+// into one fp32 partial row per group (a run of rows rounds once), summed in
+// fp64 by a separate pass; the choice follows the reference rule "atomic when
+// rows <= 8 * CU count" (rms_norm.py:325-326).
 #include "hk_common.h"
 #include "../../include/hilda_kernel_amd.h"
 
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
         if (atomic) {
           if (row0 < rows) unsafeAtomicAdd(static_cast<double*>(dw_ws) + col + i, (double)acc[j][i]);
         } else {
-          static_cast<A*>(dw_ws)[group * cols + col + i] = acc[j][i];
+          static_cast<float*>(dw_ws)[group * cols + col + i] = (float)acc[j][i];
         }
       }
     }
@@ -228,13 +228,14 @@ __global__ __launch_bounds__(256) void cast_f64_kernel(W* __restrict__ out, cons
     out[i] = from_f32<W>((float)in[i]);
 }
 
-// out[c] = sum_g part[g*cols + c]: a block of 64 columns x 16 group slices,
-// four independent partial sums per thread so its loads overlap. (A two-level
+// out[c] = sum_g part[g*cols + c] in fp64: a block of 64 columns x 16 group
+// slices, four independent partial sums per thread so its loads overlap. (A two-level
 // variant with an arrival ticket needs a device-scope fence per block, which
 // writes back the XCD's L2 and was an order of magnitude slower.)
-template <typename A, typename W>
-__global__ __launch_bounds__(1024) void reduce_partial_kernel(W* __restrict__ out, const A* __restrict__ part,
+template <typename W>
+__global__ __launch_bounds__(1024) void reduce_partial_kernel(W* __restrict__ out, const float* __restrict__ part,
                                                               int64_t groups, int cols) {
+  using A = double;
   __shared__ A red[16][65];
   const int c = threadIdx.x % 64, s = threadIdx.x / 64;
   const int col = blockIdx.x * 64 + c;
@@ -387,7 +388,6 @@ struct BwdPlan {
   int64_t rpg;        // rows per group
   int64_t grid;       // blocks
   bool atomic;
-  int acc_bytes;      // 4 (fp32 accumulators) or 8 (fp64)
   size_t total;
 };
 
@@ -395,7 +395,6 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   if (!choose_geom(cols, es, vec_ok, &p->g)) return false;
   const int64_t ncu = cu > 0 ? cu : 256;
   p->atomic = dw_mode == HK_DW_ATOMIC || (dw_mode == HK_DW_AUTO && rows <= 8 * ncu);
-  p->acc_bytes = es == 4 ? 8 : 4;
   // about two row groups per CU: long runs of rows keep the accumulator rows
   // (partials or atomics) few; more groups were not faster
   const int64_t target = (p->atomic ? 1 : 2) * ncu * p->g.rpb;
@@ -404,7 +403,7 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   p->groups = rows > 0 ? cdiv(rows, p->rpg) : 1;
   p->grid = cdiv(p->groups, (int64_t)p->g.rpb);
   p->groups = p->grid * p->g.rpb;  // every launched group owns an accumulator row
-  p->total = p->atomic ? (size_t)cols * 8 : (size_t)p->groups * cols * p->acc_bytes;
+  p->total = p->atomic ? (size_t)cols * 8 : (size_t)p->groups * cols * sizeof(float);
   return true;
 }
 
@@ -473,8 +472,8 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
       return check_launch("cast_f64_kernel");
     }
     // (no rows: zero groups are summed and dW comes out zero)
-    hipLaunchKernelGGL((reduce_partial_kernel<A, W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
-                       (const A*)part, rows > 0 ? p.groups : 0, (int)cols);
+    hipLaunchKernelGGL((reduce_partial_kernel<W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
+                       (const float*)part, rows > 0 ? p.groups : 0, (int)cols);
     return check_launch("reduce_partial_kernel");
   });
 }

@@ -31,6 +31,10 @@
 // Workgroups are renumbered so each of the 8 XCDs walks a contiguous band of
 // output tiles (grouped by GROUP_M rows of tiles), keeping the shared A/B
 // panels in that XCD's L2.
+//
+// gemm_nt_kernel takes any layout and K; gemm_kk_kernel is the same pipeline
+// specialised for two K-contiguous operands with K % 64 == 0, and launch()
+// picks it whenever the call qualifies.
 #pragma once
 
 #include "hk_common.h"
@@ -208,7 +212,7 @@ struct Operand {
 #pragma unroll
       for (int i = 0; i < I; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * 512, 16,
-                                                 key[i] < lim ? voff[i] : kOobOffset, k0 * sizeof(T), 0, 0);
+                                                 key[i] < lim ? voff[i] : kOobOffset, k0 * (int)sizeof(T), 0, 0);
     } else {
       // from the stage's first k-row to the matrix's last element
       const int64_t span = live ? ((int64_t)(K - k0 - 1) * ld + (rows_valid > 0 ? rows_valid : 0)) * sizeof(T) : 0;
@@ -265,16 +269,92 @@ struct Operand {
 // and is called once per 16-byte chunk of a row: v holds 16/sizeof(Stage)
 // consecutive columns starting at col, of which the first n are inside the
 // matrix (n is the full chunk unless the chunk straddles column N).
+//
+// The accumulators go through LDS one wave row (WTM rows x BN columns) at a
+// time and are read back as 16-byte row chunks, so global stores (and the
+// read-modify-write of an fp32 accumulator) are full, coalesced 16-byte
+// accesses; all loads of a batch of chunks are issued before its stores.
+// acc[i][j] holds a transposed 32x32 tile (the MFMA is fed B then A): element
+// e of a lane is row i*32 + lane%32, column j*32 + (e/4)*8 + (lane/32)*4 + e%4.
+// The caller has drained every load into LDS and passed a barrier.
 // ---------------------------------------------------------------------------
+template <class C, class Epi>
+constexpr int epilogue_lds_bytes() {
+  return C::WTM * (C::BN + 16 / (int)sizeof(typename Epi::Stage)) * (int)sizeof(typename Epi::Stage);
+}
+
+template <typename T, class C, class Epi>
+__device__ __forceinline__ void epilogue(const f32x16_t (&acc)[C::TM][C::TN], unsigned char* lds_raw, int m0, int n0,
+                                         const Shape& g, const Epi& epi) {
+  using S = typename Epi::Stage;
+  constexpr int EPC = 16 / sizeof(S);  // elements per 16-byte chunk
+  constexpr int LDR = C::BN + EPC;     // padded LDS row of the staged tile
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int fr = lane & 31, fk = lane >> 5;
+  auto barrier = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  S* const st = reinterpret_cast<S*>(lds_raw);
+  constexpr int CPRO = C::BN / EPC;                  // chunks per staged row
+  constexpr int PER_T = C::WTM * CPRO / C::NT;       // chunks per thread per pass
+  constexpr int BATCH = PER_T < 8 ? PER_T : 8;
+  static_assert(C::WTM * CPRO % C::NT == 0 && PER_T % BATCH == 0, "epilogue split");
+#pragma unroll 1
+  for (int p = 0; p < C::WGM; ++p) {
+    if (wm == p) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            S* dst = st + (i * 32 + fr) * LDR + wn * C::WTN + j * 32 + q * 8 + fk * 4;
+            if constexpr (sizeof(S) == 4) {
+              *reinterpret_cast<f32x4_t*>(dst) =
+                  f32x4_t{acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]};
+            } else {
+              u32x2 w;
+              w.x = pack2<S>(acc[i][j][q * 4], acc[i][j][q * 4 + 1]);
+              w.y = pack2<S>(acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+              *reinterpret_cast<u32x2*>(dst) = w;
+            }
+          }
+    }
+    barrier();
+    const int rbase = m0 + p * C::WTM;
+#pragma unroll
+    for (int b0 = 0; b0 < PER_T; b0 += BATCH) {
+      typename Epi::Prior prior[BATCH];
+      if constexpr (Epi::kReads) {
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+          const int c = (b0 + u) * C::NT + tid, r = c / CPRO, col = n0 + (c % CPRO) * EPC;
+          if (rbase + r < g.M && col < g.N) prior[u] = epi.load(rbase + r, col, min(EPC, g.N - col));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int c = (b0 + u) * C::NT + tid, r = c / CPRO, cc = c % CPRO, col = n0 + cc * EPC;
+        if (rbase + r < g.M && col < g.N) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * LDR + cc * EPC);
+          epi.store(rbase + r, col, reinterpret_cast<const S*>(&v), min(EPC, g.N - col), prior[u]);
+        }
+      }
+    }
+    if (p + 1 < C::WGM) barrier();
+  }
+}
+
 
 template <typename T, class C, bool AMN, bool BMN, class Epi>
 __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A, const T* __restrict__ B, Shape g,
                                                         Epi epi) {
-  using S = typename Epi::Stage;
-  constexpr int EPC = 16 / sizeof(S);           // elements per 16-byte chunk
-  constexpr int LDR = C::BN + EPC;              // padded LDS row of the staged tile
   constexpr int kStageBytes = C::STAGES * C::STAGE * (int)sizeof(T);
-  constexpr int kEpiBytes = C::WTM * LDR * (int)sizeof(S);
+  constexpr int kEpiBytes = epilogue_lds_bytes<C, Epi>();
   constexpr int kLdsBytes = kStageBytes > kEpiBytes ? kStageBytes : kEpiBytes;
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[kLdsBytes];
@@ -381,56 +461,197 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
   wait_vmcnt<0>();  // the dummy loads of the tail target LDS: drain them before LDS is reused
   barrier();
 
-  // ---- epilogue: one wave row (WTM rows x BN columns) at a time through LDS ----
-  S* const st = reinterpret_cast<S*>(lds_raw);
-  constexpr int CPRO = C::BN / EPC;                  // chunks per staged row
-  constexpr int PER_T = C::WTM * CPRO / C::NT;       // chunks per thread per pass
-  constexpr int BATCH = PER_T < 8 ? PER_T : 8;
-  static_assert(C::WTM * CPRO % C::NT == 0 && PER_T % BATCH == 0, "epilogue split");
-#pragma unroll 1
-  for (int p = 0; p < C::WGM; ++p) {
-    if (wm == p) {
+  epilogue<T, C>(acc, lds_raw, m0, n0, g, epi);
+}
+
+// ---------------------------------------------------------------------------
+// Both operands K-contiguous and K % BK == 0 (every FusedLinearCE GEMM): the
+// same tiles and pipeline with nothing but MFMAs, LDS reads, DMA and scalar
+// work in the K loop.
+// * LDS holds [A stage 0][A stage 1][B stage 0][B stage 1]. A fragment's LDS
+//   address is one of 16 per-lane bases (sub-step x row parity; the XOR
+//   swizzle of row R + 32 i depends on i only through its parity) plus an
+//   immediate, and the K loop is unrolled by two so the stage offset is an
+//   immediate too.
+// * No column masking: the DMA offsets are fixed per lane. An odd stage count
+//   gets one trailing all-zero stage (zero-length buffer loads).
+// * Each sub-step issues two MFMAs, then all of the next sub-step's LDS reads,
+//   then its remaining MFMAs (measured 3-4% faster than one read per MFMA).
+// ---------------------------------------------------------------------------
+template <typename T, class C, class Epi>
+__global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A, const T* __restrict__ B, Shape g,
+                                                        Epi epi) {
+  static_assert(C::STAGES == 2 && C::BK == 64, "two stages of BK = 64");
+  constexpr int kStageBytes = C::STAGES * C::STAGE * (int)sizeof(T);
+  constexpr int kEpiBytes = epilogue_lds_bytes<C, Epi>();
+  constexpr int kLdsBytes = kStageBytes > kEpiBytes ? kStageBytes : kEpiBytes;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[kLdsBytes];
+  T* const lds = reinterpret_cast<T*>(lds_raw);
+  constexpr int kABytes = C::BM * C::BK * (int)sizeof(T);  // one A stage
+  constexpr int kBBytes = C::BN * C::BK * (int)sizeof(T);
+  constexpr int kBRegion = C::STAGES * kABytes;
+  static_assert(kABytes + (C::TM - 1) * 32 * C::BK * (int)sizeof(T) < 65536 &&
+                    kBBytes + (C::TN - 1) * 32 * C::BK * (int)sizeof(T) < 65536,
+                "stage and row offsets fit the 16-bit LDS immediate");
+
+  const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
+  int tm, tn;
+  tile_of_block<C::GROUP_M>(nbm, nbn, &tm, &tn);
+  const int m0 = tm * C::BM, n0 = tn * C::BN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int fr = lane & 31, fk = lane >> 5;
+
+  f32x16_t acc[C::TM][C::TN];
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i)
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j)
+    for (int j = 0; j < C::TN; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            S* dst = st + (i * 32 + fr) * LDR + wn * C::WTN + j * 32 + q * 8 + fk * 4;
-            if constexpr (sizeof(S) == 4) {
-              *reinterpret_cast<f32x4_t*>(dst) =
-                  f32x4_t{acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]};
-            } else {
-              u32x2 w;
-              w.x = pack2<S>(acc[i][j][q * 4], acc[i][j][q * 4 + 1]);
-              w.y = pack2<S>(acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
-              *reinterpret_cast<u32x2*>(dst) = w;
-            }
-          }
-    }
-    barrier();
-    const int rbase = m0 + p * C::WTM;
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int KT = g.K / C::BK;
+
+  // Fragment (ks, row R + 32 i) of the MFMA layout: lane l reads row R + 32 i + l%32,
+  // 16-byte chunk 2 ks + l/32, stored at chunk (2 ks + l/32) ^ swz_xor(row). With R a
+  // multiple of 64, swz_xor(R + 32 i + fr) = (fr & 7) ^ (fr >> 3) ^ 4 (i & 1).
+  uint32_t abase[C::NKS][2], bbase[C::NKS][2];
+  {
+    const int sx0 = (fr & 7) ^ (fr >> 3);
 #pragma unroll
-    for (int b0 = 0; b0 < PER_T; b0 += BATCH) {
-      typename Epi::Prior prior[BATCH];
-      if constexpr (Epi::kReads) {
+    for (int ks = 0; ks < C::NKS; ++ks)
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-          const int c = (b0 + u) * C::NT + tid, r = c / CPRO, col = n0 + (c % CPRO) * EPC;
-          if (rbase + r < g.M && col < g.N) prior[u] = epi.load(rbase + r, col, min(EPC, g.N - col));
-        }
+      for (int p = 0; p < 2; ++p) {
+        const int ch = ((2 * ks + fk) ^ sx0 ^ (4 * p)) << 3;
+        abase[ks][p] = (uint32_t)(((wm * C::WTM + fr) * C::BK + ch) * (int)sizeof(T));
+        bbase[ks][p] = (uint32_t)(kBRegion + ((wn * C::WTN + fr) * C::BK + ch) * (int)sizeof(T));
+        asm volatile("" : "+v"(abase[ks][p]));  // kept in registers, not recomputed per read
+        asm volatile("" : "+v"(bbase[ks][p]));
       }
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int c = (b0 + u) * C::NT + tid, r = c / CPRO, cc = c % CPRO, col = n0 + cc * EPC;
-        if (rbase + r < g.M && col < g.N) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * LDR + cc * EPC);
-          epi.store(rbase + r, col, reinterpret_cast<const S*>(&v), min(EPC, g.N - col), prior[u]);
-        }
-      }
-    }
-    if (p + 1 < C::WGM) barrier();
   }
+  // DMA: lane offsets inside the panel (row r, chunk swizzled by r); the stage's
+  // first column goes in the scalar offset.
+  constexpr int IA = C::IA, IB = C::IB;
+  uint32_t va[IA], vb[IB];
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+    const int q = (wave * IA + i) * 64 + lane, r = q / 8;
+    va[i] = (uint32_t)(r * g.lda + (((q % 8) ^ swz_xor<C::BK>(r)) << 3)) * (uint32_t)sizeof(T);
+  }
+#pragma unroll
+  for (int i = 0; i < IB; ++i) {
+    const int q = (wave * IB + i) * 64 + lane, r = q / 8;
+    vb[i] = (uint32_t)(r * g.ldb + (((q % 8) ^ swz_xor<C::BK>(r)) << 3)) * (uint32_t)sizeof(T);
+  }
+  const T* const pa = A + (int64_t)m0 * g.lda;
+  const T* const pb = B + (int64_t)n0 * g.ldb;
+  // buffer ranges: the panel's rows inside the matrix (rows past it read zero)
+  const int nra = (int)(min(C::BM, g.M - m0) * g.lda * (int64_t)sizeof(T));
+  const int nrb = (int)(min(C::BN, g.N - n0) * g.ldb * (int64_t)sizeof(T));
+
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  auto issue = [&](auto stage_c, int kst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int st = decltype(stage_c)::value;
+    const bool live = kst < KT;  // past KT: zero-length buffers, the loads return zeros
+    const int k0b = live ? kst * C::BK * (int)sizeof(T) : 0;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pa), 0, live ? nra : 0, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pb), 0, live ? nrb : 0, kRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < IA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds + (st * kABytes) / (int)sizeof(T) + (wave * IA + i) * 512, 16,
+                                               va[i], k0b, 0, 0);
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, lds + (kBRegion + st * kBBytes) / (int)sizeof(T) + (wave * IB + i) * 512, 16, vb[i], k0b, 0, 0);
+#endif
+  };
+
+  u32x4 fa[2][C::TM], fb[2][C::TN];
+  // fragments of sub-step ks, in the order mma() consumes them
+  auto frag = [&](auto stage_c, int ks, u32x4* a, u32x4* b) {
+    constexpr int st = decltype(stage_c)::value;
+#pragma unroll
+    for (int t = 0; t < C::TM * C::TN; ++t) {
+      const int i = t / C::TN, j = t % C::TN;
+      if (j == 0)
+        a[i] = *reinterpret_cast<const u32x4*>(lds_raw + abase[ks][i & 1] +
+                                               (st * kABytes + i * 32 * C::BK * (int)sizeof(T)));
+      if (i == 0)
+        b[j] = *reinterpret_cast<const u32x4*>(lds_raw + bbase[ks][j & 1] +
+                                               (st * kBBytes + j * 32 * C::BK * (int)sizeof(T)));
+    }
+  };
+  auto mma = [&](int buf, int first, int count) {
+#pragma unroll
+    for (int t = first; t < first + count; ++t) {
+      const int i = t / C::TN, j = t % C::TN;
+      acc[i][j] = mfma32<T>(fb[buf][j], fa[buf][i], acc[i][j]);
+    }
+  };
+  auto barrier = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  constexpr int kPre = 2;  // MFMAs of a sub-step issued ahead of the next sub-step's reads
+  static_assert(C::TM * C::TN > kPre, "sub-step split");
+  // sub-steps 0 .. NKS-2 of the stage in buffer CUR
+  auto inner = [&](auto stage_c) {
+#pragma unroll
+    for (int ks = 0; ks < C::NKS - 1; ++ks) {
+      frag(stage_c, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      mma(ks & 1, 0, C::TM * C::TN);
+      __builtin_amdgcn_sched_group_barrier(0x008, kPre, 0);                 // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, C::NR, 0);                // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - kPre, 0);  // MFMA
+    }
+  };
+  constexpr int LB = (C::NKS - 1) & 1;  // register buffer of a stage's last sub-step
+  constexpr int Q = C::Q;               // MFMAs issued before the per-stage barrier
+  constexpr int R = C::TM * C::TN - Q;
+  // stage kt in buffer CUR (stage kt+1 is landing in the other one)
+  auto body = [&](auto cur_c, int kt) {
+    using NX = std::integral_constant<int, decltype(cur_c)::value ^ 1>;
+    inner(cur_c);
+    mma(LB, 0, Q);
+    wait_vmcnt<0>();  // this wave's loads of stage kt+1
+    barrier();        // every wave's loads landed, every wave done reading stage kt
+    frag(NX{}, 0, fa[0], fb[0]);
+    issue(cur_c, kt + 2);
+    mma(LB, Q, R);
+#pragma unroll
+    for (int t = 0; t < C::NR + C::NI || t < R; ++t) {
+      if (t < C::NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);             // LDS read
+      else if (t < C::NR + C::NI) __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
+      if (t < R) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                   // MFMA
+    }
+  };
+
+  issue(S0{}, 0);
+  issue(S1{}, 1);
+  wait_vmcnt<C::NI>();  // stage 0
+  barrier();
+  frag(S0{}, 0, fa[0], fb[0]);
+  const int KT2 = KT + (KT & 1);
+  // Straight-line body: no branch may split the MFMA chain, or the compiler
+  // permutes the accumulators across the back-edge.
+  for (int kt = 0; kt + 2 < KT2; kt += 2) {
+    body(S0{}, kt);
+    body(S1{}, kt + 1);
+  }
+  body(S0{}, KT2 - 2);
+  inner(S1{});
+  mma(LB, 0, C::TM * C::TN);
+  wait_vmcnt<0>();  // the trailing zero-length loads target LDS: drain them before it is reused
+  barrier();
+  epilogue<T, C>(acc, lds_raw, m0, n0, g, epi);
 }
 
 // Returns 0, or -1 with the error set for shapes the kernel does not take.
@@ -470,6 +691,12 @@ int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb
   if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
   Shape g{M, N, K, lda, ldb};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
+  if constexpr (!AMN && !BMN && C::STAGES == 2 && C::BK == 64) {
+    if (K % C::BK == 0) {
+      hipLaunchKernelGGL((gemm_kk_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);
+      return check_launch("gemm_kk_kernel");
+    }
+  }
   hipLaunchKernelGGL((gemm_nt_kernel<T, C, AMN, BMN, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g,
                      epi);
   return check_launch("gemm_nt_kernel");

@@ -297,6 +297,21 @@ def cpu_baseline(reps=3):
             "seconds_per_step": round(t, 4), "cpu_model": cpu_model}
 
 
+def copy_ceiling(work, dev, reps, flush):
+    """A device-to-device copy moving the same bytes (work/2 read, work/2 written), timed like the ops.
+
+    What a plain streaming copy reaches at that size is the practical ceiling for an HBM-bound op:
+    at a few GB per op it sits well below the 8 TB/s peak (read/write turnaround, refresh).
+    """
+    n = (work // 2 + 4095) // 4096 * 4096
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = statistics.median(time_events(lambda: dst.copy_(src), reps, flush))
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * n / (ms * 1e-3) / 1e9
+
+
 def load_traffic(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -396,6 +411,13 @@ def main(argv=None):
                              ("fused_linear_cross_entropy", bench_c5)):
                 ops[name] = fn(K, dev, max(3, args.op_reps // 2), flush)
                 torch.cuda.empty_cache()
+        log("device copy of the same bytes (practical HBM ceiling per op):")
+        for name, e in ops.items():
+            if e["unit"] != "GB/s":
+                continue
+            cc = copy_ceiling(e["work"], dev, max(3, args.op_reps // 2), flush)
+            e["copy_same_bytes"] = {"value": round(cc, 1), "unit": "GB/s", "op_over_copy": round(e["value"] / cc, 3)}
+            log(f"  {name}: copy {cc:.0f} GB/s, op at {e['value'] / cc:.1%} of it")
         del flush
 
     del c2

@@ -186,6 +186,24 @@ def bench_c1(K, dev, reps, flush):
     return e
 
 
+def bench_geglu(K, dev, reps, flush):
+    """GeGLU (next row beyond the C1-C5 configs): bf16 [8192, 14336], the reference benchmark's Mistral-7B row
+    (benchmarks/bench_geglu.py:185-190), on the C2 SwiGLU inputs."""
+    c = workloads.c2_swiglu(device=dev)
+    a = c["a"].requires_grad_(True)
+    b = c["b"].requires_grad_(True)
+    dc = c["dc"]
+
+    def fn():
+        out = K.hilda_geglu(a, b)
+        return torch.autograd.grad([out], [a, b], [dc])
+
+    e = op_entry("geglu [8192,14336] bf16", time_events(fn, reps, flush), bytes_swiglu(*a.shape), "GB/s",
+                 HBM_PEAK_GBPS)
+    log(f"  geglu: {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
 def bench_c3(K, dev, reps, flush):
     c = workloads.c3_cross_entropy(device=dev)
     logits = c["logits"].requires_grad_(True)
@@ -404,6 +422,7 @@ def main(argv=None):
         ops.update(bench_c2_ops(c2, args.op_reps, flush))
         if args.ops == "all":
             ops["rms_norm"] = bench_c1(K, dev, args.op_reps, flush)
+            ops["geglu"] = bench_geglu(K, dev, args.op_reps, flush)
             del c2
             torch.cuda.empty_cache()
             c2 = None

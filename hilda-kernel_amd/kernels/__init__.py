@@ -9,6 +9,7 @@ with the reference.
 from .rms_norm import HildaRMSNormFunction, hilda_rms_norm, RMSNorm
 from .rope import HildaRopeFunction, hilda_rope, RotaryEmbedding
 from .swiglu import HildaSwiGLUFunction, hilda_swiglu, SwiGLU
+from .geglu import HildaGeGLUFunction, hilda_geglu, GeGLU
 from .cross_entropy import HildaCrossEntropyFunction, hilda_cross_entropy, CrossEntropyLoss
 from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
 from .fused_linear_cross_entropy import (HildaFusedLinearCrossEntropyFunction, hilda_fused_linear_cross_entropy,
@@ -19,6 +20,7 @@ __all__ = [
     "HildaRMSNormFunction", "hilda_rms_norm", "RMSNorm",
     "HildaRopeFunction", "hilda_rope", "RotaryEmbedding",
     "HildaSwiGLUFunction", "hilda_swiglu", "SwiGLU",
+    "HildaGeGLUFunction", "hilda_geglu", "GeGLU",
     "HildaCrossEntropyFunction", "hilda_cross_entropy", "CrossEntropyLoss",
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
     "HildaFusedLinearCrossEntropyFunction", "hilda_fused_linear_cross_entropy", "FusedLinearCrossEntropyLoss",

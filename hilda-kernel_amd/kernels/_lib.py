@@ -40,6 +40,8 @@ SIGNATURES = {
     "hk_rope_qk": (_i32, [_p, _p] + [_i64] * 7 + [_p, _p] + [_i64] * 7 + [_p, _p] + [_i64] * 6 + [_i32, _i32, _i32, _p]),
     "hk_swiglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
     "hk_swiglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
+    "hk_geglu_fwd": (_i32, [_p, _p, _p, _i64, _i32, _p]),
+    "hk_geglu_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
     "hk_cross_entropy_workspace_size": (_sz, [_i64]),
     "hk_cross_entropy_fwd_grad": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
     "hk_cross_entropy_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),

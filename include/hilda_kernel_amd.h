@@ -133,6 +133,20 @@ int hk_swiglu_bwd(void* da, void* db, const void* a, const void* b, const void* 
                   hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
+/* GeGLU (tanh-approximated GELU gate)                                     */
+/* ----------------------------------------------------------------------- */
+/* Replaces _geglu_fwd_kernel launch (geglu.py:131-143) on n contiguous
+ * elements: c = (gelu_tanh(a) in fp32, rounded to dtype) * b, where
+ * gelu_tanh(a) = 0.5 a (1 + tanh(sqrt(2/pi) (a + 0.044715 a^3))) (geglu.py:69-71). */
+int hk_geglu_fwd(void* c, const void* a, const void* b, int64_t n, int dtype, hk_stream_t stream);
+
+/* Replaces _geglu_bwd_kernel launch (geglu.py:146-159); writes da and db to
+ * separate buffers instead of over a and b: db = dc * gelu_tanh(a),
+ * da = dc * b * gelu_tanh'(a) (geglu.py:110-124). */
+int hk_geglu_bwd(void* da, void* db, const void* a, const void* b, const void* dc, int64_t n, int dtype,
+                 hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
 /* CrossEntropy                                                            */
 /* ----------------------------------------------------------------------- */
 /* Bytes of device workspace the CrossEntropy entry points need (n_valid). */

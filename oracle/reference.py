@@ -14,6 +14,9 @@ retyping its formula:
                           position-0 identity; norm preservation; all-ones backward
                           known answer [cos+sin, cos-sin] (benchmarks/bench_rope.py:133-146)
   swiglu_ref              x * sigmoid(x) from torch.sigmoid; a = 0 -> da = 0.5*dc*b
+  geglu_ref               odd-tanh identity gelu(x) - gelu(-x) = x; gelu(0) = 0, gelu'(0) = 1/2;
+                          within 1e-3 of the exact (erf) GELU; tails x -> x and -> 0; fp64
+                          gradcheck; a dropped cubic term or sqrt(2/pi) factor fails the erf check
   cross_entropy_ref       torch.nn.functional.cross_entropy (library); uniform logits -> log V;
                           shift invariance; brute-force python loop on tiny inputs
   selective_log_softmax_ref  brute-force python loop (log-sum-exp by hand) on tiny inputs
@@ -31,7 +34,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
-    "rope_ref", "swiglu_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
+    "rope_ref", "swiglu_ref", "geglu_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
     "linear_ce_ref", "fwd_bwd",
 ]
 
@@ -110,6 +113,14 @@ def rope_ref(q, k, cos, sin):
 def swiglu_ref(a, b):
     """benchmarks/bench_swiglu.py:46-47: F.silu(a) * b."""
     return F.silu(a) * b
+
+
+# ---------------------------------------------------------------------------
+# GeGLU
+# ---------------------------------------------------------------------------
+def geglu_ref(a, b):
+    """benchmarks/bench_geglu.py:43-44: F.gelu(a, approximate='tanh') * b (the library's tanh GELU)."""
+    return F.gelu(a, approximate="tanh") * b
 
 
 # ---------------------------------------------------------------------------

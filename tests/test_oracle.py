@@ -133,6 +133,30 @@ def test_swiglu_ref():
     assert torch.allclose(z.grad, 0.5 * dc * bb, atol=1e-14)
 
 
+# ---------------------------------------------------------------- GeGLU
+def test_geglu_ref():
+    x = torch.linspace(-12, 12, 2001, dtype=torch.float64)
+    one = torch.ones_like(x)
+    g = oracle.geglu_ref(x, one)
+    gm = oracle.geglu_ref(-x, one)
+    # tanh is odd: 0.5x(1+t) + 0.5x(1-t) = x, exactly, for any correct tanh form
+    assert torch.allclose(g - gm, x, atol=1e-13)
+    # the tanh form stays within 1e-3 of the exact GELU x * Phi(x); without the cubic
+    # term or with a wrong sqrt(2/pi) factor the gap exceeds 1e-2 near |x| = 2
+    exact = x * 0.5 * (1 + torch.erf(x / math.sqrt(2.0)))
+    assert (g - exact).abs().max() < 1e-3
+    assert torch.allclose(g[x > 8], x[x > 8], atol=1e-12) and g[x < -8].abs().max() < 1e-12
+    z = torch.zeros(3, dtype=torch.float64, requires_grad=True)
+    bb = torch.tensor([1.0, -2.0, 0.5], dtype=torch.float64)
+    c = oracle.geglu_ref(z, bb)
+    assert torch.equal(c, torch.zeros_like(c))
+    c.backward(torch.ones_like(c))
+    assert torch.allclose(z.grad, 0.5 * bb, atol=1e-15)  # gelu'(0) = 1/2
+    a = torch.randn(4, 9, generator=_g(40), dtype=torch.float64, requires_grad=True)
+    b = torch.randn(4, 9, generator=_g(41), dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(oracle.geglu_ref, (a, b))
+
+
 # ---------------------------------------------------------------- CrossEntropy
 def _ce_brute(logits, targets, ignore_index, reduction):
     losses, n_valid = [], 0

@@ -204,6 +204,45 @@ def bench_geglu(K, dev, reps, flush):
     return e
 
 
+def _logprobs(rows, V, dev, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn(rows, V, generator=g, device=dev, dtype=torch.float32)
+    return torch.log_softmax(x, -1).to(torch.bfloat16)
+
+
+def bench_kl_div(K, dev, reps, flush, rows=8192, V=128256):
+    """KLDiv (next row): bf16 [8192, 128256] log-probabilities vs probabilities, 'batchmean', fwd+bwd
+    (benchmarks/bench_kl_div.py:156-160 sizes)."""
+    yp = _logprobs(rows, V, dev, 11).requires_grad_(True)
+    yt = _logprobs(rows, V, dev, 12).float().exp().to(torch.bfloat16)
+
+    def fn():
+        loss = K.hilda_kl_div(yp, yt)
+        return torch.autograd.grad([loss], [yp])
+
+    # fwd reads y_pred and y_true; bwd reads y_true and writes dy_pred
+    e = op_entry(f"kl_div [{rows},{V}] bf16", time_events(fn, reps, flush), 4 * 2 * rows * V, "GB/s", HBM_PEAK_GBPS)
+    log(f"  kl_div: {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
+def bench_jsd(K, dev, reps, flush, rows=8192, V=128256):
+    """JSD(beta = 1/2) (next row): bf16 [8192, 128256] student and teacher log-probabilities, fwd+bwd
+    (benchmarks/bench_jsd.py sizes)."""
+    X = _logprobs(rows, V, dev, 13).requires_grad_(True)
+    Y = _logprobs(rows, V, dev, 14)
+
+    def fn():
+        loss = K.hilda_jsd(X, Y, 0.5)
+        return torch.autograd.grad([loss], [X])
+
+    # one pass reads X and Y and writes dX; a unit upstream gradient leaves dX as is
+    e = op_entry(f"jsd [{rows},{V}] bf16", time_events(fn, reps, flush), 3 * 2 * rows * V, "GB/s", HBM_PEAK_GBPS)
+    log(f"  jsd: {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
 def bench_c3(K, dev, reps, flush):
     c = workloads.c3_cross_entropy(device=dev)
     logits = c["logits"].requires_grad_(True)
@@ -427,7 +466,7 @@ def main(argv=None):
             torch.cuda.empty_cache()
             c2 = None
             for name, fn in (("cross_entropy", bench_c3), ("grpo_loss", bench_c4),
-                             ("fused_linear_cross_entropy", bench_c5)):
+                             ("fused_linear_cross_entropy", bench_c5), ("kl_div", bench_kl_div), ("jsd", bench_jsd)):
                 ops[name] = fn(K, dev, max(3, args.op_reps // 2), flush)
                 torch.cuda.empty_cache()
         log("device copy of the same bytes (practical HBM ceiling per op):")

@@ -1,0 +1,316 @@
+// KL divergence and Jensen-Shannon divergence for gfx950: one pass over each
+// row, HBM-bound, loss and gradient in the same pass where the reference does.
+//
+//   kl_div_fwd_kernel  per-row sum of t (log max(t, eps) - y), or e^t (t - y)
+//                      for log targets (kernels/kl_div.py:40-67)
+//   kl_div_bwd_kernel  dy = -t * s, or -e^t * s (kl_div.py:87-107), s per row
+//                      or scalar, read on the device
+//   jsd_kernel         per-row JSD(beta) loss / n and its gradient in X, with
+//                      ignored rows zeroed (kernels/jsd.py:30-90)
+//
+// One 256-lane block per row; each lane keeps 4 16-byte vectors per input in
+// flight, and the row sum is one block reduction.
+#include "hk_common.h"
+#include "hk_internal.h"
+#include "../../include/hilda_kernel_amd.h"
+
+#include <type_traits>
+
+namespace hk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kUnroll = 4;
+
+template <bool LOGT>
+__device__ __forceinline__ float kl_term(float y, float t, float eps) {
+  if constexpr (LOGT) return exp_fast(t) * (t - y);
+  else return t * (log_fast(fmaxf(t, eps)) - y);
+}
+
+// Visit row elements: f(width, x[], y[], first column) for VEC-wide packs
+// (all loads of a group issued first), then width-1 calls for the tail.
+template <typename T, int VEC, class F>
+__device__ __forceinline__ void row_pairs(const T* __restrict__ a, const T* __restrict__ b, int64_t cols, F&& f) {
+  const int64_t nvec = VEC > 1 ? cols / VEC : 0;
+  for (int64_t base = threadIdx.x; base < nvec; base += (int64_t)kThreads * kUnroll) {
+    Pack<T, VEC> av[kUnroll], bv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads;
+      if (i < nvec) {
+        av[u] = load_pack<T, VEC>(a + i * VEC);
+        bv[u] = load_pack<T, VEC>(b + i * VEC);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads;
+      if (i < nvec) {
+        float x[VEC], y[VEC];
+        unpack(av[u], x);
+        unpack(bv[u], y);
+        f(std::integral_constant<int, VEC>{}, x, y, i * VEC);
+      }
+    }
+  }
+  for (int64_t c = nvec * VEC + threadIdx.x; c < cols; c += kThreads) {
+    float x[VEC], y[VEC];
+    x[0] = to_f32<T>(a[c]);
+    y[0] = to_f32<T>(b[c]);
+    f(std::integral_constant<int, 1>{}, x, y, c);
+  }
+}
+
+template <typename T, int VEC, bool LOGT>
+__global__ __launch_bounds__(kThreads) void kl_div_fwd_kernel(float* __restrict__ loss_rows,
+                                                              const T* __restrict__ yp, const T* __restrict__ yt,
+                                                              int64_t cols, int64_t ldp, int64_t ldt, float eps) {
+  __shared__ float red[kWaves];
+  const int64_t row = blockIdx.x;
+  float acc = 0.f;
+  row_pairs<T, VEC>(yp + row * ldp, yt + row * ldt, cols, [&](auto wc, const float* y, const float* t, int64_t) {
+    constexpr int W = decltype(wc)::value;
+#pragma unroll
+    for (int e = 0; e < W; ++e) acc += kl_term<LOGT>(y[e], t[e], eps);
+  });
+  acc = block_sum<kWaves>(acc, red);
+  if (threadIdx.x == 0) loss_rows[row] = acc;
+}
+
+// dy[row] = -(t or e^t) * g[row or 0] * factor
+template <typename T, int VEC, bool LOGT>
+__global__ __launch_bounds__(kThreads) void kl_div_bwd_kernel(T* __restrict__ dy, const T* __restrict__ yt,
+                                                              const float* __restrict__ g, int per_row, float factor,
+                                                              int64_t cols, int64_t ldt, int64_t ldo) {
+  const int64_t row = blockIdx.x;
+  const float s = -g[per_row ? row : 0] * factor;
+  const T* t = yt + row * ldt;
+  T* o = dy + row * ldo;
+  const int64_t nvec = VEC > 1 ? cols / VEC : 0;
+  for (int64_t base = threadIdx.x; base < nvec; base += (int64_t)kThreads * kUnroll) {
+    Pack<T, VEC> tv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads;
+      if (i < nvec) tv[u] = load_pack<T, VEC>(t + i * VEC);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads;
+      if (i < nvec) {
+        float x[VEC];
+        unpack(tv[u], x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[e] = (LOGT ? exp_fast(x[e]) : x[e]) * s;
+        store_pack<T, VEC>(o + i * VEC, pack<T, VEC>(x));
+      }
+    }
+  }
+  for (int64_t c = nvec * VEC + threadIdx.x; c < cols; c += kThreads) {
+    const float x = to_f32<T>(t[c]);
+    o[c] = from_f32<T>((LOGT ? exp_fast(x) : x) * s);
+  }
+}
+
+// JSD(beta) of teacher P = e^Y and student Q = e^X, both log-probabilities:
+// MODE 0 (beta = 0): KL(P||Q) = sum P (Y - X),        dX = -P
+// MODE 1 (beta = 1): KL(Q||P) = sum Q (X - Y),        dX = Q (X - Y + 1)
+// MODE 2:            beta KL(P||M) + (1-beta) KL(Q||M), M = beta P + (1-beta) Q,
+//                    dX = (1-beta) Q (X - log M)
+// Loss and dX are divided by n = max(n_valid, 1) (all rows without labels).
+template <typename T, int VEC, int MODE>
+__global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_rows, T* __restrict__ dX,
+                                                       const T* __restrict__ X, const T* __restrict__ Y,
+                                                       const int64_t* __restrict__ labels, int64_t ignore_index,
+                                                       const int* __restrict__ n_valid, int64_t rows, float beta,
+                                                       int64_t cols, int64_t ldx, int64_t ldy, int64_t ldd) {
+  __shared__ float red[kWaves];
+  const int64_t row = blockIdx.x;
+  T* d = dX + row * ldd;
+  if (labels != nullptr && labels[row] == ignore_index) {
+    for (int64_t c = threadIdx.x; c < cols; c += kThreads) d[c] = from_f32<T>(0.f);
+    if (threadIdx.x == 0) loss_rows[row] = 0.f;
+    return;
+  }
+  const float n = labels != nullptr ? (float)max(*n_valid, 1) : (float)rows;
+  const float inv_n = 1.0f / n;
+  float acc = 0.f;
+  row_pairs<T, VEC>(X + row * ldx, Y + row * ldy, cols, [&](auto wc, const float* x, const float* y, int64_t c0) {
+    constexpr int W = decltype(wc)::value;
+    float g[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      if constexpr (MODE == 0) {
+        const float p = exp_fast(y[e]);
+        acc += p * (y[e] - x[e]);
+        g[e] = -p * inv_n;
+      } else if constexpr (MODE == 1) {
+        const float q = exp_fast(x[e]);
+        acc += q * (x[e] - y[e]);
+        g[e] = q * (x[e] - y[e] + 1.0f) * inv_n;
+      } else {
+        const float q = exp_fast(x[e]), p = exp_fast(y[e]);
+        const float lm = log_fast(beta * p + (1.0f - beta) * q);
+        acc += beta * p * (y[e] - lm) + (1.0f - beta) * q * (x[e] - lm);
+        g[e] = (1.0f - beta) * q * (x[e] - lm) * inv_n;
+      }
+    }
+    if constexpr (W == VEC && VEC > 1) {
+      store_pack<T, VEC>(d + c0, pack<T, VEC>(g));
+    } else {
+#pragma unroll
+      for (int e = 0; e < W; ++e) d[c0 + e] = from_f32<T>(g[e]);
+    }
+  });
+  acc = block_sum<kWaves>(acc, red);
+  if (threadIdx.x == 0) loss_rows[row] = acc * inv_n;
+}
+
+// out = scale * sum(v[0..n))
+__global__ __launch_bounds__(1024) void scaled_sum_kernel(float* __restrict__ out, const float* __restrict__ v,
+                                                          int64_t n, float scale) {
+  __shared__ float red[16];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += v[i];
+  s = block_sum<16>(s, red);
+  if (threadIdx.x == 0) *out = s * scale;
+}
+
+template <typename T> struct Tag { using type = T; };
+
+template <typename F>
+int dispatch_t(int dt, F&& f) {
+  switch (dt) {
+    case kF32: return f(Tag<float>{});
+    case kF16: return f(Tag<_Float16>{});
+    case kBF16: return f(Tag<__bf16>{});
+  }
+  set_error("invalid dtype code %d", dt);
+  return HK_EINVAL;
+}
+
+// VEC-wide access is possible when every row start is 16-byte aligned
+template <typename T>
+bool rows_vec_ok(const void* p, int64_t ld) {
+  return aligned_to(p, 16) && (ld * (int64_t)sizeof(T)) % 16 == 0;
+}
+
+int scaled_sum_launch(float* out, const float* v, int64_t n, float scale, hipStream_t st) {
+  hipLaunchKernelGGL(scaled_sum_kernel, dim3(1), dim3(1024), 0, st, out, v, n, scale);
+  return check_launch("scaled_sum_kernel");
+}
+
+}  // namespace
+}  // namespace hk
+
+using namespace hk;
+
+extern "C" {
+
+int hk_kl_div_fwd(float* loss_out, float* loss_rows, const void* y_pred, const void* y_true, int64_t rows,
+                  int64_t cols, int64_t ld_pred, int64_t ld_true, int log_target, float eps, int reduction, int dtype,
+                  hk_stream_t stream) {
+  HK_REQUIRE(rows >= 0 && cols >= 0 && ld_pred >= cols && ld_true >= cols, "invalid shape");
+  HK_REQUIRE(rows < (1LL << 31), "too many rows");
+  HK_REQUIRE(reduction >= HK_REDUCTION_NONE && reduction <= HK_REDUCTION_BATCHMEAN, "invalid reduction %d",
+             reduction);
+  HK_REQUIRE(rows == 0 || (loss_rows && y_pred && y_true), "null pointer argument");
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    constexpr int V = 16 / sizeof(T);
+    if (rows > 0) {
+      const bool vec = rows_vec_ok<T>(y_pred, ld_pred) && rows_vec_ok<T>(y_true, ld_true);
+      auto go = [&](auto vc, auto lc) {
+        hipLaunchKernelGGL((kl_div_fwd_kernel<T, decltype(vc)::value, decltype(lc)::value>), dim3((unsigned)rows),
+                           dim3(kThreads), 0, st, loss_rows, (const T*)y_pred, (const T*)y_true, cols, ld_pred,
+                           ld_true, eps);
+      };
+      using VV = std::integral_constant<int, V>;
+      using V1 = std::integral_constant<int, 1>;
+      using LT = std::true_type;
+      using LF = std::false_type;
+      if (vec) log_target ? go(VV{}, LT{}) : go(VV{}, LF{});
+      else log_target ? go(V1{}, LT{}) : go(V1{}, LF{});
+      const int rc = check_launch("kl_div_fwd_kernel");
+      if (rc) return rc;
+    }
+    if (loss_out == nullptr || reduction == HK_REDUCTION_NONE) return HK_OK;
+    float scale = 1.0f;  // kl_div.py:130-138
+    if (reduction == HK_REDUCTION_MEAN) scale = 1.0f / (float)((double)rows * (double)cols);
+    if (reduction == HK_REDUCTION_BATCHMEAN) scale = 1.0f / (float)rows;
+    return scaled_sum_launch(loss_out, loss_rows, rows, scale, st);
+  });
+}
+
+int hk_kl_div_bwd(void* dy_pred, const void* y_true, const float* g, int per_row, float factor, int64_t rows,
+                  int64_t cols, int64_t ld_true, int64_t ld_out, int log_target, int dtype, hk_stream_t stream) {
+  HK_REQUIRE(rows >= 0 && cols >= 0 && ld_true >= cols && ld_out >= cols, "invalid shape");
+  HK_REQUIRE(rows < (1LL << 31), "too many rows");
+  HK_REQUIRE(rows == 0 || cols == 0 || (dy_pred && y_true && g), "null pointer argument");
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    constexpr int V = 16 / sizeof(T);
+    if (rows == 0 || cols == 0) return HK_OK;
+    const bool vec = rows_vec_ok<T>(y_true, ld_true) && rows_vec_ok<T>(dy_pred, ld_out);
+    auto go = [&](auto vc, auto lc) {
+      hipLaunchKernelGGL((kl_div_bwd_kernel<T, decltype(vc)::value, decltype(lc)::value>), dim3((unsigned)rows),
+                         dim3(kThreads), 0, st, (T*)dy_pred, (const T*)y_true, g, per_row, factor, cols, ld_true,
+                         ld_out);
+    };
+    using VV = std::integral_constant<int, V>;
+    using V1 = std::integral_constant<int, 1>;
+    if (vec) log_target ? go(VV{}, std::true_type{}) : go(VV{}, std::false_type{});
+    else log_target ? go(V1{}, std::true_type{}) : go(V1{}, std::false_type{});
+    return check_launch("kl_div_bwd_kernel");
+  });
+}
+
+size_t hk_jsd_workspace_size(void) { return 256; }
+
+int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const void* Y, const int64_t* labels,
+               int64_t ignore_index, float beta, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ld_dx,
+               int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+  HK_REQUIRE(rows >= 0 && cols >= 0 && ldx >= cols && ldy >= cols && ld_dx >= cols, "invalid shape");
+  HK_REQUIRE(rows < (1LL << 31), "too many rows");
+  HK_REQUIRE(beta >= 0.f && beta <= 1.f, "beta must lie in [0, 1] (got %g)", (double)beta);
+  HK_REQUIRE(rows == 0 || (loss_rows && dX && X && Y), "null pointer argument");
+  HK_REQUIRE(labels == nullptr || (workspace && workspace_bytes >= hk_jsd_workspace_size() &&
+                                   aligned_to(workspace, 4)),
+             "labels need a workspace of hk_jsd_workspace_size() bytes");
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    constexpr int V = 16 / sizeof(T);
+    int* n_valid = labels ? (int*)workspace : nullptr;
+    if (rows > 0) {
+      if (labels) {
+        const int rc = count_valid_launch(n_valid, labels, rows, ignore_index, 1, st);
+        if (rc) return rc;
+      }
+      const bool vec = rows_vec_ok<T>(X, ldx) && rows_vec_ok<T>(Y, ldy) && rows_vec_ok<T>(dX, ld_dx);
+      const int mode = beta == 0.f ? 0 : beta == 1.f ? 1 : 2;  // the reference branches on these values (jsd.py:67-87)
+      auto go = [&](auto vc, auto mc) {
+        hipLaunchKernelGGL((jsd_kernel<T, decltype(vc)::value, decltype(mc)::value>), dim3((unsigned)rows),
+                           dim3(kThreads), 0, st, loss_rows, (T*)dX, (const T*)X, (const T*)Y, labels, ignore_index,
+                           n_valid, rows, beta, cols, ldx, ldy, ld_dx);
+      };
+      using VV = std::integral_constant<int, V>;
+      using V1 = std::integral_constant<int, 1>;
+      using M0 = std::integral_constant<int, 0>;
+      using M1 = std::integral_constant<int, 1>;
+      using M2 = std::integral_constant<int, 2>;
+      if (vec) mode == 0 ? go(VV{}, M0{}) : mode == 1 ? go(VV{}, M1{}) : go(VV{}, M2{});
+      else mode == 0 ? go(V1{}, M0{}) : mode == 1 ? go(V1{}, M1{}) : go(V1{}, M2{});
+      const int rc = check_launch("jsd_kernel");
+      if (rc) return rc;
+    }
+    if (loss_out == nullptr) return HK_OK;
+    return scaled_sum_launch(loss_out, loss_rows, rows, 1.0f, st);
+  });
+}
+
+}  // extern "C"

@@ -10,6 +10,8 @@ from .rms_norm import HildaRMSNormFunction, hilda_rms_norm, RMSNorm
 from .rope import HildaRopeFunction, hilda_rope, RotaryEmbedding
 from .swiglu import HildaSwiGLUFunction, hilda_swiglu, SwiGLU
 from .geglu import HildaGeGLUFunction, hilda_geglu, GeGLU
+from .kl_div import HildaKLDivFunction, hilda_kl_div, KLDivLoss
+from .jsd import HildaJSDFunction, hilda_jsd, JSDLoss
 from .cross_entropy import HildaCrossEntropyFunction, hilda_cross_entropy, CrossEntropyLoss
 from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
 from .fused_linear_cross_entropy import (HildaFusedLinearCrossEntropyFunction, hilda_fused_linear_cross_entropy,
@@ -21,6 +23,8 @@ __all__ = [
     "HildaRopeFunction", "hilda_rope", "RotaryEmbedding",
     "HildaSwiGLUFunction", "hilda_swiglu", "SwiGLU",
     "HildaGeGLUFunction", "hilda_geglu", "GeGLU",
+    "HildaKLDivFunction", "hilda_kl_div", "KLDivLoss",
+    "HildaJSDFunction", "hilda_jsd", "JSDLoss",
     "HildaCrossEntropyFunction", "hilda_cross_entropy", "CrossEntropyLoss",
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
     "HildaFusedLinearCrossEntropyFunction", "hilda_fused_linear_cross_entropy", "FusedLinearCrossEntropyLoss",

@@ -41,6 +41,7 @@ extern "C" {
 #define HK_REDUCTION_NONE 0
 #define HK_REDUCTION_MEAN 1
 #define HK_REDUCTION_SUM 2
+#define HK_REDUCTION_BATCHMEAN 3 /* KLDiv only: sum / rows */
 
 /* dW reduction path for the norm backward passes */
 #define HK_DW_AUTO 0    /* atomic when rows <= 8 * CU count, else partial */
@@ -145,6 +146,36 @@ int hk_geglu_fwd(void* c, const void* a, const void* b, int64_t n, int dtype, hk
  * da = dc * b * gelu_tanh'(a) (geglu.py:110-124). */
 int hk_geglu_bwd(void* da, void* db, const void* a, const void* b, const void* dc, int64_t n, int dtype,
                  hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* KL divergence and JSD                                                   */
+/* ----------------------------------------------------------------------- */
+/* Replaces _kl_div_fwd_kernel launch + reduction (kl_div.py:114-138):
+ * loss_rows[r] = sum_c t (log max(t, eps) - y), or e^t (t - y) with log_target
+ * (y = y_pred log-probabilities, t = y_true); loss_out (nullable; unused for
+ * HK_REDUCTION_NONE) = sum (SUM), sum / rows (BATCHMEAN) or
+ * sum / (rows * cols) (MEAN). Rows have element strides ld_pred / ld_true. */
+int hk_kl_div_fwd(float* loss_out, float* loss_rows, const void* y_pred, const void* y_true, int64_t rows,
+                  int64_t cols, int64_t ld_pred, int64_t ld_true, int log_target, float eps, int reduction, int dtype,
+                  hk_stream_t stream);
+
+/* Replaces kl_div_backward (kl_div.py:141-166): dy_pred = -(t or e^t) * g * factor,
+ * with g[r] per row (per_row = 1, the 'none' reduction) or g[0], read on the
+ * device (the reference's float(grad_output) host read, :147-155, is gone). */
+int hk_kl_div_bwd(void* dy_pred, const void* y_true, const float* g, int per_row, float factor, int64_t rows,
+                  int64_t cols, int64_t ld_true, int64_t ld_out, int log_target, int dtype, hk_stream_t stream);
+
+/* Bytes of device workspace hk_jsd_fwd needs when labels are given. */
+size_t hk_jsd_workspace_size(void);
+
+/* Replaces jsd_forward (jsd.py:97-135, kernel :30-90): X student and Y teacher
+ * log-probabilities; per row the JSD(beta) loss and its gradient in X, both
+ * divided by max(#labels != ignore_index, 1) (counted on the device; all rows
+ * without labels); rows whose label is ignore_index get loss 0 and dX = 0.
+ * loss_out (nullable) = sum of loss_rows. dX has X's dtype. */
+int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const void* Y, const int64_t* labels,
+               int64_t ignore_index, float beta, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ld_dx,
+               int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
 /* CrossEntropy                                                            */

@@ -17,6 +17,11 @@ retyping its formula:
   geglu_ref               odd-tanh identity gelu(x) - gelu(-x) = x; gelu(0) = 0, gelu'(0) = 1/2;
                           within 1e-3 of the exact (erf) GELU; tails x -> x and -> 0; fp64
                           gradcheck; a dropped cubic term or sqrt(2/pi) factor fails the erf check
+  kl_div_ref              torch.nn.functional.kl_div (library) for every reduction and log_target;
+                          identical distributions -> 0; Gibbs' inequality (>= 0)
+  jsd_ref                 beta = 0 and beta = 1 against torch.nn.functional.kl_div (library);
+                          beta = 1/2 symmetric and within [0, ln 2]; identical rows -> 0;
+                          brute-force python loop (masked rows) on tiny inputs; fp64 gradcheck
   cross_entropy_ref       torch.nn.functional.cross_entropy (library); uniform logits -> log V;
                           shift invariance; brute-force python loop on tiny inputs
   selective_log_softmax_ref  brute-force python loop (log-sum-exp by hand) on tiny inputs
@@ -34,7 +39,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
-    "rope_ref", "swiglu_ref", "geglu_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
+    "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
     "linear_ce_ref", "fwd_bwd",
 ]
 
@@ -121,6 +126,50 @@ def swiglu_ref(a, b):
 def geglu_ref(a, b):
     """benchmarks/bench_geglu.py:43-44: F.gelu(a, approximate='tanh') * b (the library's tanh GELU)."""
     return F.gelu(a, approximate="tanh") * b
+
+
+# ---------------------------------------------------------------------------
+# KL divergence / JSD
+# ---------------------------------------------------------------------------
+def kl_div_ref(y_pred, y_true, reduction="batchmean", log_target=False, eps=1e-10):
+    """kernels/kl_div.py:40-67 and :130-138: per-row sums of t (log max(t, eps) - y)
+    (or e^t (t - y)); 'none' returns the per-row sums, 'mean' divides by rows * cols."""
+    cols = y_pred.shape[-1]
+    yp = y_pred.reshape(-1, cols)
+    yt = y_true.reshape(-1, cols)
+    if log_target:
+        per = (torch.exp(yt) * (yt - yp)).sum(-1)
+    else:
+        per = (yt * (torch.log(torch.clamp(yt, min=eps)) - yp)).sum(-1)
+    rows = yp.shape[0]
+    if reduction == "none":
+        return per
+    if reduction == "sum":
+        return per.sum()
+    if reduction == "mean":
+        return per.sum() / (rows * cols)
+    return per.sum() / rows
+
+
+def jsd_ref(X, Y, beta=0.5, labels=None, ignore_index=-100):
+    """benchmarks/bench_jsd.py:30-44 (pytorch_jsd) with kernels/jsd.py's label masking
+    (:48-58, :113-117): the per-row JSD(beta) summed over rows whose label is not
+    ignore_index, divided by max(their count, 1) (all rows without labels)."""
+    Q = X.exp()
+    P = Y.exp()
+    if beta == 0.0:
+        per = (P * (Y - X)).sum(-1)
+    elif beta == 1.0:
+        per = (Q * (X - Y)).sum(-1)
+    else:
+        M = beta * P + (1 - beta) * Q
+        log_M = M.log()
+        per = beta * (P * (Y - log_M)).sum(-1) + (1 - beta) * (Q * (X - log_M)).sum(-1)
+    if labels is None:
+        return per.sum() / X.shape[0]
+    keep = labels != ignore_index
+    n = max(int(keep.sum()), 1)
+    return torch.where(keep, per, torch.zeros_like(per)).sum() / n
 
 
 # ---------------------------------------------------------------------------

@@ -157,6 +157,65 @@ def test_geglu_ref():
     assert torch.autograd.gradcheck(oracle.geglu_ref, (a, b))
 
 
+# ---------------------------------------------------------------- KL divergence / JSD
+def _logprobs(shape, seed):
+    return torch.log_softmax(torch.randn(*shape, generator=_g(seed), dtype=torch.float64), -1)
+
+
+@pytest.mark.filterwarnings("ignore:reduction. 'mean' divides")
+@pytest.mark.parametrize("log_target", [False, True])
+def test_kl_div_ref(log_target):
+    yp = _logprobs((6, 40), 50)
+    lt = _logprobs((6, 40), 51)
+    yt = lt if log_target else lt.exp()
+    for red in ("sum", "mean", "batchmean"):
+        exp = F.kl_div(yp, yt, reduction=red, log_target=log_target)
+        assert torch.allclose(oracle.kl_div_ref(yp, yt, red, log_target), exp, atol=1e-13), red
+    per = F.kl_div(yp, yt, reduction="none", log_target=log_target).sum(-1)
+    assert torch.allclose(oracle.kl_div_ref(yp, yt, "none", log_target), per, atol=1e-13)
+    assert (per >= 0).all()  # Gibbs' inequality
+    same = oracle.kl_div_ref(lt, yt, "none", log_target)
+    assert same.abs().max() < 1e-13
+
+
+def _jsd_brute(X, Y, beta, labels, ignore_index):
+    tot, n = 0.0, 0
+    for r in range(X.shape[0]):
+        if labels is not None and int(labels[r]) == ignore_index:
+            continue
+        n += 1
+        for c in range(X.shape[1]):
+            q, p = math.exp(float(X[r, c].detach())), math.exp(float(Y[r, c].detach()))
+            if beta == 0:  # the reference's end points are the two plain KLs (jsd.py:67-75)
+                tot += p * math.log(p / q)
+            elif beta == 1:
+                tot += q * math.log(q / p)
+            else:
+                m = beta * p + (1 - beta) * q
+                tot += beta * p * math.log(p / m) + (1 - beta) * q * math.log(q / m)
+    return tot / max(n, 1)
+
+
+def test_jsd_ref():
+    X = _logprobs((5, 12), 60).requires_grad_(True)
+    Y = _logprobs((5, 12), 61)
+    # beta = 0: KL(P||Q); beta = 1: KL(Q||P) (the library's kl_div, batchmean)
+    assert torch.allclose(oracle.jsd_ref(X, Y, 0.0), F.kl_div(X, Y, reduction="batchmean", log_target=True),
+                          atol=1e-13)
+    assert torch.allclose(oracle.jsd_ref(X, Y, 1.0), F.kl_div(Y, X, reduction="batchmean", log_target=True),
+                          atol=1e-13)
+    j = oracle.jsd_ref(X, Y, 0.5)
+    assert torch.allclose(j, oracle.jsd_ref(Y, X, 0.5), atol=1e-13)  # symmetric at beta = 1/2
+    assert 0 <= float(j.detach()) <= math.log(2)
+    assert float(oracle.jsd_ref(X, X, 0.3).detach()) < 1e-13
+    labels = torch.tensor([3, -100, 1, -100, 0])
+    for beta in (0.0, 0.25, 0.5, 1.0):
+        got = float(oracle.jsd_ref(X, Y, beta, labels).detach())
+        assert abs(got - _jsd_brute(X, Y, beta, labels, -100)) < 1e-12, beta
+    assert float(oracle.jsd_ref(X, Y, 0.5, torch.full((5,), -100)).detach()) == 0.0
+    assert torch.autograd.gradcheck(lambda x: oracle.jsd_ref(x, Y, 0.3, labels), (X,))
+
+
 # ---------------------------------------------------------------- CrossEntropy
 def _ce_brute(logits, targets, ignore_index, reduction):
     losses, n_valid = [], 0

@@ -243,6 +243,27 @@ def bench_jsd(K, dev, reps, flush, rows=8192, V=128256):
     return e
 
 
+def bench_fljsd(K, dev, reps, flush, BT=8192, H=4096, V=128256):
+    """FusedLinearJSD (next row): student and teacher hidden [8192, 4096] ~ N(0,1), lm_heads [128256, 4096]
+    ~ N(0, 0.02), beta = 1/2, bf16, fwd+bwd; in TFLOP/s of its four GEMMs, 8 BT H V."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    bf = torch.bfloat16
+    si = torch.randn(BT, H, generator=g, device=dev).to(bf).requires_grad_(True)
+    sw = (0.02 * torch.randn(V, H, generator=g, device=dev)).to(bf).requires_grad_(True)
+    ti = torch.randn(BT, H, generator=g, device=dev).to(bf)
+    tw = (0.02 * torch.randn(V, H, generator=g, device=dev)).to(bf)
+
+    def fn():
+        loss = K.hilda_fused_linear_jsd(si, sw, ti, tw)
+        return torch.autograd.grad([loss], [si, sw])
+
+    e = op_entry(f"fused_linear_jsd BT={BT} H={H} V={V} bf16", time_events(fn, reps, flush, warmup=1),
+                 8 * BT * H * V, "TFLOP/s", BF16_PEAK_TFLOPS)
+    log(f"  fused_linear_jsd: {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  ({e['frac']:.1%})")
+    return e
+
+
 def bench_c3(K, dev, reps, flush):
     c = workloads.c3_cross_entropy(device=dev)
     logits = c["logits"].requires_grad_(True)
@@ -466,7 +487,8 @@ def main(argv=None):
             torch.cuda.empty_cache()
             c2 = None
             for name, fn in (("cross_entropy", bench_c3), ("grpo_loss", bench_c4),
-                             ("fused_linear_cross_entropy", bench_c5), ("kl_div", bench_kl_div), ("jsd", bench_jsd)):
+                             ("fused_linear_cross_entropy", bench_c5), ("kl_div", bench_kl_div), ("jsd", bench_jsd),
+                             ("fused_linear_jsd", bench_fljsd)):
                 ops[name] = fn(K, dev, max(3, args.op_reps // 2), flush)
                 torch.cuda.empty_cache()
         log("device copy of the same bytes (practical HBM ceiling per op):")

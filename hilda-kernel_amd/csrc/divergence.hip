@@ -7,9 +7,13 @@
 //                      or scalar, read on the device
 //   jsd_kernel         per-row JSD(beta) loss / n and its gradient in X, with
 //                      ignored rows zeroed (kernels/jsd.py:30-90)
+//   jsd_logits_kernel  the FusedLinearJSD row step on a chunk of student and
+//                      teacher logits: temperature log-softmax of both, JSD,
+//                      and the student dlogits written over its logits
+//                      (kernels/fused_linear_jsd.py:46-108,159-199)
 //
-// One 256-lane block per row; each lane keeps 4 16-byte vectors per input in
-// flight, and the row sum is one block reduction.
+// One block per row; each lane keeps 4 16-byte vectors per input in flight,
+// and the row sums are block reductions.
 #include "hk_common.h"
 #include "hk_internal.h"
 #include "../../include/hilda_kernel_amd.h"
@@ -30,15 +34,16 @@ __device__ __forceinline__ float kl_term(float y, float t, float eps) {
 }
 
 // Visit row elements: f(width, x[], y[], first column) for VEC-wide packs
-// (all loads of a group issued first), then width-1 calls for the tail.
-template <typename T, int VEC, class F>
+// (all loads of a group issued first), then width-1 calls for the tail. NT
+// lanes share the row.
+template <typename T, int VEC, int NT = kThreads, class F>
 __device__ __forceinline__ void row_pairs(const T* __restrict__ a, const T* __restrict__ b, int64_t cols, F&& f) {
   const int64_t nvec = VEC > 1 ? cols / VEC : 0;
-  for (int64_t base = threadIdx.x; base < nvec; base += (int64_t)kThreads * kUnroll) {
+  for (int64_t base = threadIdx.x; base < nvec; base += (int64_t)NT * kUnroll) {
     Pack<T, VEC> av[kUnroll], bv[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = base + (int64_t)u * kThreads;
+      const int64_t i = base + (int64_t)u * NT;
       if (i < nvec) {
         av[u] = load_pack<T, VEC>(a + i * VEC);
         bv[u] = load_pack<T, VEC>(b + i * VEC);
@@ -46,7 +51,7 @@ __device__ __forceinline__ void row_pairs(const T* __restrict__ a, const T* __re
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = base + (int64_t)u * kThreads;
+      const int64_t i = base + (int64_t)u * NT;
       if (i < nvec) {
         float x[VEC], y[VEC];
         unpack(av[u], x);
@@ -55,7 +60,7 @@ __device__ __forceinline__ void row_pairs(const T* __restrict__ a, const T* __re
       }
     }
   }
-  for (int64_t c = nvec * VEC + threadIdx.x; c < cols; c += kThreads) {
+  for (int64_t c = nvec * VEC + threadIdx.x; c < cols; c += NT) {
     float x[VEC], y[VEC];
     x[0] = to_f32<T>(a[c]);
     y[0] = to_f32<T>(b[c]);
@@ -119,6 +124,25 @@ __global__ __launch_bounds__(kThreads) void kl_div_bwd_kernel(T* __restrict__ dy
 // MODE 1 (beta = 1): KL(Q||P) = sum Q (X - Y),        dX = Q (X - Y + 1)
 // MODE 2:            beta KL(P||M) + (1-beta) KL(Q||M), M = beta P + (1-beta) Q,
 //                    dX = (1-beta) Q (X - log M)
+// One element: adds its loss term to *acc and returns dX (unscaled).
+template <int MODE>
+__device__ __forceinline__ float jsd_elem(float x, float y, float beta, float* acc) {
+  if constexpr (MODE == 0) {
+    const float p = exp_fast(y);
+    *acc += p * (y - x);
+    return -p;
+  } else if constexpr (MODE == 1) {
+    const float q = exp_fast(x);
+    *acc += q * (x - y);
+    return q * (x - y + 1.0f);
+  } else {
+    const float q = exp_fast(x), p = exp_fast(y);
+    const float lm = log_fast(beta * p + (1.0f - beta) * q);
+    *acc += beta * p * (y - lm) + (1.0f - beta) * q * (x - lm);
+    return (1.0f - beta) * q * (x - lm);
+  }
+}
+
 // Loss and dX are divided by n = max(n_valid, 1) (all rows without labels).
 template <typename T, int VEC, int MODE>
 __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_rows, T* __restrict__ dX,
@@ -141,22 +165,7 @@ __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_
     constexpr int W = decltype(wc)::value;
     float g[W];
 #pragma unroll
-    for (int e = 0; e < W; ++e) {
-      if constexpr (MODE == 0) {
-        const float p = exp_fast(y[e]);
-        acc += p * (y[e] - x[e]);
-        g[e] = -p * inv_n;
-      } else if constexpr (MODE == 1) {
-        const float q = exp_fast(x[e]);
-        acc += q * (x[e] - y[e]);
-        g[e] = q * (x[e] - y[e] + 1.0f) * inv_n;
-      } else {
-        const float q = exp_fast(x[e]), p = exp_fast(y[e]);
-        const float lm = log_fast(beta * p + (1.0f - beta) * q);
-        acc += beta * p * (y[e] - lm) + (1.0f - beta) * q * (x[e] - lm);
-        g[e] = (1.0f - beta) * q * (x[e] - lm) * inv_n;
-      }
-    }
+    for (int e = 0; e < W; ++e) g[e] = jsd_elem<MODE>(x[e], y[e], beta, &acc) * inv_n;
     if constexpr (W == VEC && VEC > 1) {
       store_pack<T, VEC>(d + c0, pack<T, VEC>(g));
     } else {
@@ -166,6 +175,119 @@ __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_
   });
   acc = block_sum<kWaves>(acc, red);
   if (threadIdx.x == 0) loss_rows[row] = acc * inv_n;
+}
+
+// (max, sum) pair of a log-sum-exp in base 2, merged over the block: every
+// lane gets lse2 = m + log2(s). red holds 2 * NT/64 floats.
+template <int NT>
+__device__ __forceinline__ float block_lse2(float m, float s, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float om = __shfl_xor(m, o), os = __shfl_xor(s, o);
+    const float M = fmaxf(m, om);
+    s = M == -INFINITY ? 0.f : s * exp2_fast(m - M) + os * exp2_fast(om - M);
+    m = M;
+  }
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  if (lane == 0) {
+    red[2 * wave] = m;
+    red[2 * wave + 1] = s;
+  }
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) M = fmaxf(M, red[2 * i]);
+  float S = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) S += red[2 * i + 1] * exp2_fast(red[2 * i] - M);
+  __syncthreads();
+  return M + log2_fast(S);
+}
+
+constexpr int kLogitLanes = 512;
+
+// One row of student logits ls and teacher logits lt (temperature T): with
+// x = ls/T - lse(ls/T) and y = lt/T - lse(lt/T), loss_rows[r] = JSD(beta)/n
+// and, when WRITE, ls is overwritten with the student dlogits
+// (dX - e^x sum(dX)) / T, dX = dJSD/dx / n (fused_linear_jsd.py:81-108), in
+// the input dtype as the reference rounds them (:201).
+// Three passes over the two rows: the two log-sum-exps, then the loss and
+// sum(dX), then the dlogits (dX recomputed exactly as in the second pass).
+// Rows labelled ignore_index get loss 0 and zero dlogits.
+template <typename T, int VEC, int MODE, bool WRITE>
+__global__ __launch_bounds__(kLogitLanes) void jsd_logits_kernel(float* __restrict__ loss_rows, T* __restrict__ ls,
+                                                                 const T* __restrict__ lt,
+                                                                 const int64_t* __restrict__ labels,
+                                                                 int64_t ignore_index, const int* __restrict__ n_valid,
+                                                                 int64_t n_all, float beta, float inv_temp,
+                                                                 int64_t cols, int64_t ld) {
+  constexpr int NW = kLogitLanes / kWave;
+  __shared__ float red[2 * NW];
+  const int64_t row = blockIdx.x;
+  T* s = ls + row * ld;
+  const T* t = lt + row * ld;
+  if (labels != nullptr && labels[row] == ignore_index) {
+    if constexpr (WRITE)
+      for (int64_t c = threadIdx.x; c < cols; c += kLogitLanes) s[c] = from_f32<T>(0.f);
+    if (threadIdx.x == 0) loss_rows[row] = 0.f;
+    return;
+  }
+  const float inv_n = 1.0f / (labels != nullptr ? (float)max(*n_valid, 1) : (float)n_all);
+  const float c2 = inv_temp * kLog2e;
+  float ms = -INFINITY, ss = 0.f, mt = -INFINITY, st = 0.f;
+  row_pairs<T, VEC, kLogitLanes>(s, t, cols, [&](auto wc, const float* a, const float* b, int64_t) {
+    constexpr int W = decltype(wc)::value;
+    float pa = -INFINITY, pb = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      pa = fmaxf(pa, a[e] * c2);
+      pb = fmaxf(pb, b[e] * c2);
+    }
+    const float na = fmaxf(ms, pa), nb = fmaxf(mt, pb);
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      sa += exp2_fast(fmaf(a[e], c2, -na));
+      sb += exp2_fast(fmaf(b[e], c2, -nb));
+    }
+    ss = ss * exp2_fast(ms - na) + sa;
+    st = st * exp2_fast(mt - nb) + sb;
+    ms = na;
+    mt = nb;
+  });
+  // natural log-softmax: x = ls/T - lse_s
+  const float lse_s = block_lse2<kLogitLanes>(ms, ss, red) * kLn2;
+  const float lse_t = block_lse2<kLogitLanes>(mt, st, red) * kLn2;
+  float acc = 0.f, sdx = 0.f;
+  row_pairs<T, VEC, kLogitLanes>(s, t, cols, [&](auto wc, const float* a, const float* b, int64_t) {
+    constexpr int W = decltype(wc)::value;
+#pragma unroll
+    for (int e = 0; e < W; ++e)
+      sdx += jsd_elem<MODE>(fmaf(a[e], inv_temp, -lse_s), fmaf(b[e], inv_temp, -lse_t), beta, &acc);
+  });
+  acc = block_sum<NW>(acc, red);
+  if (threadIdx.x == 0) loss_rows[row] = acc * inv_n;
+  if constexpr (WRITE) {
+    sdx = block_sum<NW>(sdx, red);
+    row_pairs<T, VEC, kLogitLanes>(s, t, cols, [&](auto wc, const float* a, const float* b, int64_t c0) {
+      constexpr int W = decltype(wc)::value;
+      float o[W];
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        float dummy = 0.f;
+        const float x = fmaf(a[e], inv_temp, -lse_s);
+        const float dx = jsd_elem<MODE>(x, fmaf(b[e], inv_temp, -lse_t), beta, &dummy);
+        o[e] = (dx - exp_fast(x) * sdx) * inv_n * inv_temp;
+      }
+      if constexpr (W == VEC && VEC > 1) {
+        store_pack<T, VEC>(s + c0, pack<T, VEC>(o));
+      } else {
+#pragma unroll
+        for (int e = 0; e < W; ++e) s[c0 + e] = from_f32<T>(o[e]);
+      }
+    });
+  }
 }
 
 // out = scale * sum(v[0..n))
@@ -203,6 +325,40 @@ int scaled_sum_launch(float* out, const float* v, int64_t n, float scale, hipStr
 }
 
 }  // namespace
+
+int jsd_logits_launch(float* loss_rows, void* ls, const void* lt, const int64_t* labels, int64_t ignore_index,
+                      const int* n_valid, int64_t n_all, float beta, float temperature, int64_t rows, int64_t cols,
+                      int64_t ld, int write, int dtype, hipStream_t st) {
+  if (rows == 0) return HK_OK;
+  return dispatch_t(dtype, [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    constexpr int V = 16 / sizeof(T);
+    const bool vec = rows_vec_ok<T>(ls, ld) && rows_vec_ok<T>(lt, ld);
+    const int mode = beta == 0.f ? 0 : beta == 1.f ? 1 : 2;
+    auto go = [&](auto vc, auto mc, auto wc) {
+      hipLaunchKernelGGL((jsd_logits_kernel<T, decltype(vc)::value, decltype(mc)::value, decltype(wc)::value>),
+                         dim3((unsigned)rows), dim3(kLogitLanes), 0, st, loss_rows, (T*)ls, (const T*)lt, labels,
+                         ignore_index, n_valid, n_all, beta, 1.0f / temperature, cols, ld);
+    };
+    auto by_mode = [&](auto vc, auto wc) {
+      if (mode == 0) go(vc, std::integral_constant<int, 0>{}, wc);
+      else if (mode == 1) go(vc, std::integral_constant<int, 1>{}, wc);
+      else go(vc, std::integral_constant<int, 2>{}, wc);
+    };
+    auto by_write = [&](auto vc) {
+      if (write) by_mode(vc, std::true_type{});
+      else by_mode(vc, std::false_type{});
+    };
+    if (vec) by_write(std::integral_constant<int, V>{});
+    else by_write(std::integral_constant<int, 1>{});
+    return check_launch("jsd_logits_kernel");
+  });
+}
+
+int scaled_sum_rows_launch(float* out, const float* v, int64_t n, float scale, hipStream_t st) {
+  return scaled_sum_launch(out, v, n, scale, st);
+}
+
 }  // namespace hk
 
 using namespace hk;

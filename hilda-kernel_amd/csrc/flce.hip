@@ -1,6 +1,6 @@
-// FusedLinearCrossEntropy for gfx950: lm_head GEMMs on bf16/fp16 MFMA with the
-// cross-entropy gradient produced chunk by chunk, so the full (BT, V) logits
-// never exist.
+// FusedLinearCrossEntropy and FusedLinearJSD for gfx950: lm_head GEMMs on
+// bf16/fp16 MFMA with the loss gradient produced chunk by chunk, so the full
+// (BT, V) logits never exist.
 //
 // Every contraction is one "NT" GEMM (gemm_nt.h), C[M,N] = A[M,K] * B[N,K]^T
 // with both operands K-contiguous, the layout the MFMA operand fetch wants:
@@ -177,6 +177,32 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
   return L;
 }
 
+struct FljsdLayout {
+  size_t nvalid, rows, ls, lt, wt, xt, dt, dwacc, total;
+};
+
+FljsdLayout fljsd_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad) {
+  FljsdLayout L{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  L.nvalid = take(256);
+  L.rows = take((size_t)std::max<int64_t>(BT, 1) * 4);
+  L.ls = take((size_t)chunk * V * es);
+  L.lt = take((size_t)chunk * V * es);
+  if (grad) {
+    L.wt = take((size_t)H * V * es);
+    L.xt = take((size_t)H * pad8(BT) * es);
+    L.dt = take((size_t)V * pad8(chunk) * es);
+    L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
+  }
+  L.total = off;
+  return L;
+}
+
 // Rows per chunk: a multiple of 8 (chunk starts stay 16-byte aligned in X^T), at most BT.
 int64_t flce_chunk(int64_t BT, int64_t chunk) {
   if (chunk <= 0) chunk = 8192;
@@ -290,6 +316,108 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
       return sum_rows_launch(loss_out, loss_rows, BT, divide ? n_valid : nullptr, divide, st);
     }
     return HK_OK;
+  };
+  if (dtype == HK_BF16) return run(Tag<__bf16>{});
+  return run(Tag<_Float16>{});
+}
+
+
+size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype, int with_grad) {
+  if (BT < 0 || H <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
+  return fljsd_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0).total;
+}
+
+int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
+                        const void* t_input, const void* t_weight, const int64_t* labels, int64_t BT, int64_t H,
+                        int64_t Ht, int64_t V, int64_t ignore_index, float beta, float temperature, int dtype,
+                        int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+  HK_REQUIRE(dtype == HK_BF16 || dtype == HK_F16, "fused linear JSD supports bf16 and fp16 (got %d)", dtype);
+  HK_REQUIRE(BT >= 0 && H > 0 && Ht > 0 && V > 0, "invalid shape BT=%lld H=%lld Ht=%lld V=%lld", (long long)BT,
+             (long long)H, (long long)Ht, (long long)V);
+  HK_REQUIRE(H % 8 == 0 && Ht % 8 == 0 && V % 8 == 0, "H, Ht and V must be multiples of 8 (16-byte rows)");
+  HK_REQUIRE(BT < (1LL << 31) && H < (1LL << 31) && Ht < (1LL << 31) && V < (1LL << 31) - 4096,
+             "dimension too large");
+  HK_REQUIRE(beta >= 0.f && beta <= 1.f, "beta must lie in [0, 1] (got %g)", (double)beta);
+  HK_REQUIRE(temperature > 0.f, "temperature must be positive (got %g)", (double)temperature);
+  const bool grad = dinput != nullptr || dweight != nullptr;
+  HK_REQUIRE(!grad || (dinput && dweight), "dinput and dweight are computed together");
+  HK_REQUIRE(loss_out && s_input && s_weight && t_input && t_weight, "null pointer argument");
+  HK_REQUIRE(aligned_to(s_input, 16) && aligned_to(s_weight, 16) && aligned_to(t_input, 16) &&
+                 aligned_to(t_weight, 16) && (!grad || (aligned_to(dinput, 16) && aligned_to(dweight, 16))),
+             "inputs, weights and gradients must be 16-byte aligned");
+  const int64_t C = flce_chunk(BT, chunk);
+  const FljsdLayout lay = fljsd_layout(BT, H, V, C, 2, grad);
+  HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
+             workspace_bytes);
+  HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  int* n_valid = (int*)(ws + lay.nvalid);
+  float* loss_rows = (float*)(ws + lay.rows);
+  const int64_t BTp = pad8(BT);
+
+  auto run = [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    const T* Xs = (const T*)s_input;
+    const T* Ws = (const T*)s_weight;
+    const T* Xt_in = (const T*)t_input;
+    const T* Wt_in = (const T*)t_weight;
+    T* Ls = (T*)(ws + lay.ls);
+    T* Lt = (T*)(ws + lay.lt);
+    int rc = HK_OK;
+    // n counts the labels that are not ignore_index over all BT rows (fused_linear_jsd.py:137-141)
+    if (labels && BT > 0) rc = count_valid_launch(n_valid, labels, BT, ignore_index, 1, st);
+    if (rc) return rc;
+    T* WsT = grad ? (T*)(ws + lay.wt) : nullptr;
+    T* XsT = grad ? (T*)(ws + lay.xt) : nullptr;
+    T* Dt = grad ? (T*)(ws + lay.dt) : nullptr;
+    float* dwacc = (grad && lay.dwacc) ? (float*)(ws + lay.dwacc) : nullptr;
+    if (grad) {
+      rc = launch_transpose<T>(WsT, Ws, V, V, H, H, V, st);  // Ws^T [H, V]
+      if (rc) return rc;
+      rc = launch_transpose<T>(XsT, Xs, BT, BTp, H, H, BTp, st);  // Xs^T [H, BTp], zero padded
+      if (rc) return rc;
+    }
+    const int64_t nchunks = BT > 0 ? cdiv(BT, C) : 0;
+    for (int64_t ci = 0; ci < nchunks; ++ci) {
+      const int64_t r0 = ci * C;
+      const int64_t cs = std::min<int64_t>(C, BT - r0);
+      // student and teacher logits of the chunk (fused_linear_jsd.py:159-160)
+      rc = launch_gemm<T>(Xs + r0 * H, Ws, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Ls, V}, st);
+      if (rc) return rc;
+      rc = launch_gemm<T>(Xt_in + r0 * Ht, Wt_in, (int)cs, (int)V, (int)Ht, Ht, Ht, EpiStore<T>{Lt, V}, st);
+      if (rc) return rc;
+      // log-softmaxes, JSD and, with gradients, the student dlogits over Ls (:163-199)
+      rc = jsd_logits_launch(loss_rows + r0, Ls, Lt, labels ? labels + r0 : nullptr, ignore_index, n_valid, BT, beta,
+                             temperature, cs, V, V, grad ? 1 : 0, dtype, st);
+      if (rc) return rc;
+      if (!grad) continue;
+      // dX_c = D_c Ws (:201-202)
+      rc = launch_gemm<T>(Ls, WsT, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{(T*)dinput + r0 * H, H}, st);
+      if (rc) return rc;
+      // dWs += D_c^T X_c (:203), accumulated in fp32 across chunks
+      const int64_t csp = pad8(cs);
+      rc = launch_transpose<T>(Dt, Ls, cs, csp, V, V, csp, st);
+      if (rc) return rc;
+      auto dw_gemm = [&](auto epi) {
+        return launch_gemm<T>(Dt, XsT + r0, (int)V, (int)H, (int)csp, csp, BTp, epi, st);
+      };
+      T* dWo = (T*)dweight;
+      if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
+      else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
+      else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
+      else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
+      if (rc) return rc;
+    }
+    if (grad && nchunks == 0) {
+      const int64_t n16 = V * H * (int64_t)sizeof(T) / 16;
+      hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n16, 256), 4096)), dim3(256), 0, st,
+                         (u32x4*)dweight, n16);
+      rc = check_launch("zero16_kernel");
+      if (rc) return rc;
+    }
+    // the rows already carry 1/n (:190)
+    return scaled_sum_rows_launch(loss_out, loss_rows, BT, 1.0f, st);
   };
   if (dtype == HK_BF16) return run(Tag<__bf16>{});
   return run(Tag<_Float16>{});

@@ -12,6 +12,7 @@ from .swiglu import HildaSwiGLUFunction, hilda_swiglu, SwiGLU
 from .geglu import HildaGeGLUFunction, hilda_geglu, GeGLU
 from .kl_div import HildaKLDivFunction, hilda_kl_div, KLDivLoss
 from .jsd import HildaJSDFunction, hilda_jsd, JSDLoss
+from .fused_linear_jsd import HildaFusedLinearJSDFunction, hilda_fused_linear_jsd, FusedLinearJSDLoss
 from .cross_entropy import HildaCrossEntropyFunction, hilda_cross_entropy, CrossEntropyLoss
 from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
 from .fused_linear_cross_entropy import (HildaFusedLinearCrossEntropyFunction, hilda_fused_linear_cross_entropy,
@@ -25,6 +26,7 @@ __all__ = [
     "HildaGeGLUFunction", "hilda_geglu", "GeGLU",
     "HildaKLDivFunction", "hilda_kl_div", "KLDivLoss",
     "HildaJSDFunction", "hilda_jsd", "JSDLoss",
+    "HildaFusedLinearJSDFunction", "hilda_fused_linear_jsd", "FusedLinearJSDLoss",
     "HildaCrossEntropyFunction", "hilda_cross_entropy", "CrossEntropyLoss",
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
     "HildaFusedLinearCrossEntropyFunction", "hilda_fused_linear_cross_entropy", "FusedLinearCrossEntropyLoss",

@@ -177,6 +177,23 @@ int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const
                int64_t ignore_index, float beta, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ld_dx,
                int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
+/* Bytes of device workspace hk_fused_linear_jsd needs (chunk <= 0: 8192). */
+size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype, int with_grad);
+
+/* Replaces fused_linear_jsd_forward (fused_linear_jsd.py:114-205): per chunk of
+ * `chunk` rows, student logits s_input[BT,H] * s_weight[V,H]^T and teacher
+ * logits t_input[BT,Ht] * t_weight[V,Ht]^T on bf16/fp16 MFMA, both
+ * temperature log-softmaxes, JSD(beta) per row divided by
+ * max(#labels != ignore_index, 1) (BT without labels), and (dinput, dweight
+ * non-null) the student dlogits contracted into dinput [BT,H] and dweight
+ * [V,H] (fp32 accumulation across chunks, rounded once). The teacher gets no
+ * gradient. *loss_out = the summed loss. Rows are contiguous, H, Ht and V
+ * multiples of 8, pointers 16-byte aligned. */
+int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
+                        const void* t_input, const void* t_weight, const int64_t* labels, int64_t BT, int64_t H,
+                        int64_t Ht, int64_t V, int64_t ignore_index, float beta, float temperature, int dtype,
+                        int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* CrossEntropy                                                            */
 /* ----------------------------------------------------------------------- */

@@ -22,6 +22,8 @@ retyping its formula:
   jsd_ref                 beta = 0 and beta = 1 against torch.nn.functional.kl_div (library);
                           beta = 1/2 symmetric and within [0, ln 2]; identical rows -> 0;
                           brute-force python loop (masked rows) on tiny inputs; fp64 gradcheck
+  fused_linear_jsd_ref    fp64 brute force (explicit dot products, log-sum-exp and JSD by hand) on
+                          tiny shapes with labels and temperature; fp64 gradcheck
   cross_entropy_ref       torch.nn.functional.cross_entropy (library); uniform logits -> log V;
                           shift invariance; brute-force python loop on tiny inputs
   selective_log_softmax_ref  brute-force python loop (log-sum-exp by hand) on tiny inputs
@@ -39,7 +41,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
-    "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
+    "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "fused_linear_jsd_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
     "linear_ce_ref", "fwd_bwd",
 ]
 
@@ -170,6 +172,16 @@ def jsd_ref(X, Y, beta=0.5, labels=None, ignore_index=-100):
     keep = labels != ignore_index
     n = max(int(keep.sum()), 1)
     return torch.where(keep, per, torch.zeros_like(per)).sum() / n
+
+
+def fused_linear_jsd_ref(s_input, s_weight, t_input, t_weight, labels=None, beta=0.5, temperature=1.0,
+                         ignore_index=-100):
+    """benchmarks/bench_fused_linear_jsd.py:30-41 (pytorch_linear_jsd: logits / T, log_softmax, JSD) with
+    jsd_ref's beta end points and label masking (kernels/fused_linear_jsd.py:137-141,180-190); the teacher
+    side is detached (:5-12)."""
+    X = torch.log_softmax((s_input @ s_weight.T) / temperature, -1)
+    Y = torch.log_softmax((t_input @ t_weight.T) / temperature, -1).detach()
+    return jsd_ref(X, Y, beta, labels, ignore_index)
 
 
 # ---------------------------------------------------------------------------

@@ -216,6 +216,32 @@ def test_jsd_ref():
     assert torch.autograd.gradcheck(lambda x: oracle.jsd_ref(x, Y, 0.3, labels), (X,))
 
 
+def test_fused_linear_jsd_ref():
+    g = _g(70)
+    BT, H, Ht, V, T = 5, 6, 4, 9, 1.7
+    si = torch.randn(BT, H, generator=g, dtype=torch.float64, requires_grad=True)
+    sw = torch.randn(V, H, generator=g, dtype=torch.float64, requires_grad=True)
+    ti = torch.randn(BT, Ht, generator=g, dtype=torch.float64)
+    tw = torch.randn(V, Ht, generator=g, dtype=torch.float64)
+    labels = torch.tensor([1, -100, 3, 0, -100])
+
+    def logprobs(inp, w):  # explicit dot products and log-sum-exp
+        out = torch.empty(inp.shape[0], w.shape[0], dtype=torch.float64)
+        for r in range(inp.shape[0]):
+            z = [sum(float(inp[r, k]) * float(w[v, k]) for k in range(inp.shape[1])) / T for v in range(w.shape[0])]
+            m = max(z)
+            lse = m + math.log(sum(math.exp(zz - m) for zz in z))
+            for v in range(w.shape[0]):
+                out[r, v] = z[v] - lse
+        return out
+
+    X, Y = logprobs(si.detach(), sw.detach()), logprobs(ti, tw)
+    for beta in (0.0, 0.4, 1.0):
+        got = float(oracle.fused_linear_jsd_ref(si, sw, ti, tw, labels, beta, T).detach())
+        assert abs(got - _jsd_brute(X, Y, beta, labels, -100)) < 1e-12, beta
+    assert torch.autograd.gradcheck(lambda a, b: oracle.fused_linear_jsd_ref(a, b, ti, tw, labels, 0.4, T), (si, sw))
+
+
 # ---------------------------------------------------------------- CrossEntropy
 def _ce_brute(logits, targets, ignore_index, reduction):
     losses, n_valid = [], 0

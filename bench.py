@@ -264,6 +264,28 @@ def bench_fljsd(K, dev, reps, flush, BT=8192, H=4096, V=128256):
     return e
 
 
+def bench_attn_res(K, dev, reps, flush, N=8, B=4, T=2048, D=4096):
+    """AttnRes (next row): N=8 blocks [4, 2048, 4096] bf16 ~ N(0,1), w_query 0.02 N(0,1), w_norm 1, fwd+bwd
+    (benchmarks/bench_attn_res.py:205-211, its bf16 row)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(31)
+    bf = torch.bfloat16
+    V = torch.randn(N, B, T, D, generator=g, device=dev).to(bf).requires_grad_(True)
+    wq = (0.02 * torch.randn(D, generator=g, device=dev)).to(bf).requires_grad_(True)
+    wn = torch.ones(D, device=dev, dtype=bf).requires_grad_(True)
+    dh = torch.randn(B, T, D, generator=g, device=dev).to(bf)
+
+    def fn():
+        h = K.hilda_attn_res(V, wq, wn)
+        return torch.autograd.grad([h], [V, wq, wn], [dh])
+
+    # fwd reads V, writes h; bwd reads dh and V, writes dV
+    e = op_entry(f"attn_res N={N} [{B},{T},{D}] bf16", time_events(fn, reps, flush), (3 * N + 2) * B * T * D * 2,
+                 "GB/s", HBM_PEAK_GBPS)
+    log(f"  attn_res: {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    return e
+
+
 def bench_c3(K, dev, reps, flush):
     c = workloads.c3_cross_entropy(device=dev)
     logits = c["logits"].requires_grad_(True)
@@ -483,6 +505,7 @@ def main(argv=None):
         if args.ops == "all":
             ops["rms_norm"] = bench_c1(K, dev, args.op_reps, flush)
             ops["geglu"] = bench_geglu(K, dev, args.op_reps, flush)
+            ops["attn_res"] = bench_attn_res(K, dev, args.op_reps, flush)
             del c2
             torch.cuda.empty_cache()
             c2 = None

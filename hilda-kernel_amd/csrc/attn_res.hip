@@ -1,0 +1,379 @@
+// AttnRes (attention over depth) for gfx950, row-wise and HBM-bound
+// (kernels/attn_res.py):
+//   k_i = round(round(v_i * rstd_i) * w_norm), rstd_i = 1/sqrt(mean(v_i^2) + eps)
+//   score_i = <w_query, k_i>,  alpha = softmax_i(score),  h = sum_i alpha_i v_i
+// over the N stacked blocks v_i of one token (attn_res.py:31-98), and the
+// analytic backward of attn_res.py:101-190: dV, with dW_query / dW_norm summed
+// over tokens.
+//
+// One 256-lane block per token. Each lane owns P 16-byte packs of the D
+// columns. The N per-block sums of a pass (sum of squares, then the scores; in
+// the backward <dh, v_i>, then <dk_i, v_i>) are reduced together: one wave
+// butterfly per value and one LDS exchange for all N; the per-block scalars
+// live in LDS, so the loops over blocks stay rolled. The forward reads V three
+// times and the backward four times per token; the token's N rows (N*D*es,
+// 64 KB at N = 8, D = 4096 bf16) stay in the caches between passes. In the backward each
+// block walks a run of tokens and keeps its dW_query / dW_norm partials in
+// registers (P*VEC columns per lane), writes one fp32 partial row per block,
+// and a column reduction adds the rows in fp64 (the reference uses fp32
+// atomics per token, attn_res.py:189-190).
+#include "hk_common.h"
+#include "../../include/hilda_kernel_amd.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace hk {
+namespace {
+
+constexpr int kMaxBlocks = 32;  // the reference's largest MAX_BLOCKS (attn_res.py:201-206)
+constexpr int kNT = 256;        // lanes per token
+constexpr int kNW = kNT / kWave;
+
+template <int VEC>
+__device__ __forceinline__ int64_t col_of(int j) {  // column of pack j of this lane
+  return ((int64_t)j * kNT + threadIdx.x) * VEC;
+}
+
+// Per-block sums over the token's lanes: each lane adds its part for block i
+// with add(i, part) (a wave reduction, then one LDS slot per wave and block);
+// finish(n, out) sums the waves into out[0..n) (LDS). Two barriers per pass,
+// whatever the block count.
+struct BlockSums {
+  float* red;  // kNW * kMaxBlocks floats of LDS
+  __device__ __forceinline__ void add(int i, float part) const {
+    part = wave_sum(part);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[(threadIdx.x / kWave) * kMaxBlocks + i] = part;
+  }
+  __device__ __forceinline__ void finish(int n, float* out) const {
+    __syncthreads();
+    if ((int)threadIdx.x < n) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < kNW; ++w) t += red[w * kMaxBlocks + threadIdx.x];
+      out[threadIdx.x] = t;
+    }
+    __syncthreads();
+  }
+};
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
+                                                           float* __restrict__ rstd_out, const T* __restrict__ V,
+                                                           const T* __restrict__ wq, const T* __restrict__ wn, int N,
+                                                           int P, int64_t ntok, int64_t D, float eps) {
+  __shared__ float red[kNW * kMaxBlocks];
+  __shared__ float rs[kMaxBlocks], al[kMaxBlocks];
+  const BlockSums bs{red};
+  const int64_t tok = blockIdx.x;
+  const int64_t bstride = ntok * D;  // elements between blocks i and i+1
+  const T* v0 = V + tok * D;
+  // pass 1: sums of squares -> rstd_i
+  for (int i = 0; i < N; ++i) {
+    float part = 0.f;
+    for (int j = 0; j < P; ++j) {
+      const int64_t c = col_of<VEC>(j);
+      if (c < D) {
+        float x[VEC];
+        unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part = fmaf(x[e], x[e], part);
+      }
+    }
+    bs.add(i, part);
+  }
+  bs.finish(N, rs);
+  if ((int)threadIdx.x < N) rs[threadIdx.x] = rsqrtf(rs[threadIdx.x] / (float)D + eps);
+  __syncthreads();
+  // pass 2: score_i = <w_query, round(round(v_i * rstd_i) * w_norm)>
+  for (int i = 0; i < N; ++i) {
+    const float r = rs[i];
+    float part = 0.f;
+    for (int j = 0; j < P; ++j) {
+      const int64_t c = col_of<VEC>(j);
+      if (c < D) {
+        float x[VEC], q[VEC], w[VEC];
+        unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+        unpack(load_pack<T, VEC>(wq + c), q);
+        unpack(load_pack<T, VEC>(wn + c), w);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part = fmaf(q[e], round_through<T>(round_through<T>(x[e] * r) * w[e]), part);
+      }
+    }
+    bs.add(i, part);
+  }
+  bs.finish(N, al);
+  // softmax over the blocks (every lane; the N scores are in LDS)
+  float m = -INFINITY;
+  for (int i = 0; i < N; ++i) m = fmaxf(m, al[i]);
+  float z = 0.f;
+  for (int i = 0; i < N; ++i) z += exp_fast(al[i] - m);
+  const float iz = 1.0f / z;
+  __syncthreads();  // every lane has read the scores
+  if ((int)threadIdx.x < N) {
+    const float a = exp_fast(al[threadIdx.x] - m) * iz;
+    al[threadIdx.x] = a;
+    alpha_out[threadIdx.x * ntok + tok] = a;
+    rstd_out[threadIdx.x * ntok + tok] = rs[threadIdx.x];
+  }
+  __syncthreads();
+  // pass 3: h = sum_i alpha_i v_i
+  for (int j = 0; j < P; ++j) {
+    const int64_t c = col_of<VEC>(j);
+    if (c < D) {
+      float h[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) h[e] = 0.f;
+      for (int i = 0; i < N; ++i) {
+        const float a = al[i];
+        float x[VEC];
+        unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) h[e] = fmaf(a, x[e], h[e]);
+      }
+      store_pack<T, VEC>(out + tok * D + c, pack<T, VEC>(h));
+    }
+  }
+}
+
+// Backward for tokens [blockIdx.x * tpb, +tpb): dV written, dW partial rows
+// part[blockIdx.x][2][D] (query, norm) in fp32. P: packs per lane (template,
+// as the dW partials of P*VEC columns stay in registers).
+template <typename T, int VEC, int P>
+__global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, float* __restrict__ part,
+                                                           const T* __restrict__ dh, const T* __restrict__ V,
+                                                           const T* __restrict__ wq, const T* __restrict__ wn,
+                                                           const float* __restrict__ alpha,
+                                                           const float* __restrict__ rstd, int N, int64_t ntok,
+                                                           int64_t D, int64_t tpb) {
+  __shared__ float red[kNW * kMaxBlocks];
+  __shared__ float da[kMaxBlocks], kv[kMaxBlocks], ds[kMaxBlocks], al[kMaxBlocks], rs[kMaxBlocks];
+  const BlockSums bs{red};
+  const int64_t bstride = ntok * D;
+  float dwq[P][VEC], dwn[P][VEC];
+#pragma unroll
+  for (int j = 0; j < P; ++j)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dwq[j][e] = dwn[j][e] = 0.f;
+  const int64_t t0 = (int64_t)blockIdx.x * tpb, t1 = min(t0 + tpb, ntok);
+  for (int64_t tok = t0; tok < t1; ++tok) {
+    const T* v0 = V + tok * D;
+    const T* g = dh + tok * D;
+    if ((int)threadIdx.x < N) {
+      al[threadIdx.x] = alpha[threadIdx.x * ntok + tok];
+      rs[threadIdx.x] = rstd[threadIdx.x * ntok + tok];
+    }
+    // d_alpha_i = <dh, v_i>
+    for (int i = 0; i < N; ++i) {
+      float p = 0.f;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int64_t c = col_of<VEC>(j);
+        if (c < D) {
+          float x[VEC], y[VEC];
+          unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+          unpack(load_pack<T, VEC>(g + c), y);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) p = fmaf(x[e], y[e], p);
+        }
+      }
+      bs.add(i, p);
+    }
+    bs.finish(N, da);
+    // softmax backward: ds_i = alpha_i (da_i - sum_j alpha_j da_j)  (attn_res.py:148-149)
+    if ((int)threadIdx.x < N) {
+      float sa = 0.f;
+      for (int i = 0; i < N; ++i) sa = fmaf(al[i], da[i], sa);
+      ds[threadIdx.x] = al[threadIdx.x] * (da[threadIdx.x] - sa);
+    }
+    __syncthreads();
+    // <dk_i, v_i> with dk_i = ds_i * w_query * w_norm
+    for (int i = 0; i < N; ++i) {
+      float p = 0.f;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int64_t c = col_of<VEC>(j);
+        if (c < D) {
+          float x[VEC], q[VEC], w[VEC];
+          unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+          unpack(load_pack<T, VEC>(wq + c), q);
+          unpack(load_pack<T, VEC>(wn + c), w);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) p = fmaf(q[e] * w[e], x[e], p);
+        }
+      }
+      bs.add(i, p * ds[i]);
+    }
+    bs.finish(N, kv);
+    // dv_i = alpha_i dh + rstd dk - rstd^3 <dk, v>/D v; dW sums (attn_res.py:151-190)
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int64_t c = col_of<VEC>(j);
+      if (c < D) {
+        float y[VEC], q[VEC], w[VEC];
+        unpack(load_pack<T, VEC>(g + c), y);
+        unpack(load_pack<T, VEC>(wq + c), q);
+        unpack(load_pack<T, VEC>(wn + c), w);
+        for (int i = 0; i < N; ++i) {
+          const float a = al[i], d = ds[i], r = rs[i];
+          const float coef = r * r * r * (kv[i] / (float)D);
+          float x[VEC];
+          unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float dk = d * q[e] * w[e];
+            const float vn = x[e] * r;
+            dwq[j][e] = fmaf(d, vn * w[e], dwq[j][e]);
+            dwn[j][e] = fmaf(d * q[e], vn, dwn[j][e]);
+            x[e] = a * y[e] + r * dk - coef * x[e];
+          }
+          store_pack<T, VEC>(dV + i * bstride + tok * D + c, pack<T, VEC>(x));
+        }
+      }
+    }
+    __syncthreads();  // the token's LDS scalars are read before the next token overwrites them
+  }
+  float* pq = part + (int64_t)blockIdx.x * 2 * D;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int64_t c = col_of<VEC>(j);
+    if (c < D) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        pq[c + e] = dwq[j][e];
+        pq[D + c + e] = dwn[j][e];
+      }
+    }
+  }
+}
+
+// out_q[c] = sum_g part[g][0][c], out_n[c] = sum_g part[g][1][c] (fp64 sums)
+template <typename W>
+__global__ __launch_bounds__(1024) void attn_res_reduce_kernel(W* __restrict__ out_q, W* __restrict__ out_n,
+                                                               const float* __restrict__ part, int64_t groups,
+                                                               int64_t D) {
+  __shared__ double red[16][65];
+  const int c = threadIdx.x % 64, s = threadIdx.x / 64;
+  const int64_t col = (int64_t)blockIdx.x * 64 + c;  // in [0, 2D)
+  double t = 0.0;
+  if (col < 2 * D) {
+    const int64_t which = col / D, cc = col % D;
+    for (int64_t g = s; g < groups; g += 16) t += part[g * 2 * D + which * D + cc];
+  }
+  red[s][c] = t;
+  __syncthreads();
+  if (s == 0 && col < 2 * D) {
+    double u = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u += red[i][c];
+    if (col < D) out_q[col] = from_f32<W>((float)u);
+    else out_n[col - D] = from_f32<W>((float)u);
+  }
+}
+
+template <typename T> struct Tag { using type = T; };
+
+template <typename F>
+int dispatch_t(int dt, F&& f) {
+  switch (dt) {
+    case kF32: return f(Tag<float>{});
+    case kF16: return f(Tag<_Float16>{});
+    case kBF16: return f(Tag<__bf16>{});
+  }
+  set_error("invalid dtype code %d", dt);
+  return HK_EINVAL;
+}
+
+// packs per lane for D columns of T
+template <typename T>
+int packs_per_lane(int64_t D) {
+  constexpr int VEC = 16 / sizeof(T);
+  return (int)cdiv(D / VEC, kNT);
+}
+
+// f(P) with P rounded up to 2, 4 or 8 (the backward keeps P*VEC dW columns per lane)
+template <class F>
+int dispatch_p(int P, F&& f) {
+  if (P <= 2) return f(std::integral_constant<int, 2>{});
+  if (P <= 4) return f(std::integral_constant<int, 4>{});
+  return f(std::integral_constant<int, 8>{});
+}
+
+int64_t bwd_groups(int64_t ntok) {
+  const int dev = current_device();
+  const int cu = dev >= 0 ? cu_count(dev) : 256;
+  return std::max<int64_t>(1, std::min<int64_t>(ntok, (int64_t)cu * 4));
+}
+
+}  // namespace
+}  // namespace hk
+
+using namespace hk;
+
+extern "C" {
+
+int hk_attn_res_fwd(void* out, float* alpha, float* rstd, const void* V, const void* w_query, const void* w_norm,
+                    int64_t n_blocks, int64_t n_tokens, int64_t D, float eps, int dtype, hk_stream_t stream) {
+  HK_REQUIRE(n_blocks >= 1 && n_blocks <= kMaxBlocks, "AttnRes supports 1..%d blocks (got %lld)", kMaxBlocks,
+             (long long)n_blocks);
+  HK_REQUIRE(n_tokens >= 0 && D > 0 && n_tokens < (1LL << 31), "invalid shape");
+  HK_REQUIRE(n_tokens == 0 || (out && alpha && rstd && V && w_query && w_norm), "null pointer argument");
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    constexpr int VEC = 16 / sizeof(T);
+    HK_REQUIRE(D % VEC == 0 && D <= 8 * kNT * VEC, "D must be a multiple of %d and at most %d", VEC, 8 * kNT * VEC);
+    HK_REQUIRE(aligned_to(V, 16) && aligned_to(out, 16) && aligned_to(w_query, 16) && aligned_to(w_norm, 16),
+               "16-byte aligned tensors expected");
+    if (n_tokens == 0) return HK_OK;
+    const int P = packs_per_lane<T>(D);
+    hipLaunchKernelGGL((attn_res_fwd_kernel<T, VEC>), dim3((unsigned)n_tokens), dim3(kNT), 0, st, (T*)out, alpha,
+                       rstd, (const T*)V, (const T*)w_query, (const T*)w_norm, (int)n_blocks, P, n_tokens, D, eps);
+    return check_launch("attn_res_fwd_kernel");
+  });
+}
+
+size_t hk_attn_res_bwd_workspace_size(int64_t n_tokens, int64_t D) {
+  return (size_t)bwd_groups(n_tokens) * 2 * (size_t)D * 4;
+}
+
+int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, const void* V, const void* w_query,
+                    const void* w_norm, const float* alpha, const float* rstd, int64_t n_blocks, int64_t n_tokens,
+                    int64_t D, int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+  HK_REQUIRE(n_blocks >= 1 && n_blocks <= kMaxBlocks, "AttnRes supports 1..%d blocks (got %lld)", kMaxBlocks,
+             (long long)n_blocks);
+  HK_REQUIRE(n_tokens >= 0 && D > 0 && n_tokens < (1LL << 31), "invalid shape");
+  HK_REQUIRE(dw_query && dw_norm && w_query && w_norm, "null pointer argument");
+  HK_REQUIRE(n_tokens == 0 || (dV && dh && V && alpha && rstd), "null pointer argument");
+  const size_t need = hk_attn_res_bwd_workspace_size(n_tokens, D);
+  HK_REQUIRE(workspace && workspace_bytes >= need && aligned_to(workspace, 16),
+             "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  return dispatch_t(dtype, [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    constexpr int VEC = 16 / sizeof(T);
+    HK_REQUIRE(D % VEC == 0 && D <= 8 * kNT * VEC, "D must be a multiple of %d and at most %d", VEC, 8 * kNT * VEC);
+    HK_REQUIRE(aligned_to(V, 16) && aligned_to(dV, 16) && aligned_to(dh, 16) && aligned_to(w_query, 16) &&
+                   aligned_to(w_norm, 16),
+               "16-byte aligned tensors expected");
+    const int64_t groups = bwd_groups(n_tokens);
+    const int64_t tpb = n_tokens > 0 ? cdiv(n_tokens, groups) : 0;
+    const int64_t used = n_tokens > 0 ? cdiv(n_tokens, tpb) : 1;
+    float* part = (float*)workspace;
+    if (n_tokens > 0) {
+      const int rc = dispatch_p(packs_per_lane<T>(D), [&](auto pc) {
+        constexpr int PP = decltype(pc)::value;
+        hipLaunchKernelGGL((attn_res_bwd_kernel<T, VEC, PP>), dim3((unsigned)used), dim3(kNT), 0, st, (T*)dV, part,
+                           (const T*)dh, (const T*)V, (const T*)w_query, (const T*)w_norm, alpha, rstd,
+                           (int)n_blocks, n_tokens, D, tpb);
+        return check_launch("attn_res_bwd_kernel");
+      });
+      if (rc) return rc;
+    }
+    hipLaunchKernelGGL((attn_res_reduce_kernel<T>), dim3((unsigned)cdiv(2 * D, 64)), dim3(1024), 0, st,
+                       (T*)dw_query, (T*)dw_norm, (const float*)part, n_tokens > 0 ? used : 0, D);
+    return check_launch("attn_res_reduce_kernel");
+  });
+}
+
+}  // extern "C"

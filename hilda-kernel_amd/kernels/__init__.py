@@ -13,6 +13,7 @@ from .geglu import HildaGeGLUFunction, hilda_geglu, GeGLU
 from .kl_div import HildaKLDivFunction, hilda_kl_div, KLDivLoss
 from .jsd import HildaJSDFunction, hilda_jsd, JSDLoss
 from .fused_linear_jsd import HildaFusedLinearJSDFunction, hilda_fused_linear_jsd, FusedLinearJSDLoss
+from .attn_res import HildaAttnResFunction, hilda_attn_res, AttnRes
 from .cross_entropy import HildaCrossEntropyFunction, hilda_cross_entropy, CrossEntropyLoss
 from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rms_norm, FusedAddRMSNorm
 from .fused_linear_cross_entropy import (HildaFusedLinearCrossEntropyFunction, hilda_fused_linear_cross_entropy,
@@ -27,6 +28,7 @@ __all__ = [
     "HildaKLDivFunction", "hilda_kl_div", "KLDivLoss",
     "HildaJSDFunction", "hilda_jsd", "JSDLoss",
     "HildaFusedLinearJSDFunction", "hilda_fused_linear_jsd", "FusedLinearJSDLoss",
+    "HildaAttnResFunction", "hilda_attn_res", "AttnRes",
     "HildaCrossEntropyFunction", "hilda_cross_entropy", "CrossEntropyLoss",
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
     "HildaFusedLinearCrossEntropyFunction", "hilda_fused_linear_cross_entropy", "FusedLinearCrossEntropyLoss",

@@ -195,6 +195,29 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
                         int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
+/* AttnRes (attention residuals over depth)                                */
+/* ----------------------------------------------------------------------- */
+/* Replaces attn_res_forward (attn_res.py:209-257, kernel :31-98): V holds
+ * n_blocks stacked blocks [n_blocks, n_tokens, D]; per token
+ * k_i = round(round(v_i * rstd_i) * w_norm), score_i = <w_query, k_i>,
+ * alpha = softmax over blocks, out = sum_i alpha_i v_i (dtype of V).
+ * alpha and rstd are [n_blocks, n_tokens] fp32 (saved for the backward).
+ * 1 <= n_blocks <= 32; D a multiple of 16/sizeof(dtype), at most 2048 vectors of 16 bytes. */
+int hk_attn_res_fwd(void* out, float* alpha, float* rstd, const void* V, const void* w_query, const void* w_norm,
+                    int64_t n_blocks, int64_t n_tokens, int64_t D, float eps, int dtype, hk_stream_t stream);
+
+/* Bytes of device workspace hk_attn_res_bwd needs (fp32 partial rows). */
+size_t hk_attn_res_bwd_workspace_size(int64_t n_tokens, int64_t D);
+
+/* Replaces attn_res_backward (attn_res.py:260-288, kernel :101-190): dV
+ * [n_blocks, n_tokens, D] and dw_query / dw_norm [D] (dtype of the weights,
+ * summed over tokens in fp64 from per-block fp32 partials instead of fp32
+ * atomics). */
+int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, const void* V, const void* w_query,
+                    const void* w_norm, const float* alpha, const float* rstd, int64_t n_blocks, int64_t n_tokens,
+                    int64_t D, int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
 /* CrossEntropy                                                            */
 /* ----------------------------------------------------------------------- */
 /* Bytes of device workspace the CrossEntropy entry points need (n_valid). */

@@ -24,6 +24,9 @@ retyping its formula:
                           brute-force python loop (masked rows) on tiny inputs; fp64 gradcheck
   fused_linear_jsd_ref    fp64 brute force (explicit dot products, log-sum-exp and JSD by hand) on
                           tiny shapes with labels and temperature; fp64 gradcheck
+  attn_res_ref            N = 1 -> h = v exactly (alpha = 1); equal blocks -> h = v; a w_query that
+                          singles out one block (large score) -> h = that block; brute-force python
+                          loop on tiny inputs (RMSNorm, dot, softmax, weighted sum); fp64 gradcheck
   cross_entropy_ref       torch.nn.functional.cross_entropy (library); uniform logits -> log V;
                           shift invariance; brute-force python loop on tiny inputs
   selective_log_softmax_ref  brute-force python loop (log-sum-exp by hand) on tiny inputs
@@ -41,7 +44,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
-    "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "fused_linear_jsd_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
+    "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "fused_linear_jsd_ref", "attn_res_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
     "linear_ce_ref", "fwd_bwd",
 ]
 
@@ -182,6 +185,25 @@ def fused_linear_jsd_ref(s_input, s_weight, t_input, t_weight, labels=None, beta
     X = torch.log_softmax((s_input @ s_weight.T) / temperature, -1)
     Y = torch.log_softmax((t_input @ t_weight.T) / temperature, -1).detach()
     return jsd_ref(X, Y, beta, labels, ignore_index)
+
+
+# ---------------------------------------------------------------------------
+# AttnRes
+# ---------------------------------------------------------------------------
+def attn_res_ref(V, w_query, w_norm, eps=1e-6, key_dtype=None):
+    """benchmarks/bench_attn_res.py:33-50 (pytorch_attn_res): V [N, ..., D];
+    K = (V / rms(V)).to(V.dtype) * w_norm, scores <w_query, K>, softmax over N, h = sum alpha V.
+
+    key_dtype (default V.dtype) is the dtype the keys are rounded to, twice, as the
+    reference does (bench_attn_res.py:43, kernels/attn_res.py:70): pass the 16-bit
+    dtype when V has been widened for the computation."""
+    kd = V.dtype if key_dtype is None else key_dtype
+    Vf = V.float() if V.dtype in (torch.float16, torch.bfloat16) else V
+    rms = torch.sqrt(Vf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    K = ((Vf / rms).to(kd) * w_norm.to(kd)).to(Vf.dtype)
+    scores = (K * w_query.to(Vf.dtype)).sum(-1)
+    alpha = scores.softmax(dim=0)
+    return (alpha.unsqueeze(-1) * Vf).sum(0).to(V.dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -242,6 +242,37 @@ def test_fused_linear_jsd_ref():
     assert torch.autograd.gradcheck(lambda a, b: oracle.fused_linear_jsd_ref(a, b, ti, tw, labels, 0.4, T), (si, sw))
 
 
+# ---------------------------------------------------------------- AttnRes
+def test_attn_res_ref():
+    g = _g(80)
+    N, T, D, eps = 3, 4, 6, 1e-6
+    V = torch.randn(N, T, D, generator=g, dtype=torch.float64, requires_grad=True)
+    wq = torch.randn(D, generator=g, dtype=torch.float64, requires_grad=True)
+    wn = (1 + 0.1 * torch.randn(D, generator=g, dtype=torch.float64)).requires_grad_(True)
+    h = oracle.attn_res_ref(V, wq, wn, eps).detach()
+    Vd, wqd, wnd = V.detach(), wq.detach(), wn.detach()
+    for t in range(T):  # brute force: RMSNorm keys, dot, softmax over blocks, weighted sum
+        sc = []
+        for i in range(N):
+            v = [float(Vd[i, t, d]) for d in range(D)]
+            r = 1.0 / math.sqrt(sum(x * x for x in v) / D + eps)
+            sc.append(sum(float(wqd[d]) * v[d] * r * float(wnd[d]) for d in range(D)))
+        m = max(sc)
+        e = [math.exp(x - m) for x in sc]
+        a = [x / sum(e) for x in e]
+        for d in range(D):
+            assert abs(float(h[t, d]) - sum(a[i] * float(Vd[i, t, d]) for i in range(N))) < 1e-12
+    one = V[:1].detach()
+    assert torch.allclose(oracle.attn_res_ref(one, wq.detach(), wn.detach()), one[0], atol=1e-15)
+    same = V[:1].detach().expand(4, T, D)
+    assert torch.allclose(oracle.attn_res_ref(same, wq.detach(), wn.detach()), same[0], atol=1e-14)
+    # a query aligned with block 1's normalised key (and large) puts all the weight on it
+    k1 = V[1, 0].detach() / V[1, 0].detach().pow(2).mean().sqrt()
+    big = oracle.attn_res_ref(V.detach()[:, :1], 1e3 * k1 / wn.detach(), wn.detach())
+    assert torch.allclose(big[0], V[1, 0].detach(), atol=1e-9)
+    assert torch.autograd.gradcheck(lambda a, b, c: oracle.attn_res_ref(a, b, c, eps), (V, wq, wn))
+
+
 # ---------------------------------------------------------------- CrossEntropy
 def _ce_brute(logits, targets, ignore_index, reduction):
     losses, n_valid = [], 0

@@ -429,7 +429,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--ops", choices=["all", "c2", "none"], default="all")
+    ap.add_argument("--ops", default="all",
+                    help="all | c2 | none | a comma list of op names (e.g. attn_res,jsd) after the C2 ops")
     ap.add_argument("--op-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -502,17 +503,22 @@ def main(argv=None):
         flush = Flusher(dev)
         log("per-op fwd+bwd (median, cache flushed between reps):")
         ops.update(bench_c2_ops(c2, args.op_reps, flush))
-        if args.ops == "all":
-            ops["rms_norm"] = bench_c1(K, dev, args.op_reps, flush)
-            ops["geglu"] = bench_geglu(K, dev, args.op_reps, flush)
-            ops["attn_res"] = bench_attn_res(K, dev, args.op_reps, flush)
-            del c2
-            torch.cuda.empty_cache()
-            c2 = None
-            for name, fn in (("cross_entropy", bench_c3), ("grpo_loss", bench_c4),
-                             ("fused_linear_cross_entropy", bench_c5), ("kl_div", bench_kl_div), ("jsd", bench_jsd),
-                             ("fused_linear_jsd", bench_fljsd)):
-                ops[name] = fn(K, dev, max(3, args.op_reps // 2), flush)
+        # (name, bench, full reps): the large-vocabulary ops run half the reps
+        table = (("rms_norm", bench_c1, True), ("geglu", bench_geglu, True), ("attn_res", bench_attn_res, True),
+                 ("cross_entropy", bench_c3, False), ("grpo_loss", bench_c4, False),
+                 ("fused_linear_cross_entropy", bench_c5, False), ("kl_div", bench_kl_div, False),
+                 ("jsd", bench_jsd, False), ("fused_linear_jsd", bench_fljsd, False))
+        wanted = [n for n, _, _ in table] if args.ops == "all" else \
+            [] if args.ops == "c2" else args.ops.split(",")
+        unknown = set(wanted) - {n for n, _, _ in table}
+        if unknown:
+            raise SystemExit(f"unknown op(s) {sorted(unknown)}; known: {[n for n, _, _ in table]}")
+        del c2
+        torch.cuda.empty_cache()
+        c2 = None
+        for name, fn, full in table:
+            if name in wanted:
+                ops[name] = fn(K, dev, args.op_reps if full else max(3, args.op_reps // 2), flush)
                 torch.cuda.empty_cache()
         log("device copy of the same bytes (practical HBM ceiling per op):")
         for name, e in ops.items():

@@ -6,17 +6,22 @@
 // analytic backward of attn_res.py:101-190: dV, with dW_query / dW_norm summed
 // over tokens.
 //
-// One 256-lane block per token. Each lane owns P 16-byte packs of the D
-// columns. The N per-block sums of a pass (sum of squares, then the scores; in
-// the backward <dh, v_i>, then <dk_i, v_i>) are reduced together: one wave
-// butterfly per value and one LDS exchange for all N; the per-block scalars
-// live in LDS, so the loops over blocks stay rolled. The forward reads V three
-// times and the backward four times per token; the token's N rows (N*D*es,
-// 64 KB at N = 8, D = 4096 bf16) stay in the caches between passes. In the backward each
-// block walks a run of tokens and keeps its dW_query / dW_norm partials in
-// registers (P*VEC columns per lane), writes one fp32 partial row per block,
-// and a column reduction adds the rows in fp64 (the reference uses fp32
-// atomics per token, attn_res.py:189-190).
+// 256 lanes per token. Each lane owns P 16-byte packs of the D columns. The
+// N per-block sums of a pass (sum of squares, then the scores; in the
+// backward <dh, v_i>, then <dk_i, v_i>) are reduced together: one wave
+// butterfly per value and one LDS exchange for all N.
+//
+// When a token's N rows fit in registers (N <= 8 and D <= 512*VEC, or
+// N <= 16 and D <= 256*VEC; VEC = 8 for bf16/fp16, 4 for fp32) the register-resident
+// kernels read V once per direction. Otherwise the streaming kernels keep the
+// per-block scalars in LDS, so the loops over blocks stay rolled, and re-read
+// the token's rows per pass (three times forward, four times backward; the
+// N*D*es bytes stay in L2 between passes).
+//
+// In the backward each workgroup walks a run of tokens and keeps its
+// dW_query / dW_norm partials in registers (P*VEC columns per lane), writes
+// one fp32 partial row per workgroup, and a column reduction adds the rows in
+// fp64 (the reference uses fp32 atomics per token, attn_res.py:189-190).
 #include "hk_common.h"
 #include "../../include/hilda_kernel_amd.h"
 
@@ -29,6 +34,8 @@ namespace {
 constexpr int kMaxBlocks = 32;  // the reference's largest MAX_BLOCKS (attn_res.py:201-206)
 constexpr int kNT = 256;        // lanes per token
 constexpr int kNW = kNT / kWave;
+
+constexpr int kU = 4;           // blocks whose loads are in flight together
 
 template <int VEC>
 __device__ __forceinline__ int64_t col_of(int j) {  // column of pack j of this lane
@@ -68,39 +75,69 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, 
   const int64_t tok = blockIdx.x;
   const int64_t bstride = ntok * D;  // elements between blocks i and i+1
   const T* v0 = V + tok * D;
-  // pass 1: sums of squares -> rstd_i
-  for (int i = 0; i < N; ++i) {
-    float part = 0.f;
+  // pass 1: sums of squares -> rstd_i (kU blocks at a time, all their loads first)
+  for (int i0 = 0; i0 < N; i0 += kU) {
+    float part[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) part[u] = 0.f;
     for (int j = 0; j < P; ++j) {
       const int64_t c = col_of<VEC>(j);
       if (c < D) {
-        float x[VEC];
-        unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+        Pack<T, VEC> pv[kU];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) part = fmaf(x[e], x[e], part);
+        for (int u = 0; u < kU; ++u)
+          if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          if (i0 + u < N) {
+            float x[VEC];
+            unpack(pv[u], x);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) part[u] = fmaf(x[e], x[e], part[u]);
+          }
+        }
       }
     }
-    bs.add(i, part);
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (i0 + u < N) bs.add(i0 + u, part[u]);
   }
   bs.finish(N, rs);
   if ((int)threadIdx.x < N) rs[threadIdx.x] = rsqrtf(rs[threadIdx.x] / (float)D + eps);
   __syncthreads();
   // pass 2: score_i = <w_query, round(round(v_i * rstd_i) * w_norm)>
-  for (int i = 0; i < N; ++i) {
-    const float r = rs[i];
-    float part = 0.f;
+  for (int i0 = 0; i0 < N; i0 += kU) {
+    float part[kU], r[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      part[u] = 0.f;
+      r[u] = i0 + u < N ? rs[i0 + u] : 0.f;
+    }
     for (int j = 0; j < P; ++j) {
       const int64_t c = col_of<VEC>(j);
       if (c < D) {
-        float x[VEC], q[VEC], w[VEC];
-        unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+        Pack<T, VEC> pv[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+          if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
+        float q[VEC], w[VEC];
         unpack(load_pack<T, VEC>(wq + c), q);
         unpack(load_pack<T, VEC>(wn + c), w);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) part = fmaf(q[e], round_through<T>(round_through<T>(x[e] * r) * w[e]), part);
+        for (int u = 0; u < kU; ++u) {
+          if (i0 + u < N) {
+            float x[VEC];
+            unpack(pv[u], x);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+              part[u] = fmaf(q[e], round_through<T>(round_through<T>(x[e] * r[u]) * w[e]), part[u]);
+          }
+        }
       }
     }
-    bs.add(i, part);
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (i0 + u < N) bs.add(i0 + u, part[u]);
   }
   bs.finish(N, al);
   // softmax over the blocks (every lane; the N scores are in LDS)
@@ -124,12 +161,21 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, 
       float h[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) h[e] = 0.f;
-      for (int i = 0; i < N; ++i) {
-        const float a = al[i];
-        float x[VEC];
-        unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+      for (int i0 = 0; i0 < N; i0 += kU) {
+        Pack<T, VEC> pv[kU];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) h[e] = fmaf(a, x[e], h[e]);
+        for (int u = 0; u < kU; ++u)
+          if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          if (i0 + u < N) {
+            const float a = al[i0 + u];
+            float x[VEC];
+            unpack(pv[u], x);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) h[e] = fmaf(a, x[e], h[e]);
+          }
+        }
       }
       store_pack<T, VEC>(out + tok * D + c, pack<T, VEC>(h));
     }
@@ -164,20 +210,34 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, f
       rs[threadIdx.x] = rstd[threadIdx.x * ntok + tok];
     }
     // d_alpha_i = <dh, v_i>
-    for (int i = 0; i < N; ++i) {
-      float p = 0.f;
+    for (int i0 = 0; i0 < N; i0 += kU) {
+      float p[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) p[u] = 0.f;
 #pragma unroll
       for (int j = 0; j < P; ++j) {
         const int64_t c = col_of<VEC>(j);
         if (c < D) {
-          float x[VEC], y[VEC];
-          unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+          Pack<T, VEC> pv[kU];
+#pragma unroll
+          for (int u = 0; u < kU; ++u)
+            if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
+          float y[VEC];
           unpack(load_pack<T, VEC>(g + c), y);
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) p = fmaf(x[e], y[e], p);
+          for (int u = 0; u < kU; ++u) {
+            if (i0 + u < N) {
+              float x[VEC];
+              unpack(pv[u], x);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) p[u] = fmaf(x[e], y[e], p[u]);
+            }
+          }
         }
       }
-      bs.add(i, p);
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (i0 + u < N) bs.add(i0 + u, p[u]);
     }
     bs.finish(N, da);
     // softmax backward: ds_i = alpha_i (da_i - sum_j alpha_j da_j)  (attn_res.py:148-149)
@@ -188,21 +248,35 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, f
     }
     __syncthreads();
     // <dk_i, v_i> with dk_i = ds_i * w_query * w_norm
-    for (int i = 0; i < N; ++i) {
-      float p = 0.f;
+    for (int i0 = 0; i0 < N; i0 += kU) {
+      float p[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) p[u] = 0.f;
 #pragma unroll
       for (int j = 0; j < P; ++j) {
         const int64_t c = col_of<VEC>(j);
         if (c < D) {
-          float x[VEC], q[VEC], w[VEC];
-          unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+          Pack<T, VEC> pv[kU];
+#pragma unroll
+          for (int u = 0; u < kU; ++u)
+            if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
+          float q[VEC], w[VEC];
           unpack(load_pack<T, VEC>(wq + c), q);
           unpack(load_pack<T, VEC>(wn + c), w);
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) p = fmaf(q[e] * w[e], x[e], p);
+          for (int u = 0; u < kU; ++u) {
+            if (i0 + u < N) {
+              float x[VEC];
+              unpack(pv[u], x);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) p[u] = fmaf(q[e] * w[e], x[e], p[u]);
+            }
+          }
         }
       }
-      bs.add(i, p * ds[i]);
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (i0 + u < N) bs.add(i0 + u, p[u] * ds[i0 + u]);
     }
     bs.finish(N, kv);
     // dv_i = alpha_i dh + rstd dk - rstd^3 <dk, v>/D v; dW sums (attn_res.py:151-190)
@@ -214,11 +288,258 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, f
         unpack(load_pack<T, VEC>(g + c), y);
         unpack(load_pack<T, VEC>(wq + c), q);
         unpack(load_pack<T, VEC>(wn + c), w);
-        for (int i = 0; i < N; ++i) {
+        for (int i0 = 0; i0 < N; i0 += kU) {
+          Pack<T, VEC> pv[kU];
+#pragma unroll
+          for (int u = 0; u < kU; ++u)
+            if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
+#pragma unroll
+          for (int u = 0; u < kU; ++u) {
+            const int i = i0 + u;
+            if (i < N) {
+              const float a = al[i], d = ds[i], r = rs[i];
+              const float coef = r * r * r * (kv[i] / (float)D);
+              float x[VEC];
+              unpack(pv[u], x);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                const float dk = d * q[e] * w[e];
+                const float vn = x[e] * r;
+                dwq[j][e] = fmaf(d, vn * w[e], dwq[j][e]);
+                dwn[j][e] = fmaf(d * q[e], vn, dwn[j][e]);
+                x[e] = a * y[e] + r * dk - coef * x[e];
+              }
+              store_pack<T, VEC>(dV + i * bstride + tok * D + c, pack<T, VEC>(x));
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the token's LDS scalars are read before the next token overwrites them
+  }
+  float* pq = part + (int64_t)blockIdx.x * 2 * D;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int64_t c = col_of<VEC>(j);
+    if (c < D) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        pq[c + e] = dwq[j][e];
+        pq[D + c + e] = dwn[j][e];
+      }
+    }
+  }
+}
+
+// Register-resident forms, used when a token's N rows fit in NB*P packs per
+// lane (64 VGPRs at most): V is read once per direction, the passes work on
+// the registers. Same arithmetic, in the same order, as the streaming forms.
+template <typename T, int VEC, int NB, int P>
+__global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
+                                                               float* __restrict__ rstd_out, const T* __restrict__ V,
+                                                               const T* __restrict__ wq, const T* __restrict__ wn,
+                                                               int N, int64_t ntok, int64_t D, float eps) {
+  // one token per workgroup: the workgroups resident on a CU overlap one
+  // token's loads with another's reductions (measured faster than a run of
+  // tokens per workgroup with the next token's rows prefetched). The weights
+  // are loaded with the rows, so the token costs one memory round trip.
+  __shared__ float red[kNW * kMaxBlocks];
+  __shared__ float rs[kMaxBlocks], al[kMaxBlocks];
+  const BlockSums bs{red};
+  const int64_t tok = blockIdx.x;
+  const int64_t bstride = ntok * D;
+  const T* v0 = V + tok * D;
+  Pack<T, VEC> pv[NB][P], qv[P], wv[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int64_t c = col_of<VEC>(j) < D ? col_of<VEC>(j) : 0;
+    qv[j] = load_pack<T, VEC>(wq + c);
+    wv[j] = load_pack<T, VEC>(wn + c);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < P; ++j)
+      if (i < N && col_of<VEC>(j) < D) pv[i][j] = load_pack<T, VEC>(v0 + i * bstride + col_of<VEC>(j));
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if (i < N) {
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        if (col_of<VEC>(j) < D) {
+          float x[VEC];
+          unpack(pv[i][j], x);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) part = fmaf(x[e], x[e], part);
+        }
+      }
+      bs.add(i, part);
+    }
+  }
+  bs.finish(N, rs);
+  if ((int)threadIdx.x < N) rs[threadIdx.x] = rsqrtf(rs[threadIdx.x] / (float)D + eps);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if (i < N) {
+      const float r = rs[i];
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        if (col_of<VEC>(j) < D) {
+          float x[VEC], q[VEC], w[VEC];
+          unpack(pv[i][j], x);
+          unpack(qv[j], q);
+          unpack(wv[j], w);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            part = fmaf(q[e], round_through<T>(round_through<T>(x[e] * r) * w[e]), part);
+        }
+      }
+      bs.add(i, part);
+    }
+  }
+  bs.finish(N, al);
+  float m = -INFINITY;
+  for (int i = 0; i < N; ++i) m = fmaxf(m, al[i]);
+  float z = 0.f;
+  for (int i = 0; i < N; ++i) z += exp_fast(al[i] - m);
+  const float iz = 1.0f / z;
+  __syncthreads();
+  if ((int)threadIdx.x < N) {
+    const float a = exp_fast(al[threadIdx.x] - m) * iz;
+    al[threadIdx.x] = a;
+    alpha_out[threadIdx.x * ntok + tok] = a;
+    rstd_out[threadIdx.x * ntok + tok] = rs[threadIdx.x];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int64_t c = col_of<VEC>(j);
+    if (c < D) {
+      float h[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) h[e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if (i < N) {
+          const float a = al[i];
+          float x[VEC];
+          unpack(pv[i][j], x);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) h[e] = fmaf(a, x[e], h[e]);
+        }
+      }
+      store_pack<T, VEC>(out + tok * D + c, pack<T, VEC>(h));
+    }
+  }
+}
+
+template <typename T, int VEC, int NB, int P>
+__global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ dV, float* __restrict__ part,
+                                                               const T* __restrict__ dh, const T* __restrict__ V,
+                                                               const T* __restrict__ wq, const T* __restrict__ wn,
+                                                               const float* __restrict__ alpha,
+                                                               const float* __restrict__ rstd, int N, int64_t ntok,
+                                                               int64_t D, int64_t tpb) {
+  __shared__ float red[kNW * kMaxBlocks];
+  __shared__ float da[kMaxBlocks], kv[kMaxBlocks], ds[kMaxBlocks], al[kMaxBlocks], rs[kMaxBlocks];
+  const BlockSums bs{red};
+  const int64_t bstride = ntok * D;
+  Pack<T, VEC> qv[P], wv[P];
+  float dwq[P][VEC], dwn[P][VEC];
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dwq[j][e] = dwn[j][e] = 0.f;
+    const int64_t c = col_of<VEC>(j) < D ? col_of<VEC>(j) : 0;
+    qv[j] = load_pack<T, VEC>(wq + c);
+    wv[j] = load_pack<T, VEC>(wn + c);
+  }
+  const int64_t t0 = (int64_t)blockIdx.x * tpb, t1 = min(t0 + tpb, ntok);
+  // the token's rows live in pv/gv; the next token's are loaded into them as the
+  // current token's dV is stored (the last token reloads itself), so loads of
+  // one token overlap the stores and reductions of the previous one
+  Pack<T, VEC> pv[NB][P], gv[P];
+  auto load_token = [&](int64_t t, int i, int j) {
+    const int64_t c = col_of<VEC>(j) < D ? col_of<VEC>(j) : 0;  // in-bounds address; unused when >= D
+    if (i < 0) gv[j] = load_pack<T, VEC>(dh + t * D + c);
+    else pv[i][j] = load_pack<T, VEC>(V + i * bstride + t * D + c);
+  };
+  if (t0 < t1) {
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      load_token(t0, -1, j);
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        if (i < N) load_token(t0, i, j);
+    }
+  }
+  for (int64_t tok = t0; tok < t1; ++tok) {
+    const int64_t nxt = tok + 1 < t1 ? tok + 1 : tok;
+    if ((int)threadIdx.x < N) {
+      al[threadIdx.x] = alpha[threadIdx.x * ntok + tok];
+      rs[threadIdx.x] = rstd[threadIdx.x * ntok + tok];
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (i < N) {
+        float p = 0.f;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+          if (col_of<VEC>(j) < D) {
+            float x[VEC], y[VEC];
+            unpack(pv[i][j], x);
+            unpack(gv[j], y);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) p = fmaf(x[e], y[e], p);
+          }
+        }
+        bs.add(i, p);  // d_alpha_i = <dh, v_i>
+      }
+    }
+    bs.finish(N, da);
+    if ((int)threadIdx.x < N) {
+      float sa = 0.f;
+      for (int i = 0; i < N; ++i) sa = fmaf(al[i], da[i], sa);
+      ds[threadIdx.x] = al[threadIdx.x] * (da[threadIdx.x] - sa);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (i < N) {
+        float pk = 0.f;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+          if (col_of<VEC>(j) < D) {
+            float x[VEC], q[VEC], w[VEC];
+            unpack(pv[i][j], x);
+            unpack(qv[j], q);
+            unpack(wv[j], w);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) pk = fmaf(q[e] * w[e], x[e], pk);
+          }
+        }
+        bs.add(i, pk * ds[i]);
+      }
+    }
+    bs.finish(N, kv);
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int64_t c = col_of<VEC>(j);
+      float y[VEC], q[VEC], w[VEC];
+      unpack(gv[j], y);
+      unpack(qv[j], q);
+      unpack(wv[j], w);
+      load_token(nxt, -1, j);
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if (i < N) {
           const float a = al[i], d = ds[i], r = rs[i];
           const float coef = r * r * r * (kv[i] / (float)D);
           float x[VEC];
-          unpack(load_pack<T, VEC>(v0 + i * bstride + c), x);
+          unpack(pv[i][j], x);
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
             const float dk = d * q[e] * w[e];
@@ -227,11 +548,12 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, f
             dwn[j][e] = fmaf(d * q[e], vn, dwn[j][e]);
             x[e] = a * y[e] + r * dk - coef * x[e];
           }
-          store_pack<T, VEC>(dV + i * bstride + tok * D + c, pack<T, VEC>(x));
+          if (c < D) store_pack<T, VEC>(dV + i * bstride + tok * D + c, pack<T, VEC>(x));
+          load_token(nxt, i, j);
         }
       }
     }
-    __syncthreads();  // the token's LDS scalars are read before the next token overwrites them
+    __syncthreads();
   }
   float* pq = part + (int64_t)blockIdx.x * 2 * D;
 #pragma unroll
@@ -255,12 +577,19 @@ __global__ __launch_bounds__(1024) void attn_res_reduce_kernel(W* __restrict__ o
   __shared__ double red[16][65];
   const int c = threadIdx.x % 64, s = threadIdx.x / 64;
   const int64_t col = (int64_t)blockIdx.x * 64 + c;  // in [0, 2D)
-  double t = 0.0;
+  double t0 = 0.0, t1 = 0.0, t2 = 0.0, t3 = 0.0;
   if (col < 2 * D) {
-    const int64_t which = col / D, cc = col % D;
-    for (int64_t g = s; g < groups; g += 16) t += part[g * 2 * D + which * D + cc];
+    const float* pc = part + (col / D) * D + col % D;
+    int64_t g = s;
+    for (; g + 48 < groups; g += 64) {  // four independent chains
+      t0 += pc[g * 2 * D];
+      t1 += pc[(g + 16) * 2 * D];
+      t2 += pc[(g + 32) * 2 * D];
+      t3 += pc[(g + 48) * 2 * D];
+    }
+    for (; g < groups; g += 16) t0 += pc[g * 2 * D];
   }
-  red[s][c] = t;
+  red[s][c] = (t0 + t1) + (t2 + t3);
   __syncthreads();
   if (s == 0 && col < 2 * D) {
     double u = 0.0;
@@ -299,11 +628,13 @@ int dispatch_p(int P, F&& f) {
   return f(std::integral_constant<int, 8>{});
 }
 
-int64_t bwd_groups(int64_t ntok) {
+// workgroups walking runs of tokens: per_cu per CU (what the register use lets run at once)
+int64_t token_groups(int64_t ntok, int per_cu) {
   const int dev = current_device();
   const int cu = dev >= 0 ? cu_count(dev) : 256;
-  return std::max<int64_t>(1, std::min<int64_t>(ntok, (int64_t)cu * 4));
+  return std::max<int64_t>(1, std::min<int64_t>(ntok, (int64_t)cu * per_cu));
 }
+int64_t bwd_groups(int64_t ntok) { return token_groups(ntok, 2); }
 
 }  // namespace
 }  // namespace hk
@@ -327,8 +658,17 @@ int hk_attn_res_fwd(void* out, float* alpha, float* rstd, const void* V, const v
                "16-byte aligned tensors expected");
     if (n_tokens == 0) return HK_OK;
     const int P = packs_per_lane<T>(D);
+    const int N = (int)n_blocks;
+    auto resident = [&](auto nbc, auto pc) {
+      constexpr int NB = decltype(nbc)::value, PP = decltype(pc)::value;
+      hipLaunchKernelGGL((attn_res_fwd_res_kernel<T, VEC, NB, PP>), dim3((unsigned)n_tokens), dim3(kNT), 0, st,
+                         (T*)out, alpha, rstd, (const T*)V, (const T*)w_query, (const T*)w_norm, N, n_tokens, D, eps);
+      return check_launch("attn_res_fwd_res_kernel");
+    };
+    if (N <= 8 && P <= 2) return resident(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
+    if (N <= 16 && P <= 1) return resident(std::integral_constant<int, 16>{}, std::integral_constant<int, 1>{});
     hipLaunchKernelGGL((attn_res_fwd_kernel<T, VEC>), dim3((unsigned)n_tokens), dim3(kNT), 0, st, (T*)out, alpha,
-                       rstd, (const T*)V, (const T*)w_query, (const T*)w_norm, (int)n_blocks, P, n_tokens, D, eps);
+                       rstd, (const T*)V, (const T*)w_query, (const T*)w_norm, N, P, n_tokens, D, eps);
     return check_launch("attn_res_fwd_kernel");
   });
 }
@@ -360,7 +700,21 @@ int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, con
     const int64_t tpb = n_tokens > 0 ? cdiv(n_tokens, groups) : 0;
     const int64_t used = n_tokens > 0 ? cdiv(n_tokens, tpb) : 1;
     float* part = (float*)workspace;
-    if (n_tokens > 0) {
+    const int N = (int)n_blocks, Pl = packs_per_lane<T>(D);
+    auto resident = [&](auto nbc, auto pc) {
+      constexpr int NB = decltype(nbc)::value, PP = decltype(pc)::value;
+      hipLaunchKernelGGL((attn_res_bwd_res_kernel<T, VEC, NB, PP>), dim3((unsigned)used), dim3(kNT), 0, st, (T*)dV,
+                         part, (const T*)dh, (const T*)V, (const T*)w_query, (const T*)w_norm, alpha, rstd, N,
+                         n_tokens, D, tpb);
+      return check_launch("attn_res_bwd_res_kernel");
+    };
+    if (n_tokens > 0 && N <= 8 && Pl <= 2) {
+      const int rc = resident(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
+      if (rc) return rc;
+    } else if (n_tokens > 0 && N <= 16 && Pl <= 1) {
+      const int rc = resident(std::integral_constant<int, 16>{}, std::integral_constant<int, 1>{});
+      if (rc) return rc;
+    } else if (n_tokens > 0) {
       const int rc = dispatch_p(packs_per_lane<T>(D), [&](auto pc) {
         constexpr int PP = decltype(pc)::value;
         hipLaunchKernelGGL((attn_res_bwd_kernel<T, VEC, PP>), dim3((unsigned)used), dim3(kNT), 0, st, (T*)dV, part,

@@ -348,6 +348,40 @@ def bench_c5(K, dev, reps, flush):
     return e
 
 
+def bench_flgrpo(K, dev, reps, flush):
+    """FusedLinear-GRPO (no counterpart in the reference): C4's batch (B 16, L+1 1024, V 151936, beta 0.1)
+    behind an H = 4096 bf16 lm_head, fwd+bwd."""
+    from kernels import fused_linear_grpo as flg
+
+    def logp_fn(h, w, ids):
+        # lse from a no-grad pass of the op itself, the id logits by a gather
+        _, _, _, _, _, rows = flg.fused_linear_grpo_forward(h, w, ids, torch.zeros(h.shape[0], device=dev),
+                                                            compute_grad=False)
+        return (h[:, :-1].float() * w[ids].float()).sum(-1) - rows[0]
+
+    c = workloads.f3_fused_linear_grpo(logp_fn, device=dev)
+    h = c["hidden"].requires_grad_(True)
+    w = c["weight"].requires_grad_(True)
+    args = [c[k] for k in ("completion_ids", "advantages", "old_logp", "ref_logp", "completion_mask", "temperature",
+                           "beta", "eps_low", "eps_high")]
+    B, T, H = h.shape
+    V = w.shape[0]
+    n_live = int(c["completion_mask"].sum())
+
+    def fn():
+        loss, _, _ = K.hilda_fused_linear_grpo_loss(h, w, *args)
+        return torch.autograd.grad([loss], [h, w])
+
+    work = 6 * n_live * H * V  # conservative: masked tokens and position L need no FLOPs
+    e = op_entry(f"fused_linear_grpo B={B} L+1={T} H={H} V={V} bf16", time_events(fn, reps, flush, warmup=1), work,
+                 "TFLOP/s", BF16_PEAK_TFLOPS)
+    e["dense_equivalent_tflops"] = round(6 * B * T * H * V / (e["ms"] * 1e-3) / 1e12, 2)
+    e["n_live_tokens"] = n_live
+    log(f"  fused_linear_grpo: {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  ({e['frac']:.1%}); "
+        f"dense-equivalent {e['dense_equivalent_tflops']} TFLOP/s")
+    return e
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (the reference's PyTorch path) on the host cores
 # ---------------------------------------------------------------------------
@@ -507,7 +541,8 @@ def main(argv=None):
         table = (("rms_norm", bench_c1, True), ("geglu", bench_geglu, True), ("attn_res", bench_attn_res, True),
                  ("cross_entropy", bench_c3, False), ("grpo_loss", bench_c4, False),
                  ("fused_linear_cross_entropy", bench_c5, False), ("kl_div", bench_kl_div, False),
-                 ("jsd", bench_jsd, False), ("fused_linear_jsd", bench_fljsd, False))
+                 ("jsd", bench_jsd, False), ("fused_linear_jsd", bench_fljsd, False),
+                 ("fused_linear_grpo", bench_flgrpo, False))
         wanted = [n for n, _, _ in table] if args.ops == "all" else \
             [] if args.ops == "c2" else args.ops.split(",")
         unknown = set(wanted) - {n for n, _, _ in table}

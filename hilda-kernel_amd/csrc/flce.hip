@@ -1,6 +1,6 @@
-// FusedLinearCrossEntropy and FusedLinearJSD for gfx950: lm_head GEMMs on
-// bf16/fp16 MFMA with the loss gradient produced chunk by chunk, so the full
-// (BT, V) logits never exist.
+// FusedLinearCrossEntropy, FusedLinearJSD and FusedLinear-GRPO for gfx950:
+// lm_head GEMMs on bf16/fp16 MFMA with the loss gradient produced chunk by
+// chunk, so the full (BT, V) logits never exist.
 //
 // Every contraction is one "NT" GEMM (gemm_nt.h), C[M,N] = A[M,K] * B[N,K]^T
 // with both operands K-contiguous, the layout the MFMA operand fetch wants:
@@ -154,10 +154,11 @@ int64_t pad8(int64_t x) { return (x + 7) & ~(int64_t)7; }
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct FlceLayout {
-  size_t wt, xt, lg, dt, dwacc, nvalid, total;
+  size_t wt, xt, lg, dt, dwacc, nvalid, extra, total;
 };
 
-FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad) {
+// extra: bytes for the row step's own scratch (16-byte aligned)
+FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad, size_t extra = 0) {
   FlceLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -173,6 +174,7 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
     L.dt = take((size_t)V * pad8(chunk) * es);
     L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
   }
+  L.extra = extra ? take(extra) : 0;
   L.total = off;
   return L;
 }
@@ -208,6 +210,61 @@ int64_t flce_chunk(int64_t BT, int64_t chunk) {
   if (chunk <= 0) chunk = 8192;
   chunk = std::max<int64_t>(8, chunk & ~(int64_t)7);
   return std::min<int64_t>(chunk, BT > 0 ? BT : 1);
+}
+
+// The chunked lm_head shared by the fused-linear losses. Per chunk of C rows:
+// logits_c = X_c W^T into the chunk buffer; row_step(Lg, r0, cs) produces the
+// row losses and, with gradients, the dlogits D_c written over the logits;
+// then dX_c = D_c W and dW += D_c^T X_c (fp32 accumulator across chunks, the
+// result rounded once into dWo). X [BT, H] and W [V, H] are K-contiguous.
+template <typename T, class RowStep>
+int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, int64_t C, char* ws,
+                    const FlceLayout& lay, bool grad, T* dX, T* dWo, RowStep&& row_step, hipStream_t st) {
+  const int64_t BTp = pad8(BT);
+  T* Lg = (T*)(ws + lay.lg);
+  T* Wt = grad ? (T*)(ws + lay.wt) : nullptr;
+  T* Xt = grad ? (T*)(ws + lay.xt) : nullptr;
+  T* Dt = grad ? (T*)(ws + lay.dt) : nullptr;
+  float* dwacc = (grad && lay.dwacc) ? (float*)(ws + lay.dwacc) : nullptr;
+  int rc = HK_OK;
+  if (grad) {
+    rc = launch_transpose<T>(Wt, W, V, V, H, H, V, st);  // W^T [H, V]
+    if (rc) return rc;
+    rc = launch_transpose<T>(Xt, X, BT, BTp, H, H, BTp, st);  // X^T [H, BTp], zero padded
+    if (rc) return rc;
+  }
+  const int64_t nchunks = BT > 0 ? cdiv(BT, C) : 0;
+  for (int64_t ci = 0; ci < nchunks; ++ci) {
+    const int64_t r0 = ci * C;
+    const int64_t cs = std::min<int64_t>(C, BT - r0);
+    // logits_c = X_c W^T
+    rc = launch_gemm<T>(X + r0 * H, W, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Lg, V}, st);
+    if (rc) return rc;
+    rc = row_step(Lg, r0, cs);
+    if (rc) return rc;
+    if (!grad) continue;
+    // dX_c = D_c W
+    rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{dX + r0 * H, H}, st);
+    if (rc) return rc;
+    // dW += D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands
+    const int64_t csp = pad8(cs);
+    rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, csp, st);
+    if (rc) return rc;
+    auto dw_gemm = [&](auto epi) { return launch_gemm<T>(Dt, Xt + r0, (int)V, (int)H, (int)csp, csp, BTp, epi, st); };
+    if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
+    else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
+    else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
+    else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
+    if (rc) return rc;
+  }
+  if (grad && nchunks == 0) {
+    // no rows: the weight gradient is zero (dX is empty)
+    const int64_t n16 = V * H * (int64_t)sizeof(T) / 16;
+    hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n16, 256), 4096)), dim3(256), 0, st,
+                       (u32x4*)dWo, n16);
+    rc = check_launch("zero16_kernel");
+  }
+  return rc;
 }
 
 }  // namespace
@@ -251,65 +308,21 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
   // every target equal to ignore_index is ignored (fused_linear_cross_entropy.py:121,62-65);
   // unlike the CrossEntropy op, -1 is not a "no ignore" sentinel here
   const int has_ignore = 1;
-  const int64_t BTp = pad8(BT);
 
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
-    const int dt = dtype;
-    const T* X = (const T*)hidden;
-    const T* W = (const T*)weight;
-    T* Lg = (T*)(ws + lay.lg);
     int rc = HK_OK;
     if (BT > 0) rc = count_valid_launch(n_valid, targets, BT, ignore_index, has_ignore, st);
     if (rc) return rc;
-    T* Wt = grad ? (T*)(ws + lay.wt) : nullptr;
-    T* Xt = grad ? (T*)(ws + lay.xt) : nullptr;
-    T* Dt = grad ? (T*)(ws + lay.dt) : nullptr;
-    float* dwacc = (grad && lay.dwacc) ? (float*)(ws + lay.dwacc) : nullptr;
-    if (grad) {
-      rc = launch_transpose<T>(Wt, W, V, V, H, H, V, st);  // W^T [H, V]
-      if (rc) return rc;
-      rc = launch_transpose<T>(Xt, X, BT, BTp, H, H, BTp, st);  // X^T [H, BTp], zero padded
-      if (rc) return rc;
-    }
-    const int64_t nchunks = BT > 0 ? cdiv(BT, C) : 0;
-    for (int64_t ci = 0; ci < nchunks; ++ci) {
-      const int64_t r0 = ci * C;
-      const int64_t cs = std::min<int64_t>(C, BT - r0);
-      // logits_c = X_c W^T
-      rc = launch_gemm<T>(X + r0 * H, W, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Lg, V}, st);
-      if (rc) return rc;
-      // per-row loss; with gradients, D_c = (softmax - onehot) * s * row_scale written over the logits
-      rc = ce_rows_launch(grad ? (void*)Lg : nullptr, loss_rows + r0, Lg, targets + r0, cs, V, V, V, ignore_index,
-                          has_ignore, n_valid, grad && reduction == HK_REDUCTION_MEAN,
-                          row_scale ? row_scale + r0 : nullptr, dt, st);
-      if (rc) return rc;
-      if (!grad) continue;
-      // dX_c = D_c W
-      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{(T*)dhidden + r0 * H, H}, st);
-      if (rc) return rc;
-      // dW += D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands
-      const int64_t csp = pad8(cs);
-      rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, csp, st);
-      if (rc) return rc;
-      auto dw_gemm = [&](auto epi) {
-        return launch_gemm<T>(Dt, Xt + r0, (int)V, (int)H, (int)csp, csp, BTp, epi, st);
-      };
-      T* dWo = (T*)dweight;
-      if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
-      else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
-      else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
-      else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
-      if (rc) return rc;
-    }
-    if (grad && nchunks == 0) {
-      // no rows: the weight gradient is zero (dhidden is empty)
-      const int64_t n16 = V * H * (int64_t)sizeof(T) / 16;
-      hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n16, 256), 4096)), dim3(256), 0, st,
-                         (u32x4*)dweight, n16);
-      rc = check_launch("zero16_kernel");
-      if (rc) return rc;
-    }
+    // per-row loss; with gradients, D_c = (softmax - onehot) * s * row_scale written over the logits
+    auto ce_step = [&](T* Lg, int64_t r0, int64_t cs) {
+      return ce_rows_launch(grad ? (void*)Lg : nullptr, loss_rows + r0, Lg, targets + r0, cs, V, V, V, ignore_index,
+                            has_ignore, n_valid, grad && reduction == HK_REDUCTION_MEAN,
+                            row_scale ? row_scale + r0 : nullptr, dtype, st);
+    };
+    rc = chunked_lm_head<T>((const T*)hidden, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden,
+                            (T*)dweight, ce_step, st);
+    if (rc) return rc;
     if (loss_out) {
       // with gradients the rows already carry 1/max(n_valid,1) for 'mean'; without, divide here
       const bool divide = !grad && reduction == HK_REDUCTION_MEAN && BT > 0;
@@ -418,6 +431,64 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
     }
     // the rows already carry 1/n (:190)
     return scaled_sum_rows_launch(loss_out, loss_rows, BT, 1.0f, st);
+  };
+  if (dtype == HK_BF16) return run(Tag<__bf16>{});
+  return run(Tag<_Float16>{});
+}
+
+size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int dtype,
+                                           int with_grad) {
+  if (B <= 0 || L < 0 || H <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
+  const int64_t BT = B * (L + 1);
+  return flce_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0, grpo_scratch_bytes(B, L)).total;
+}
+
+int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float* lse_rows, float* loss_rows,
+                         float* kl_rows, float* clip_rows, void* dhidden, void* dweight, const void* hidden,
+                         const void* weight, const int64_t* ids, int64_t ids_sB, int64_t ids_sL,
+                         const float* advantages, const float* old_logp, int64_t old_sB, int64_t old_sL,
+                         const float* ref_logp, int64_t ref_sB, int64_t ref_sL, const void* mask, int mask_dtype,
+                         int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t H, int64_t V,
+                         float temperature, float beta, float eps_low, float eps_high, int dtype, int64_t chunk,
+                         void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+  HK_REQUIRE(dtype == HK_BF16 || dtype == HK_F16, "fused linear GRPO supports bf16 and fp16 (got %d)", dtype);
+  const GrpoInputs in{ids,    ids_sB, ids_sL, advantages, old_logp, old_sB,      old_sL, ref_logp,
+                      ref_sB, ref_sL, mask,   mask_dtype, mask_sB,  mask_sL,     B,      L,
+                      V,      temperature,    beta,       eps_low,  eps_high};
+  if (const int rc = grpo_check(in)) return rc;
+  HK_REQUIRE(H > 0 && H % 8 == 0 && V % 8 == 0, "H and V must be positive multiples of 8 (16-byte rows)");
+  HK_REQUIRE(B * (L + 1) < (1LL << 31) && H < (1LL << 31), "dimension too large");
+  const bool grad = dhidden != nullptr || dweight != nullptr;
+  HK_REQUIRE(!grad || (dhidden && dweight), "dhidden and dweight are computed together");
+  HK_REQUIRE(loss_out && clip_out && hidden && weight && (L == 0 || (lse_rows && loss_rows && kl_rows && clip_rows)),
+             "null pointer argument");
+  HK_REQUIRE(aligned_to(hidden, 16) && aligned_to(weight, 16) && (!grad || (aligned_to(dhidden, 16) &&
+                                                                             aligned_to(dweight, 16))),
+             "hidden, weight and gradients must be 16-byte aligned");
+  const int64_t BT = B * (L + 1);
+  const int64_t C = flce_chunk(BT, chunk);
+  const FlceLayout lay = flce_layout(BT, H, V, C, 2, grad, grpo_scratch_bytes(B, L));
+  HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
+             workspace_bytes);
+  HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  void* scratch = ws + lay.extra;
+  auto run = [&](auto tag) -> int {
+    using T = typename decltype(tag)::type;
+    int rc = grpo_prep_launch(in, scratch, st);
+    if (rc) return rc;
+    // rows of the chunk are positions r0.. of the (B, L+1) hidden rows: the
+    // GRPO row kernel writes the per-token results and, with gradients, the
+    // dlogits over the logits (zero rows at masked tokens and at position L)
+    auto grpo_step = [&](T* Lg, int64_t r0, int64_t cs) {
+      return grpo_rows_launch(grad ? (void*)Lg : nullptr, Lg, r0, cs, in, scratch, dtype, st);
+    };
+    rc = chunked_lm_head<T>((const T*)hidden, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden,
+                            (T*)dweight, grpo_step, st);
+    if (rc) return rc;
+    return grpo_finalize_launch(in, scratch, loss_out, kl_out, clip_out, lse_rows, loss_rows, kl_rows, clip_rows,
+                                st);
   };
   if (dtype == HK_BF16) return run(Tag<__bf16>{});
   return run(Tag<_Float16>{});

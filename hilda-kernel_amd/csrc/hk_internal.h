@@ -33,4 +33,41 @@ int jsd_logits_launch(float* loss_rows, void* ls, const void* lt, const int64_t*
                       const int* n_valid, int64_t n_all, float beta, float temperature, int64_t rows, int64_t cols,
                       int64_t ld, int write, int dtype, hipStream_t st);
 
+// GRPO's per-call inputs (kernels/grpo_loss.py:241-297): ids, old/ref log-probs
+// (fp32, nullable) and mask (any HK_ dtype, nullable) with element strides;
+// advantages [B] fp32.
+struct GrpoInputs {
+  const int64_t* ids;
+  int64_t ids_sB, ids_sL;
+  const float* adv;
+  const float* old_logp;
+  int64_t old_sB, old_sL;
+  const float* ref_logp;
+  int64_t ref_sB, ref_sL;
+  const void* mask;
+  int mask_dt;
+  int64_t mask_sB, mask_sL;
+  int64_t B, L, V;
+  float temperature, beta, eps_lo, eps_hi;
+};
+
+// Argument checks shared by the GRPO entry points: HK_OK, or HK_EINVAL with the message set.
+int grpo_check(const GrpoInputs& in);
+
+// Bytes of GRPO scratch (16-byte aligned): token records and per-token results for B x L tokens.
+size_t grpo_scratch_bytes(int64_t B, int64_t L);
+
+// Token records (id, old/ref, advantage, mask, mask / (len_b * B) / T) into scratch.
+int grpo_prep_launch(const GrpoInputs& in, void* scratch, hipStream_t st);
+
+// Rows [row0, row0 + nrows) of the B x (L+1) logits rows, `logits` pointing at
+// row row0 (row stride V): per-token results into scratch and, with dlogits
+// (may alias logits), the gradient rows at unit upstream gradient.
+int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nrows, const GrpoInputs& in,
+                     void* scratch, int dtype, hipStream_t st);
+
+// The reductions (loss, kl_mean, clip_ratio) and the per-token rows [B, L].
+int grpo_finalize_launch(const GrpoInputs& in, const void* scratch, float* loss_out, float* kl_out, float* clip_out,
+                         float* lse_rows, float* loss_rows, float* kl_rows, float* clip_rows, hipStream_t st);
+
 }  // namespace hk

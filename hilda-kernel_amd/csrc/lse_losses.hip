@@ -610,13 +610,15 @@ struct GrpoHot {
   const GrpoTok* tok;
   GrpoOut* out;
   int64_t B, L, V;
+  int64_t row0, nrows;  // the launch covers rows [row0, row0 + nrows) of the (B, L+1) positions
   float inv_T, beta, eps_lo, eps_hi;
   int has_old;
 };
 
 // GRPO forward with the gradient fused in (kernels/grpo_loss.py:87-159 forward,
-// :166-234 backward at unit upstream gradient). Rows are all B*(L+1) positions
-// of the logits; the last position and masked tokens get a zero gradient row.
+// :166-234 backward at unit upstream gradient). Rows are positions
+// [row0, row0 + nrows) of the B*(L+1) logits rows; `logits` and `dlogits`
+// point at row row0. The last position and masked tokens get a zero gradient row.
 // The per-token loss terms from logp (kernels/grpo_loss.py:103-133): the
 // result row and d loss / d logp.
 __device__ __forceinline__ GrpoOut grpo_terms(const GrpoHot& a, const GrpoTok& tk, float lse, float logp,
@@ -645,26 +647,26 @@ template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT, bool GRAD>
 __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
                                                      GrpoHot a) {
   __shared__ float red[4 * (BLOCK / kWave)];
-  const int64_t rows = a.B * (a.L + 1);
+  const int64_t rows = a.nrows;  // row below: local to the launch
   const int64_t G = gridDim.x;
   const float c = kLog2e * a.inv_T;
   // a row is live when it is a token position (l < L) with a nonzero mask
   auto live = [&](int64_t row, GrpoTok* tk) {
-    const int64_t b = row / (a.L + 1), l = row - b * (a.L + 1);
+    const int64_t g = a.row0 + row, b = g / (a.L + 1), l = g - b * (a.L + 1);
     if (l == a.L) return false;
     *tk = a.tok[b * a.L + l];
     return tk->m != 0.f;
   };
   auto token = [&](int64_t row) {
-    const int64_t b = row / (a.L + 1);
-    return row - b;  // b * L + l
+    const int64_t g = a.row0 + row, b = g / (a.L + 1);
+    return g - b;  // b * L + l
   };
   // dead rows: a zero gradient row (never read) and zero results
   for (int64_t row = blockIdx.x; row < rows; row += G) {
     GrpoTok tk{};
     if (!live(row, &tk)) {
       if constexpr (GRAD) fill_row<T, VEC, BLOCK>(dlogits + row * a.V, (int)a.V, 0.f);
-      const int64_t b = row / (a.L + 1), l = row - b * (a.L + 1);
+      const int64_t g = a.row0 + row, b = g / (a.L + 1), l = g - b * (a.L + 1);
       if (l < a.L && threadIdx.x == 0) a.out[b * a.L + l] = GrpoOut{0.f, 0.f, 0.f, 0.f};
     }
   }
@@ -722,6 +724,9 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       T* out = GRAD ? dlogits + row * a.V : nullptr;
       const T* in = logits + row * a.V;
       const int n = row_len(a.V);
+      // the id logit is read before the reduction's barriers: dlogits may alias
+      // logits, and no lane stores before every lane has passed them
+      const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
       float lse2;
       if constexpr (RESIDENT) {
         // the same reduction as the gradient path, so both give bitwise equal results
@@ -735,7 +740,7 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
         lse2 = row_lse2_stream<T, VEC, BLOCK>(in, n, c, red);
       }
       const float lse = lse2 * kLn2;
-      const float logp = tk.id >= 0 ? to_f32<T>(in[tk.id]) * a.inv_T - lse : NAN;
+      const float logp = tk.id >= 0 ? xid * a.inv_T - lse : NAN;
       float dlogp;
       const GrpoOut res = grpo_terms(a, tk, lse, logp, &dlogp);
       if (threadIdx.x == 0) a.out[token(row)] = res;
@@ -898,6 +903,114 @@ int esize(int dt) { return dt == HK_F32 ? 4 : 2; }
 }  // namespace hk
 
 namespace hk {
+
+namespace {
+GrpoArgs grpo_args(const GrpoInputs& in) {
+  GrpoArgs a{};
+  a.ids = in.ids;
+  a.ids_sB = in.ids_sB;
+  a.ids_sL = in.ids_sL;
+  a.adv = in.adv;
+  a.old_logp = in.old_logp;
+  a.old_sB = in.old_sB;
+  a.old_sL = in.old_sL;
+  a.ref_logp = in.ref_logp;
+  a.ref_sB = in.ref_sB;
+  a.ref_sL = in.ref_sL;
+  a.mask = in.mask;
+  a.mask_dt = in.mask_dt;
+  a.mask_sB = in.mask_sB;
+  a.mask_sL = in.mask_sL;
+  a.B = in.B;
+  a.L = in.L;
+  a.V = in.V;
+  a.inv_T = 1.f / in.temperature;
+  a.beta = in.beta;
+  a.eps_lo = in.eps_lo;
+  a.eps_hi = in.eps_hi;
+  return a;
+}
+}  // namespace
+
+size_t grpo_scratch_bytes(int64_t B, int64_t L) {
+  // token records then per-token results
+  return (size_t)(B * L) * (sizeof(GrpoTok) + sizeof(GrpoOut)) + 256;
+}
+
+int grpo_check(const GrpoInputs& in) {
+  HK_REQUIRE(in.B > 0 && in.L >= 0 && in.V > 0, "invalid shape B=%lld L=%lld V=%lld", (long long)in.B,
+             (long long)in.L, (long long)in.V);
+  HK_REQUIRE(in.temperature > 0.f, "temperature must be positive");
+  HK_REQUIRE(!in.mask || valid_mask_dtype(in.mask_dt), "invalid mask dtype code %d", in.mask_dt);
+  HK_REQUIRE(in.beta == 0.f || in.ref_logp != nullptr, "beta != 0 needs ref_logp");
+  HK_REQUIRE(in.V < (1LL << 31) - 4096, "V=%lld too large", (long long)in.V);
+  HK_REQUIRE(in.ids && in.adv, "null pointer argument");
+  return HK_OK;
+}
+
+int grpo_prep_launch(const GrpoInputs& in, void* scratch, hipStream_t st) {
+  if (in.L == 0) return HK_OK;
+  hipLaunchKernelGGL(grpo_prep_kernel, dim3((unsigned)in.B), dim3(1024), 0, st, grpo_args(in), (GrpoTok*)scratch);
+  return check_launch("grpo_prep_kernel");
+}
+
+int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nrows, const GrpoInputs& in,
+                     void* scratch, int dtype, hipStream_t st) {
+  if (nrows <= 0) return HK_OK;
+  GrpoHot h{};
+  h.tok = (const GrpoTok*)scratch;
+  h.out = (GrpoOut*)((char*)scratch + (size_t)(in.B * in.L) * sizeof(GrpoTok));
+  h.B = in.B;
+  h.L = in.L;
+  h.V = in.V;
+  h.row0 = row0;
+  h.nrows = nrows;
+  h.inv_T = 1.f / in.temperature;
+  h.beta = in.beta;
+  h.eps_lo = in.eps_lo;
+  h.eps_hi = in.eps_hi;
+  h.has_old = in.old_logp != nullptr;
+  const int es = esize(dtype);
+  const bool vec_ok = in.V % (16 / es) == 0 && aligned_to(logits, 16) && (!dlogits || aligned_to(dlogits, 16));
+  const RowCfg cfg = choose_row_cfg(in.V, es, vec_ok);
+  return dispatch_t(dtype, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    return dispatch_cfg(cfg, [&](auto blk, auto nch) {
+      constexpr int BLOCK = decltype(blk)::value;
+      constexpr int NCH = decltype(nch)::value;
+      const dim3 grid((unsigned)persistent_grid(nrows, BLOCK));
+      auto go = [&](auto grad_c) {
+        constexpr bool GRAD = decltype(grad_c)::value;
+        if (cfg.vec == 1) {
+          hipLaunchKernelGGL((grpo_kernel<T, 1, 1, 1024, false, GRAD>), grid, dim3(1024), 0, st, (T*)dlogits,
+                             (const T*)logits, h);
+        } else if constexpr (NCH == 0) {
+          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>), grid, dim3(BLOCK), 0, st,
+                             (T*)dlogits, (const T*)logits, h);
+        } else {
+          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>), grid, dim3(BLOCK), 0, st,
+                             (T*)dlogits, (const T*)logits, h);
+        }
+        return check_launch("grpo_kernel");
+      };
+      if (dlogits) return go(std::true_type{});
+      return go(std::false_type{});
+    });
+  });
+}
+
+int grpo_finalize_launch(const GrpoInputs& in, const void* scratch, float* loss_out, float* kl_out, float* clip_out,
+                         float* lse_rows, float* loss_rows, float* kl_rows, float* clip_rows, hipStream_t st) {
+  GrpoArgs a = grpo_args(in);
+  a.lse_rows = lse_rows;
+  a.loss_rows = loss_rows;
+  a.kl_rows = kl_rows;
+  a.clip_rows = clip_rows;
+  const GrpoTok* tok = (const GrpoTok*)scratch;
+  const GrpoOut* res = (const GrpoOut*)((const char*)scratch + (size_t)(in.B * in.L) * sizeof(GrpoTok));
+  hipLaunchKernelGGL(grpo_finalize_kernel, dim3(1), dim3(1024), 0, st, a, tok, res, loss_out, kl_out, clip_out);
+  return check_launch("grpo_finalize_kernel");
+}
 
 int count_valid_launch(int* n_valid, const int64_t* targets, int64_t rows, int64_t ignore_index, int has_ignore,
                        hipStream_t st) {
@@ -1120,8 +1233,7 @@ int hk_selective_log_softmax(float* logp, const void* logits, const int64_t* ids
 
 size_t hk_grpo_workspace_size(int64_t B, int64_t L) {
   if (B < 0 || L < 0) return 0;
-  // token records then per-token results
-  return (size_t)(B * L) * (sizeof(GrpoTok) + sizeof(GrpoOut)) + 256;
+  return grpo_scratch_bytes(B, L);
 }
 
 int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_out, float* lse_rows,
@@ -1132,94 +1244,20 @@ int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_
                      float temperature, float beta, float eps_low, float eps_high, int dtype, void* workspace,
                      size_t workspace_bytes, hk_stream_t stream) {
   HK_REQUIRE(valid_float_dtype(dtype), "invalid logits dtype code %d", dtype);
-  HK_REQUIRE(B > 0 && L >= 0 && V > 0, "invalid shape B=%lld L=%lld V=%lld", (long long)B, (long long)L,
-             (long long)V);
-  HK_REQUIRE(temperature > 0.f, "temperature must be positive");
-  HK_REQUIRE(!mask || valid_mask_dtype(mask_dtype), "invalid mask dtype code %d", mask_dtype);
-  HK_REQUIRE(beta == 0.f || ref_logp != nullptr, "beta != 0 needs ref_logp");
-  HK_REQUIRE(V < (1LL << 31) - 4096, "V=%lld too large", (long long)V);
+  const GrpoInputs in{ids,  ids_sB,    ids_sL,  advantages, old_logp, old_sB,      old_sL,  ref_logp,
+                      ref_sB, ref_sL,  mask,    mask_dtype, mask_sB,  mask_sL,     B,       L,
+                      V,    temperature, beta,  eps_low,    eps_high};
+  if (const int rc = grpo_check(in)) return rc;
   HK_REQUIRE(workspace && workspace_bytes >= hk_grpo_workspace_size(B, L), "workspace too small");
-  HK_REQUIRE(loss_out && clip_out && logits && ids && advantages && (L == 0 || (lse_rows && loss_rows && kl_rows && clip_rows)),
-             "null pointer argument");
-  GrpoArgs a{};
-  a.ids = ids;
-  a.ids_sB = ids_sB;
-  a.ids_sL = ids_sL;
-  a.adv = advantages;
-  a.old_logp = old_logp;
-  a.old_sB = old_sB;
-  a.old_sL = old_sL;
-  a.ref_logp = ref_logp;
-  a.ref_sB = ref_sB;
-  a.ref_sL = ref_sL;
-  a.mask = mask;
-  a.mask_dt = mask_dtype;
-  a.mask_sB = mask_sB;
-  a.mask_sL = mask_sL;
-  a.B = B;
-  a.L = L;
-  a.V = V;
-  a.inv_T = 1.f / temperature;
-  a.beta = beta;
-  a.eps_lo = eps_low;
-  a.eps_hi = eps_high;
-  a.lse_rows = lse_rows;
-  a.loss_rows = loss_rows;
-  a.kl_rows = kl_rows;
-  a.clip_rows = clip_rows;
-  hipStream_t st = (hipStream_t)stream;
   HK_REQUIRE(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
-  GrpoTok* tok = (GrpoTok*)workspace;
-  GrpoOut* res = (GrpoOut*)((char*)workspace + (size_t)(B * L) * sizeof(GrpoTok));
-  GrpoHot h{};
-  h.tok = tok;
-  h.out = res;
-  h.B = B;
-  h.L = L;
-  h.V = V;
-  h.inv_T = a.inv_T;
-  h.beta = beta;
-  h.eps_lo = eps_low;
-  h.eps_hi = eps_high;
-  h.has_old = old_logp != nullptr;
-  if (L > 0) {
-    hipLaunchKernelGGL(grpo_prep_kernel, dim3((unsigned)B), dim3(1024), 0, st, a, tok);
-    int rc = check_launch("grpo_prep_kernel");
-    if (rc) return rc;
-  }
-  int rc = HK_OK;
-  const int es = esize(dtype);
-  const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (!dlogits || aligned_to(dlogits, 16));
-  const RowCfg cfg = choose_row_cfg(V, es, vec_ok);
-  const int64_t rows = B * (L + 1);
-  rc = dispatch_t(dtype, [&](auto tt) {
-    using T = typename decltype(tt)::type;
-    return dispatch_cfg(cfg, [&](auto blk, auto nch) {
-      constexpr int BLOCK = decltype(blk)::value;
-      constexpr int NCH = decltype(nch)::value;
-      const dim3 grid((unsigned)persistent_grid(rows, BLOCK));
-      auto go = [&](auto grad_c) {
-        constexpr bool GRAD = decltype(grad_c)::value;
-        if (cfg.vec == 1) {
-          hipLaunchKernelGGL((grpo_kernel<T, 1, 1, 1024, false, GRAD>), grid, dim3(1024), 0, st, (T*)dlogits,
-                             (const T*)logits, h);
-        } else if constexpr (NCH == 0) {
-          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>), grid, dim3(BLOCK), 0, st,
-                             (T*)dlogits, (const T*)logits, h);
-        } else {
-          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>), grid, dim3(BLOCK), 0, st,
-                             (T*)dlogits, (const T*)logits, h);
-        }
-        return check_launch("grpo_kernel");
-      };
-      if (dlogits) return go(std::true_type{});
-      return go(std::false_type{});
-    });
-  });
+  HK_REQUIRE(loss_out && clip_out && logits && (L == 0 || (lse_rows && loss_rows && kl_rows && clip_rows)),
+             "null pointer argument");
+  hipStream_t st = (hipStream_t)stream;
+  int rc = grpo_prep_launch(in, workspace, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(grpo_finalize_kernel, dim3(1), dim3(1024), 0, st, a, (const GrpoTok*)tok, (const GrpoOut*)res,
-                     loss_out, kl_out, clip_out);
-  return check_launch("grpo_finalize_kernel");
+  rc = grpo_rows_launch(dlogits, logits, 0, B * (L + 1), in, workspace, dtype, st);
+  if (rc) return rc;
+  return grpo_finalize_launch(in, workspace, loss_out, kl_out, clip_out, lse_rows, loss_rows, kl_rows, clip_rows, st);
 }
 
 }  // extern "C"

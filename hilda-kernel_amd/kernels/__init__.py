@@ -3,6 +3,9 @@
 Drop-in for the reference package ``kernels`` (triton-kernels/kernels/__init__.py:1-28),
 restricted to the hot path: the same functional names, autograd Functions and
 modules, backed by hand-written HIP kernels in ``libhilda_kernel_amd.so``.
+FusedLinear-GRPO (``hilda_fused_linear_grpo_loss``) has no counterpart in the
+reference: it is the GRPO loss behind the lm_head, chunked like
+FusedLinearCrossEntropy.
 Put ``hilda-kernel_amd/`` on ``sys.path`` and ``from kernels import ...`` as
 with the reference.
 """
@@ -19,6 +22,7 @@ from .fused_add_rms_norm import HildaFusedAddRMSNormFunction, hilda_fused_add_rm
 from .fused_linear_cross_entropy import (HildaFusedLinearCrossEntropyFunction, hilda_fused_linear_cross_entropy,
                                          FusedLinearCrossEntropyLoss)
 from .grpo_loss import HildaGRPOLossFunction, hilda_grpo_loss, GRPOLoss, fused_selective_log_softmax
+from .fused_linear_grpo import HildaFusedLinearGRPOFunction, hilda_fused_linear_grpo_loss, FusedLinearGRPOLoss
 
 __all__ = [
     "HildaRMSNormFunction", "hilda_rms_norm", "RMSNorm",
@@ -33,4 +37,5 @@ __all__ = [
     "HildaFusedAddRMSNormFunction", "hilda_fused_add_rms_norm", "FusedAddRMSNorm",
     "HildaFusedLinearCrossEntropyFunction", "hilda_fused_linear_cross_entropy", "FusedLinearCrossEntropyLoss",
     "HildaGRPOLossFunction", "hilda_grpo_loss", "GRPOLoss", "fused_selective_log_softmax",
+    "HildaFusedLinearGRPOFunction", "hilda_fused_linear_grpo_loss", "FusedLinearGRPOLoss",
 ]

@@ -64,6 +64,10 @@ SIGNATURES = {
                                              _i64, _p, _sz, _p]),
     "hk_grpo_loss_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _p,
                                 _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _i32, _p, _sz, _p]),
+    "hk_fused_linear_grpo_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
+    "hk_fused_linear_grpo": (_i32, [_p] * 7 + [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64,
+                                               _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32,
+                                               _i32, _i64, _p, _sz, _p]),
 }
 
 ABI_VERSION = 1

@@ -195,6 +195,31 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
                         int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
+/* FusedLinear-GRPO                                                        */
+/* ----------------------------------------------------------------------- */
+/* No counterpart in the reference: its GRPO op takes materialised logits
+ * (grpo_loss.py:241-330). This is that op behind the lm_head, chunked like
+ * fused_linear_cross_entropy_forward (fused_linear_cross_entropy.py:103-171),
+ * so the (B, L+1, V) logits never exist. Bytes of workspace it needs (0 for an
+ * unsupported dtype); chunk <= 0 selects the default (8192 rows). */
+size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int dtype,
+                                           int with_grad);
+
+/* hidden (B, L+1, H) and weight [V, H] (bf16 or fp16, contiguous): logits =
+ * hidden weight^T, then exactly hk_grpo_loss_fwd's loss, kl_mean, clip_ratio
+ * and per-token rows, and with dhidden (B, L+1, H) / dweight [V, H] (both or
+ * neither) the gradients of the loss at unit upstream gradient (zero rows of
+ * dhidden at masked tokens and at position L; dW accumulated in fp32). */
+int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float* lse_rows, float* loss_rows,
+                         float* kl_rows, float* clip_rows, void* dhidden, void* dweight, const void* hidden,
+                         const void* weight, const int64_t* ids, int64_t ids_sB, int64_t ids_sL,
+                         const float* advantages, const float* old_logp, int64_t old_sB, int64_t old_sL,
+                         const float* ref_logp, int64_t ref_sB, int64_t ref_sL, const void* mask, int mask_dtype,
+                         int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t H, int64_t V,
+                         float temperature, float beta, float eps_low, float eps_high, int dtype, int64_t chunk,
+                         void* workspace, size_t workspace_bytes, hk_stream_t stream);
+
+/* ----------------------------------------------------------------------- */
 /* AttnRes (attention residuals over depth)                                */
 /* ----------------------------------------------------------------------- */
 /* Replaces attn_res_forward (attn_res.py:209-257, kernel :31-98): V holds

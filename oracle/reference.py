@@ -34,6 +34,9 @@ retyping its formula:
                           dlogits = -A_b/(len_b*B) * (onehot - p); ref = logp -> kl = 0;
                           brute-force python loop of the per-token objective
   linear_ce_ref           fp64 brute force (explicit dot products) on tiny shapes
+  fused_linear_grpo_ref   fp64 brute force: grpo_loss_ref on logits from explicit dot products; the
+                          on-policy closed form (loss = -mean(A), dlogits = -A_b/(len_b*B) * (onehot - p) / T)
+                          carried through the lm_head by explicit loops for dhidden and dweight
 """
 from __future__ import annotations
 
@@ -45,7 +48,7 @@ import torch.nn.functional as F
 __all__ = [
     "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
     "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "fused_linear_jsd_ref", "attn_res_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
-    "linear_ce_ref", "fwd_bwd",
+    "linear_ce_ref", "fused_linear_grpo_ref", "fwd_bwd",
 ]
 
 
@@ -295,6 +298,24 @@ def linear_ce_ref(hidden, weight, targets, ignore_index=-100, reduction="mean"):
     """
     logits = hidden @ weight.T
     return cross_entropy_ref(logits, targets, ignore_index=ignore_index, reduction=reduction)
+
+
+# ---------------------------------------------------------------------------
+# FusedLinear-GRPO (no counterpart in the reference)
+# ---------------------------------------------------------------------------
+def fused_linear_grpo_ref(hidden, weight, completion_ids, advantages, old_logp=None, ref_logp=None,
+                          completion_mask=None, temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2,
+                          logits_dtype=None):
+    """The reference's GRPO loss (grpo_loss_ref, benchmarks/bench_grpo.py:30-57) on the lm_head
+    logits hidden @ weight.T (the linear of benchmarks/bench_fused_linear_ce.py:36-38).
+
+    hidden (B, L+1, H), weight (V, H). logits_dtype rounds the logits to that dtype, as an lm_head
+    GEMM that returns 16-bit logits does. Returns (loss, kl_mean or None, clip_ratio)."""
+    logits = hidden @ weight.T
+    if logits_dtype is not None:
+        logits = logits.to(logits_dtype).to(hidden.dtype)
+    return grpo_loss_ref(logits, completion_ids, advantages, old_logp, ref_logp, completion_mask, temperature,
+                         beta, eps_low, eps_high)
 
 
 # ---------------------------------------------------------------------------

@@ -418,6 +418,50 @@ def test_linear_ce_brute_force():
     assert oracle.linear_ce_ref(h, w, torch.full((N,), -100)).item() == 0.0
 
 
+def test_fused_linear_grpo_brute_force_and_closed_form():
+    B, L, H, V = 2, 3, 4, 7
+    g = _g(41)
+    h = torch.randn(B, L + 1, H, generator=g, dtype=torch.float64)
+    w = torch.randn(V, H, generator=g, dtype=torch.float64)
+    ids = torch.randint(0, V, (B, L), generator=g)
+    adv = torch.tensor([0.9, -0.6], dtype=torch.float64)
+    # logits by explicit dot products, then the (separately pinned) GRPO loss
+    logits = torch.tensor([[[sum(float(h[b, t, c]) * float(w[v, c]) for c in range(H)) for v in range(V)]
+                            for t in range(L + 1)] for b in range(B)], dtype=torch.float64)
+    logp = oracle.selective_log_softmax_ref(logits, ids).double()
+    old = logp + 0.3 * torch.randn(B, L, generator=g, dtype=torch.float64)
+    ref = logp + 0.2 * torch.randn(B, L, generator=g, dtype=torch.float64)
+    mask = torch.tensor([[1, 1, 0], [1, 1, 1]], dtype=torch.int32)
+    args = (ids, adv, old, ref, mask, 0.8, 0.1, 0.2, 0.25)
+    for x, y in zip(oracle.fused_linear_grpo_ref(h, w, *args), oracle.grpo_loss_ref(logits, *args)):
+        assert math.isclose(x.item(), y.item(), rel_tol=1e-12, abs_tol=1e-14)
+    # on-policy, beta = 0, temperature T: loss = -mean(A) and
+    # dlogits = -A_b/(len_b*B) * (onehot - softmax(logits/T)) / T, carried through the lm_head by loops
+    T = 0.8
+    hg = h.clone().requires_grad_(True)
+    wg = w.clone().requires_grad_(True)
+    loss, kl, clip = oracle.fused_linear_grpo_ref(hg, wg, ids, adv, completion_mask=mask, temperature=T)
+    assert math.isclose(loss.item(), -adv.mean().item(), rel_tol=1e-12, abs_tol=1e-12)
+    loss.backward()
+    lens = mask.sum(-1).double()
+    dl = torch.zeros(B, L + 1, V, dtype=torch.float64)
+    for b in range(B):
+        for t in range(L):
+            if not mask[b, t]:
+                continue
+            z = [float(logits[b, t, v]) / T for v in range(V)]
+            mx = max(z)
+            e = [math.exp(q - mx) for q in z]
+            for v in range(V):
+                dl[b, t, v] = -float(adv[b]) / (float(lens[b]) * B) * (float(v == int(ids[b, t])) - e[v] / sum(e)) / T
+    dh = torch.tensor([[[sum(float(dl[b, t, v]) * float(w[v, c]) for v in range(V)) for c in range(H)]
+                        for t in range(L + 1)] for b in range(B)], dtype=torch.float64)
+    dw = torch.tensor([[sum(float(dl[b, t, v]) * float(h[b, t, c]) for b in range(B) for t in range(L + 1))
+                        for c in range(H)] for v in range(V)], dtype=torch.float64)
+    assert torch.allclose(hg.grad, dh, atol=1e-14) and torch.allclose(wg.grad, dw, atol=1e-14)
+    assert torch.count_nonzero(hg.grad[:, -1]) == 0 and torch.count_nonzero(hg.grad[0, 2]) == 0
+
+
 # ---------------------------------------------------------------- generators
 def test_config_generators_small():
     c = configs.c3_cross_entropy(rows=4000, vocab=50)

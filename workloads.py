@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-SEEDS = {"c1": 1, "c2": 2, "c3": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c2": 2, "c3": 3, "c4": 4, "c5": 5, "f3": 6}
 
 
 def rope_tables(dim, max_position_embeddings=2048, base=10000.0):
@@ -129,3 +129,24 @@ def c5_fused_linear_ce(bt=16384, hidden=4096, vocab=128256, ignore_frac=0.05, de
     drop = torch.rand(bt, generator=g, device=device) < ignore_frac
     targets[drop] = -100
     return {"hidden": h, "weight": w, "targets": targets, "ignore_index": -100, "reduction": "mean"}
+
+
+def f3_fused_linear_grpo(logp_fn, B=16, T=1024, hidden=4096, vocab=151936, device="cpu", seed=SEEDS["f3"]):
+    """FusedLinear-GRPO (no counterpart in the reference): C4's GRPO batch behind an lm_head.
+    hidden = N(0,1).bf16 (B, T, H) read as (B, L+1, H), L = T-1; weight = (0.02 N(0,1)).bf16 [V, H];
+    ids, advantages and prefix masks drawn as in C4; old = logp + 0.05 N, ref = logp + 0.1 N with
+    ``logp_fn(hidden, weight, ids)`` the fp32 log-probs of the ids under the lm_head logits."""
+    g = _gen(device, seed)
+    L = T - 1
+    h = _randn(g, (B, T, hidden), device, dtype=torch.bfloat16)
+    w = _randn(g, (vocab, hidden), device, 0.02, torch.bfloat16)
+    ids = torch.randint(0, vocab, (B, L), generator=g, device=device)
+    adv = _randn(g, (B,), device)
+    lo = min(256, L)
+    lengths = torch.randint(lo, max(T, lo + 1), (B,), generator=g, device=device).clamp(max=L)
+    mask = (torch.arange(L, device=device)[None, :] < lengths[:, None]).to(torch.int32)
+    logp = logp_fn(h, w, ids).float()
+    old = logp + _randn(g, (B, L), device, 0.05)
+    ref = logp + _randn(g, (B, L), device, 0.1)
+    return {"hidden": h, "weight": w, "completion_ids": ids, "advantages": adv, "old_logp": old, "ref_logp": ref,
+            "completion_mask": mask, "temperature": 1.0, "beta": 0.1, "eps_low": 0.2, "eps_high": 0.2}

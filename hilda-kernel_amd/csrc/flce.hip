@@ -155,6 +155,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct FlceLayout {
   size_t wt, xt, lg, dt, dwacc, nvalid, extra, total;
+  bool defer;  // the whole D^T [V, BTp] is kept and dW is one GEMM after the chunk loop
 };
 
 // extra: bytes for the row step's own scratch (16-byte aligned)
@@ -171,8 +172,16 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
   if (grad) {
     L.wt = take((size_t)H * V * es);
     L.xt = take((size_t)H * pad8(BT) * es);
-    L.dt = take((size_t)V * pad8(chunk) * es);
-    L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
+    // Several chunks: keep every chunk's D^T and run dW as one GEMM over K = BT
+    // (no fp32 accumulator round trips) when that takes no more memory than
+    // one chunk's D^T plus the fp32 accumulator; otherwise accumulate per chunk.
+    L.defer = BT > chunk && pad8(BT) <= pad8(chunk) + 2 * H;
+    if (L.defer) {
+      L.dt = take((size_t)V * pad8(BT) * es);
+    } else {
+      L.dt = take((size_t)V * pad8(chunk) * es);
+      L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
+    }
   }
   L.extra = extra ? take(extra) : 0;
   L.total = off;
@@ -215,8 +224,10 @@ int64_t flce_chunk(int64_t BT, int64_t chunk) {
 // The chunked lm_head shared by the fused-linear losses. Per chunk of C rows:
 // logits_c = X_c W^T into the chunk buffer; row_step(Lg, r0, cs) produces the
 // row losses and, with gradients, the dlogits D_c written over the logits;
-// then dX_c = D_c W and dW += D_c^T X_c (fp32 accumulator across chunks, the
-// result rounded once into dWo). X [BT, H] and W [V, H] are K-contiguous.
+// then dX_c = D_c W, and dW = sum_c D_c^T X_c either as one GEMM over all rows
+// after the loop (the chunks' D_c^T side by side, lay.defer) or per chunk into
+// an fp32 accumulator, the result rounded once into dWo. X [BT, H] and W [V, H]
+// are K-contiguous.
 template <typename T, class RowStep>
 int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, int64_t C, char* ws,
                     const FlceLayout& lay, bool grad, T* dX, T* dWo, RowStep&& row_step, hipStream_t st) {
@@ -246,6 +257,12 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
     // dX_c = D_c W
     rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{dX + r0 * H, H}, st);
     if (rc) return rc;
+    if (lay.defer) {
+      // D_c^T into columns [r0, r0 + cs) of D^T [V, BTp]; the last chunk zero-pads to BTp
+      rc = launch_transpose<T>(Dt + r0, Lg, cs, ci + 1 < nchunks ? cs : BTp - r0, V, V, BTp, st);
+      if (rc) return rc;
+      continue;
+    }
     // dW += D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands
     const int64_t csp = pad8(cs);
     rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, csp, st);
@@ -255,6 +272,10 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
     else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
     else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
     else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
+    if (rc) return rc;
+  }
+  if (grad && lay.defer && nchunks > 0) {
+    rc = launch_gemm<T>(Dt, Xt, (int)V, (int)H, (int)BTp, BTp, BTp, EpiStore<T>{dWo, H}, st);
     if (rc) return rc;
   }
   if (grad && nchunks == 0) {

@@ -45,6 +45,27 @@ struct EpiStore {
   }
 };
 
+// C (T) = acc with GEMM row r stored at row rows[r] of C (the live rows of a
+// compacted operand back in place), in 16-byte chunks of 8 columns.
+template <typename T>
+struct EpiScatter {
+  using Stage = T;
+  using Prior = NoPrior;
+  static constexpr bool kReads = false;
+  T* C;
+  int64_t ldc;  // a multiple of 8
+  const int* rows;
+  __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
+  __device__ __forceinline__ void store(int row, int col, const T* v, int n, const Prior&) const {
+    T* p = C + (int64_t)rows[row] * ldc + col;
+    if (n == 8) {
+      *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(v);
+    } else {
+      for (int e = 0; e < n; ++e) p[e] = v[e];
+    }
+  }
+};
+
 // fp32 accumulator across calls, 4 columns per chunk; the last call writes T.
 // MODE 0: acc = v; 1: acc += v; 2: out = acc + v
 template <typename T, int MODE>
@@ -89,20 +110,77 @@ __global__ __launch_bounds__(256) void zero16_kernel(u32x4* __restrict__ p, int6
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0, 0, 0, 0};
 }
 
+// Compacted rows (rows of n16 16-byte words): out[i] = in[rowmap[i]] for
+// i < *n_live, zero rows for i in [*n_live, rows).
+__global__ __launch_bounds__(256) void gather_rows_kernel(u32x4* __restrict__ out, const u32x4* __restrict__ in,
+                                                          const int* __restrict__ rowmap,
+                                                          const int* __restrict__ n_live, int64_t rows, int64_t n16) {
+  const int64_t n = *n_live;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    u32x4* o = out + r * n16;
+    if (r < n) {
+      const u32x4* src = in + (int64_t)rowmap[r] * n16;
+      for (int64_t w = threadIdx.x; w < n16; w += 256) o[w] = src[w];
+    } else {
+      for (int64_t w = threadIdx.x; w < n16; w += 256) o[w] = u32x4{0, 0, 0, 0};
+    }
+  }
+}
+
+// Per-row CE inputs of the compacted rows: targets and the optional row scale.
+__global__ __launch_bounds__(256) void gather_ce_kernel(int64_t* __restrict__ t_out, float* __restrict__ s_out,
+                                                        const int64_t* __restrict__ t_in,
+                                                        const float* __restrict__ s_in, const int* __restrict__ rowmap,
+                                                        const int* __restrict__ n_live) {
+  const int64_t n = *n_live;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int r = rowmap[i];
+    t_out[i] = t_in[r];
+    if (s_in) s_out[i] = s_in[r];
+  }
+}
+
+// Rows of the original order after a compacted pass: dead rows (inv[r] < 0)
+// get a zero dX row (when dX) and loss 0; live rows take their loss from the
+// compacted losses (when loss_rows).
+__global__ __launch_bounds__(256) void finish_rows_kernel(u32x4* __restrict__ dX, int64_t n16,
+                                                          float* __restrict__ loss_rows,
+                                                          const float* __restrict__ loss_c,
+                                                          const int* __restrict__ inv, int64_t rows) {
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const int k = inv[r];
+    if (loss_rows && threadIdx.x == 0) loss_rows[r] = k >= 0 ? loss_c[k] : 0.f;
+    if (dX && k < 0)
+      for (int64_t w = threadIdx.x; w < n16; w += 256) dX[r * n16 + w] = u32x4{0, 0, 0, 0};
+  }
+}
+
 // out[c, r] = in[r, c] for a rows x cols matrix of a 16-bit type (row strides
 // ld_in, ld_out, both multiples of 8; cols a multiple of 8); output columns r
 // in [rows, rows_pad) are written as zeros (rows_pad a multiple of 8). 64x64
 // tiles: 16-byte global loads and stores, the tile staged in LDS with a pitch
 // of 66 elements (33 dwords), so the column-gathering 2-byte reads of a wave
 // fall in distinct banks.
+// With lim (a compacted input whose first *lim - lim_off rows are live), rows
+// past that are read as zeros and zeros are written up to the next multiple
+// of 64 of the bound, both relative to lim_off and absolute: what a GEMM
+// whose K is cut by the same bound reads (at least 64 columns).
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, const T* __restrict__ in, int64_t rows,
                                                         int64_t rows_pad, int64_t cols, int64_t ld_in,
-                                                        int64_t ld_out) {
+                                                        int64_t ld_out, const int* __restrict__ lim,
+                                                        int64_t lim_off) {
   constexpr int P = 66;
   __shared__ __attribute__((aligned(16))) uint16_t tile[64 * P];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  if (lim) {
+    const int64_t n = *lim, v = n - lim_off;
+    rows = std::max<int64_t>(0, std::min<int64_t>(rows, v));
+    const int64_t z = std::max<int64_t>(64, std::max<int64_t>((v + 63) / 64 * 64, (n + 63) / 64 * 64 - lim_off));
+    rows_pad = std::min<int64_t>(rows_pad, z);
+    if (r0 >= rows_pad) return;  // uniform
+  }
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int rr = t / 8 + 32 * k, cc = (t % 8) * 8;
@@ -132,34 +210,47 @@ __global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, con
 
 template <typename T> struct Tag { using type = T; };
 
+// lim (nullable): a device-side bound on M (or K with lim_k), see gemm::Shape
 template <typename T, class Epi>
-int launch_gemm(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st) {
-  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st);
+int launch_gemm(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
+                const int* lim = nullptr, int lim_off = 0, bool lim_k = false) {
+  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st, lim, lim_off, lim_k);
 }
 
 template <typename T>
 int launch_transpose(T* out, const T* in, int64_t rows, int64_t rows_pad, int64_t cols, int64_t ld_in,
-                     int64_t ld_out, hipStream_t st) {
+                     int64_t ld_out, hipStream_t st, const int* lim = nullptr, int64_t lim_off = 0) {
   if (rows_pad == 0 || cols == 0) return HK_OK;
   HK_REQUIRE(cols % 8 == 0 && rows_pad % 8 == 0 && ld_in % 8 == 0 && ld_out % 8 == 0 && aligned_to(in, 16) &&
                  aligned_to(out, 16),
              "transpose: 16-byte rows and chunks expected");
   const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows_pad, 64));
-  hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out);
+  hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out, lim,
+                     lim_off);
   return check_launch("transpose_kernel");
 }
 
 int64_t pad8(int64_t x) { return (x + 7) & ~(int64_t)7; }
+
+// Leading dimension of the transposed GEMM operands (X^T, D^T): 128 bytes past
+// the K extent, so the rows of a tile's panel do not all start at the same
+// large power-of-two offset.
+int64_t ld_t(int64_t k) { return pad8(k) + 64; }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct FlceLayout {
   size_t wt, xt, lg, dt, dwacc, nvalid, extra, total;
   bool defer;  // the whole D^T [V, BTp] is kept and dW is one GEMM after the chunk loop
+  // the compaction of the live rows: row map, inverse map, live count, compacted hidden rows;
+  // for CrossEntropy also the compacted targets, row scales and losses
+  size_t rowmap, inv, nlive, xc, tc, sc, lc;
 };
 
-// extra: bytes for the row step's own scratch (16-byte aligned)
-FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad, size_t extra = 0) {
+// extra: bytes for the row step's own scratch (16-byte aligned); ce: room for the
+// compacted CrossEntropy row inputs and outputs
+FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad, size_t extra = 0,
+                       bool ce = false) {
   FlceLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -168,18 +259,28 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
     return o;
   };
   L.nvalid = take(256);
+  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
+  L.nlive = take(256);
+  L.rowmap = take(bt * 4);
+  L.inv = take(bt * 4);
+  L.xc = take((size_t)pad8(BT) * H * es);
+  if (ce) {
+    L.tc = take(bt * 8);
+    L.sc = take(bt * 4);
+    L.lc = take(bt * 4);
+  }
   L.lg = take((size_t)chunk * V * es);
   if (grad) {
     L.wt = take((size_t)H * V * es);
-    L.xt = take((size_t)H * pad8(BT) * es);
+    L.xt = take((size_t)H * ld_t(BT) * es);
     // Several chunks: keep every chunk's D^T and run dW as one GEMM over K = BT
     // (no fp32 accumulator round trips) when that takes no more memory than
     // one chunk's D^T plus the fp32 accumulator; otherwise accumulate per chunk.
     L.defer = BT > chunk && pad8(BT) <= pad8(chunk) + 2 * H;
     if (L.defer) {
-      L.dt = take((size_t)V * pad8(BT) * es);
+      L.dt = take((size_t)V * ld_t(BT) * es);
     } else {
-      L.dt = take((size_t)V * pad8(chunk) * es);
+      L.dt = take((size_t)V * ld_t(chunk) * es);
       L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
     }
   }
@@ -214,6 +315,25 @@ FljsdLayout fljsd_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es
   return L;
 }
 
+// The compacted hidden rows (live rows in order, zero rows after them).
+template <typename T>
+int gather_rows(T* Xc, const T* X, const int* rowmap, const int* n_live, int64_t BT, int64_t H, hipStream_t st) {
+  if (BT == 0) return HK_OK;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<int64_t>(BT, 4096)), dim3(256), 0, st, (u32x4*)Xc,
+                     (const u32x4*)X, rowmap, n_live, BT, H * (int64_t)sizeof(T) / 16);
+  return check_launch("gather_rows_kernel");
+}
+
+// Zero dX rows of the dead rows and, with loss_rows, the losses back in the original order.
+template <typename T>
+int finish_rows(T* dX, float* loss_rows, const float* loss_c, const int* inv, int64_t BT, int64_t H,
+                hipStream_t st) {
+  if (BT == 0 || (!dX && !loss_rows)) return HK_OK;
+  hipLaunchKernelGGL(finish_rows_kernel, dim3((unsigned)std::min<int64_t>(BT, 4096)), dim3(256), 0, st, (u32x4*)dX,
+                     H * (int64_t)sizeof(T) / 16, loss_rows, loss_c, inv, BT);
+  return check_launch("finish_rows_kernel");
+}
+
 // Rows per chunk: a multiple of 8 (chunk starts stay 16-byte aligned in X^T), at most BT.
 int64_t flce_chunk(int64_t BT, int64_t chunk) {
   if (chunk <= 0) chunk = 8192;
@@ -228,10 +348,18 @@ int64_t flce_chunk(int64_t BT, int64_t chunk) {
 // after the loop (the chunks' D_c^T side by side, lay.defer) or per chunk into
 // an fp32 accumulator, the result rounded once into dWo. X [BT, H] and W [V, H]
 // are K-contiguous.
+//
+// The rows are compacted first: X holds the live rows of the caller's hidden
+// states in order (rowmap[i] is row i's original row), zero rows after them,
+// and *n_live (device memory) is their count. Every GEMM is cut to the live
+// rows on the device (tiles past them exit, the dW GEMM's K stops at them),
+// and dX_c is stored straight into the original rows; the caller zeroes the
+// dead rows of dX.
 template <typename T, class RowStep>
 int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, int64_t C, char* ws,
-                    const FlceLayout& lay, bool grad, T* dX, T* dWo, RowStep&& row_step, hipStream_t st) {
-  const int64_t BTp = pad8(BT);
+                    const FlceLayout& lay, bool grad, T* dX, T* dWo, const int* n_live, const int* rowmap,
+                    RowStep&& row_step, hipStream_t st) {
+  const int64_t BTp = pad8(BT), ldx = ld_t(BT);
   T* Lg = (T*)(ws + lay.lg);
   T* Wt = grad ? (T*)(ws + lay.wt) : nullptr;
   T* Xt = grad ? (T*)(ws + lay.xt) : nullptr;
@@ -241,33 +369,37 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
   if (grad) {
     rc = launch_transpose<T>(Wt, W, V, V, H, H, V, st);  // W^T [H, V]
     if (rc) return rc;
-    rc = launch_transpose<T>(Xt, X, BT, BTp, H, H, BTp, st);  // X^T [H, BTp], zero padded
+    rc = launch_transpose<T>(Xt, X, BT, BTp, H, H, ldx, st);  // X^T [H, BTp] (row stride ldx), zero padded
     if (rc) return rc;
   }
   const int64_t nchunks = BT > 0 ? cdiv(BT, C) : 0;
   for (int64_t ci = 0; ci < nchunks; ++ci) {
     const int64_t r0 = ci * C;
     const int64_t cs = std::min<int64_t>(C, BT - r0);
-    // logits_c = X_c W^T
-    rc = launch_gemm<T>(X + r0 * H, W, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Lg, V}, st);
+    // logits_c = X_c W^T (live rows only)
+    rc = launch_gemm<T>(X + r0 * H, W, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Lg, V}, st, n_live, (int)r0);
     if (rc) return rc;
     rc = row_step(Lg, r0, cs);
     if (rc) return rc;
     if (!grad) continue;
-    // dX_c = D_c W
-    rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{dX + r0 * H, H}, st);
+    // dX_c = D_c W, stored into the live rows' original places
+    rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiScatter<T>{dX, H, rowmap + r0}, st, n_live,
+                        (int)r0);
     if (rc) return rc;
     if (lay.defer) {
-      // D_c^T into columns [r0, r0 + cs) of D^T [V, BTp]; the last chunk zero-pads to BTp
-      rc = launch_transpose<T>(Dt + r0, Lg, cs, ci + 1 < nchunks ? cs : BTp - r0, V, V, BTp, st);
+      // D_c^T into columns [r0, r0 + cs) of D^T [V, BTp]; zeros past the live rows
+      rc = launch_transpose<T>(Dt + r0, Lg, cs, ci + 1 < nchunks ? cs : BTp - r0, V, V, ldx, st, n_live, r0);
       if (rc) return rc;
       continue;
     }
-    // dW += D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands
-    const int64_t csp = pad8(cs);
-    rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, csp, st);
+    // dW += D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands, and cut
+    // on the device to the live rows
+    const int64_t csp = pad8(cs), ldd = ld_t(cs);
+    rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, ldd, st, n_live, r0);
     if (rc) return rc;
-    auto dw_gemm = [&](auto epi) { return launch_gemm<T>(Dt, Xt + r0, (int)V, (int)H, (int)csp, csp, BTp, epi, st); };
+    auto dw_gemm = [&](auto epi) {
+      return launch_gemm<T>(Dt, Xt + r0, (int)V, (int)H, (int)csp, ldd, ldx, epi, st, n_live, (int)r0, true);
+    };
     if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
     else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
     else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
@@ -275,7 +407,7 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
     if (rc) return rc;
   }
   if (grad && lay.defer && nchunks > 0) {
-    rc = launch_gemm<T>(Dt, Xt, (int)V, (int)H, (int)BTp, BTp, BTp, EpiStore<T>{dWo, H}, st);
+    rc = launch_gemm<T>(Dt, Xt, (int)V, (int)H, (int)BTp, ldx, ldx, EpiStore<T>{dWo, H}, st, n_live, 0, true);
     if (rc) return rc;
   }
   if (grad && nchunks == 0) {
@@ -298,7 +430,7 @@ extern "C" {
 size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype,
                                                     int with_grad) {
   if (BT < 0 || H <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
-  return flce_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0).total;
+  return flce_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0, 0, true).total;
 }
 
 int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
@@ -319,30 +451,52 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
                                                                              aligned_to(dweight, 16))),
              "hidden, weight and gradients must be 16-byte aligned");
   const int64_t C = flce_chunk(BT, chunk);
-  const FlceLayout lay = flce_layout(BT, H, V, C, 2, grad);
+  const FlceLayout lay = flce_layout(BT, H, V, C, 2, grad, 0, true);
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int* n_valid = (int*)(ws + lay.nvalid);
+  int* n_live = (int*)(ws + lay.nlive);
+  int* rowmap = (int*)(ws + lay.rowmap);
+  int* inv = (int*)(ws + lay.inv);
+  int64_t* tc = (int64_t*)(ws + lay.tc);
+  float* sc = (float*)(ws + lay.sc);
+  float* lc = (float*)(ws + lay.lc);
   // every target equal to ignore_index is ignored (fused_linear_cross_entropy.py:121,62-65);
   // unlike the CrossEntropy op, -1 is not a "no ignore" sentinel here
   const int has_ignore = 1;
 
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
+    T* Xc = (T*)(ws + lay.xc);
     int rc = HK_OK;
-    if (BT > 0) rc = count_valid_launch(n_valid, targets, BT, ignore_index, has_ignore, st);
-    if (rc) return rc;
-    // per-row loss; with gradients, D_c = (softmax - onehot) * s * row_scale written over the logits
+    if (BT > 0) {
+      rc = count_valid_launch(n_valid, targets, BT, ignore_index, has_ignore, st);
+      if (rc) return rc;
+      // the non-ignored rows, compacted: their hidden rows, targets and row scales
+      rc = ce_compact_launch(rowmap, inv, n_live, targets, BT, ignore_index, st);
+      if (rc) return rc;
+      rc = gather_rows<T>(Xc, (const T*)hidden, rowmap, n_live, BT, H, st);
+      if (rc) return rc;
+      hipLaunchKernelGGL(gather_ce_kernel, dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 1024)), dim3(256), 0, st,
+                         tc, sc, targets, row_scale, rowmap, n_live);
+      rc = check_launch("gather_ce_kernel");
+      if (rc) return rc;
+    }
+    // per-row loss of the compacted rows; with gradients, D_c = (softmax - onehot) * s * row_scale
+    // written over the logits
     auto ce_step = [&](T* Lg, int64_t r0, int64_t cs) {
-      return ce_rows_launch(grad ? (void*)Lg : nullptr, loss_rows + r0, Lg, targets + r0, cs, V, V, V, ignore_index,
-                            has_ignore, n_valid, grad && reduction == HK_REDUCTION_MEAN,
-                            row_scale ? row_scale + r0 : nullptr, dtype, st);
+      return ce_rows_launch(grad ? (void*)Lg : nullptr, lc + r0, Lg, tc + r0, cs, V, V, V, ignore_index, has_ignore,
+                            n_valid, grad && reduction == HK_REDUCTION_MEAN, row_scale ? sc + r0 : nullptr, dtype, st,
+                            n_live, r0);
     };
-    rc = chunked_lm_head<T>((const T*)hidden, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden,
-                            (T*)dweight, ce_step, st);
+    rc = chunked_lm_head<T>(Xc, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden, (T*)dweight, n_live,
+                            rowmap, ce_step, st);
+    if (rc) return rc;
+    // losses back in row order (ignored rows 0); ignored rows of dhidden are zero
+    rc = finish_rows<T>(grad ? (T*)dhidden : nullptr, loss_rows, lc, inv, BT, H, st);
     if (rc) return rc;
     if (loss_out) {
       // with gradients the rows already carry 1/max(n_valid,1) for 'mean'; without, divide here
@@ -495,18 +649,29 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   void* scratch = ws + lay.extra;
+  int* n_live = (int*)(ws + lay.nlive);
+  int* rowmap = (int*)(ws + lay.rowmap);
+  int* inv = (int*)(ws + lay.inv);
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
+    T* Xc = (T*)(ws + lay.xc);
     int rc = grpo_prep_launch(in, scratch, st);
     if (rc) return rc;
-    // rows of the chunk are positions r0.. of the (B, L+1) hidden rows: the
-    // GRPO row kernel writes the per-token results and, with gradients, the
-    // dlogits over the logits (zero rows at masked tokens and at position L)
+    // the live positions (l < L, mask != 0), compacted: only their logits are computed
+    rc = grpo_compact_launch(rowmap, inv, n_live, in, st);
+    if (rc) return rc;
+    rc = gather_rows<T>(Xc, (const T*)hidden, rowmap, n_live, BT, H, st);
+    if (rc) return rc;
+    // compacted row q of a chunk is position rowmap[r0 + q]: the GRPO row kernel
+    // writes that token's results and, with gradients, its dlogits over the logits
     auto grpo_step = [&](T* Lg, int64_t r0, int64_t cs) {
-      return grpo_rows_launch(grad ? (void*)Lg : nullptr, Lg, r0, cs, in, scratch, dtype, st);
+      return grpo_rows_launch(grad ? (void*)Lg : nullptr, Lg, r0, cs, in, scratch, dtype, st, rowmap, n_live);
     };
-    rc = chunked_lm_head<T>((const T*)hidden, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden,
-                            (T*)dweight, grpo_step, st);
+    rc = chunked_lm_head<T>(Xc, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden, (T*)dweight, n_live,
+                            rowmap, grpo_step, st);
+    if (rc) return rc;
+    // masked tokens and position L: zero rows of dhidden
+    rc = finish_rows<T>(grad ? (T*)dhidden : nullptr, nullptr, nullptr, inv, BT, H, st);
     if (rc) return rc;
     return grpo_finalize_launch(in, scratch, loss_out, kl_out, clip_out, lse_rows, loss_rows, kl_rows, clip_rows,
                                 st);

@@ -52,7 +52,23 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 struct Shape {
   int M, N, K;
   int64_t lda, ldb;
+  // optional device-side bound: with lim, M (or K when lim_k) is cut to
+  // *lim - lim_off rows (K rounded up to a whole stage; the operands must hold
+  // zeros there). The grid is sized for the host M; the tiles of the cut M are
+  // rastered over the first workgroups (so they spread over every XCD) and the
+  // rest exit.
+  const int* lim = nullptr;
+  int lim_off = 0;
+  int lim_k = 0;
 };
+
+// Applies Shape::lim (a uniform scalar load); kq: the K granule of the kernel.
+__device__ __forceinline__ void apply_bound(Shape& g, int kq) {
+  if (!g.lim) return;
+  const int v = max(0, *g.lim - g.lim_off);
+  if (g.lim_k) g.K = min(g.K, max(kq, (v + kq - 1) / kq * kq));
+  else g.M = min(g.M, v);
+}
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int GROUP_M_ = 16>
 struct Cfg {
@@ -360,7 +376,9 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
   __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[kLdsBytes];
   T* const lds = reinterpret_cast<T*>(lds_raw);
 
+  apply_bound(g, 8);
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
+  if ((int)blockIdx.x >= nbm * nbn) return;  // uniform: past a device-side bound
   int tm, tn;
   tile_of_block<C::GROUP_M>(nbm, nbn, &tm, &tn);
   const int m0 = tm * C::BM, n0 = tn * C::BN;
@@ -495,7 +513,9 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
                     kBBytes + (C::TN - 1) * 32 * C::BK * (int)sizeof(T) < 65536,
                 "stage and row offsets fit the 16-bit LDS immediate");
 
+  apply_bound(g, C::BK);
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
+  if ((int)blockIdx.x >= nbm * nbn) return;  // uniform: past a device-side bound
   int tm, tn;
   tile_of_block<C::GROUP_M>(nbm, nbn, &tm, &tn);
   const int m0 = tm * C::BM, n0 = tn * C::BN;
@@ -659,7 +679,8 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
 // K-contiguous (A[m][k], B[n][k]); lda / ldb are the leading dimensions of
 // whichever layout is used.
 template <typename T, class C = DefaultCfg, bool AMN = false, bool BMN = false, class Epi>
-int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st) {
+int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
+           const int* lim = nullptr, int lim_off = 0, bool lim_k = false) {
   if (M == 0 || N == 0) return 0;
   if (K <= 0) {
     set_error("gemm: K (%d) must be positive", K);
@@ -689,7 +710,7 @@ int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb
     return true;
   };
   if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
-  Shape g{M, N, K, lda, ldb};
+  Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
   if constexpr (!AMN && !BMN && C::STAGES == 2 && C::BK == 64) {
     if (K % C::BK == 0) {

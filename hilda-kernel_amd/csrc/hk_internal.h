@@ -14,9 +14,16 @@ int count_valid_launch(int* n_valid, const int64_t* targets, int64_t rows, int64
 // dlogits = (softmax - onehot) * s * row_scale[r] (row_scale nullable), s = 1/max(n_valid,1)
 // when scale_by_n_valid, else 1; ignored rows give 0 and a zero row. dlogits may alias logits.
 // Without dlogits: loss_rows = lse - x_t (0 if ignored), no scaling.
+// rows_lim (nullable): a device-side bound, only rows < *rows_lim - rows_off are processed.
 int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const int64_t* targets, int64_t rows,
                    int64_t V, int64_t ld_in, int64_t ld_out, int64_t ignore_index, int has_ignore, const int* n_valid,
-                   int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st);
+                   int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st,
+                   const int* rows_lim = nullptr, int64_t rows_off = 0);
+
+// Stable compaction of the rows whose target is not ignore_index: rowmap[0 .. n)
+// the live rows in order, inv[r] their place (-1 for ignored rows), *n_live = n.
+int ce_compact_launch(int* rowmap, int* inv, int* n_live, const int64_t* targets, int64_t rows,
+                      int64_t ignore_index, hipStream_t st);
 
 // out[0] = sum(v[0:n]) (fp64 accumulation), / max(n_valid, 1) when divide
 int sum_rows_launch(float* out, const float* v, int64_t n, const int* n_valid, int divide, hipStream_t st);
@@ -62,9 +69,16 @@ int grpo_prep_launch(const GrpoInputs& in, void* scratch, hipStream_t st);
 
 // Rows [row0, row0 + nrows) of the B x (L+1) logits rows, `logits` pointing at
 // row row0 (row stride V): per-token results into scratch and, with dlogits
-// (may alias logits), the gradient rows at unit upstream gradient.
+// (may alias logits), the gradient rows at unit upstream gradient. With rowmap
+// (a compaction, see grpo_compact_launch) row q of the launch is position
+// rowmap[row0 + q], and only q < *n_live - row0 exist.
 int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nrows, const GrpoInputs& in,
-                     void* scratch, int dtype, hipStream_t st);
+                     void* scratch, int dtype, hipStream_t st, const int* rowmap = nullptr,
+                     const int* n_live = nullptr);
+
+// Stable compaction of the live positions (l < L, mask != 0) of the B x (L+1)
+// rows: rowmap, inv and *n_live as for ce_compact_launch.
+int grpo_compact_launch(int* rowmap, int* inv, int* n_live, const GrpoInputs& in, hipStream_t st);
 
 // The reductions (loss, kl_mean, clip_ratio) and the per-token rows [B, L].
 int grpo_finalize_launch(const GrpoInputs& in, const void* scratch, float* loss_out, float* kl_out, float* clip_out,

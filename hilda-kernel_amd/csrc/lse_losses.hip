@@ -367,7 +367,14 @@ struct CeArgs {
   int64_t rows, V, ld_in, ld_out, ignore_index;
   int has_ignore;
   int scale_by_n_valid;
+  const int* rows_lim;  // optional device-side bound: rows cut to *rows_lim - rows_off
+  int64_t rows_off;
 };
+
+// Applies CeArgs::rows_lim (a uniform scalar load) to the kernel's copy of the arguments.
+__device__ __forceinline__ void ce_bound(CeArgs& a) {
+  if (a.rows_lim) a.rows = min(a.rows, max((int64_t)0, (int64_t)*a.rows_lim - a.rows_off));
+}
 
 __device__ __forceinline__ float ce_scale(const CeArgs& a) {
   return a.scale_by_n_valid ? 1.f / fmaxf((float)*a.n_valid, 1.f) : 1.f;
@@ -382,6 +389,7 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
   // same thread overwrites it, and a row's stores are issued before the next
   // row's loads of the same vector, so the pointers are not declared __restrict__.
   __shared__ float red[4 * (BLOCK / kWave)];
+  ce_bound(a);
   const float scale = ce_scale(a);
   const int64_t G = gridDim.x;
   auto is_live = [&](int64_t t) { return !(a.has_ignore && t == a.ignore_index) && t >= 0 && t < a.V; };
@@ -457,6 +465,7 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
 template <typename T, int VEC, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void ce_fwd_kernel(const T* __restrict__ logits, CeArgs a) {
   __shared__ float red[BLOCK / kWave];
+  ce_bound(a);
   for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
     const T* in = logits + row * a.ld_in;
     const float lse = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red) * kLn2;
@@ -611,6 +620,10 @@ struct GrpoHot {
   GrpoOut* out;
   int64_t B, L, V;
   int64_t row0, nrows;  // the launch covers rows [row0, row0 + nrows) of the (B, L+1) positions
+  // optional compaction: launch row q is position rowmap[row0 + q], and only
+  // q < *nlim - row0 exist (a device-side bound)
+  const int* rowmap;
+  const int* nlim;
   float inv_T, beta, eps_lo, eps_hi;
   int has_old;
 };
@@ -647,18 +660,20 @@ template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT, bool GRAD>
 __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
                                                      GrpoHot a) {
   __shared__ float red[4 * (BLOCK / kWave)];
-  const int64_t rows = a.nrows;  // row below: local to the launch
+  const int64_t rows =
+      a.nlim ? min(a.nrows, max((int64_t)0, (int64_t)*a.nlim - a.row0)) : a.nrows;  // row below: local to the launch
   const int64_t G = gridDim.x;
   const float c = kLog2e * a.inv_T;
   // a row is live when it is a token position (l < L) with a nonzero mask
+  auto pos = [&](int64_t row) -> int64_t { return a.rowmap ? a.rowmap[a.row0 + row] : a.row0 + row; };
   auto live = [&](int64_t row, GrpoTok* tk) {
-    const int64_t g = a.row0 + row, b = g / (a.L + 1), l = g - b * (a.L + 1);
+    const int64_t g = pos(row), b = g / (a.L + 1), l = g - b * (a.L + 1);
     if (l == a.L) return false;
     *tk = a.tok[b * a.L + l];
     return tk->m != 0.f;
   };
   auto token = [&](int64_t row) {
-    const int64_t g = a.row0 + row, b = g / (a.L + 1);
+    const int64_t g = pos(row), b = g / (a.L + 1);
     return g - b;  // b * L + l
   };
   // dead rows: a zero gradient row (never read) and zero results
@@ -666,7 +681,7 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
     GrpoTok tk{};
     if (!live(row, &tk)) {
       if constexpr (GRAD) fill_row<T, VEC, BLOCK>(dlogits + row * a.V, (int)a.V, 0.f);
-      const int64_t g = a.row0 + row, b = g / (a.L + 1), l = g - b * (a.L + 1);
+      const int64_t g = pos(row), b = g / (a.L + 1), l = g - b * (a.L + 1);
       if (l < a.L && threadIdx.x == 0) a.out[b * a.L + l] = GrpoOut{0.f, 0.f, 0.f, 0.f};
     }
   }
@@ -749,8 +764,10 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
   }
 }
 
-// One block per sequence b: len_b = sum_l mask[b, l], then the token records.
-__global__ __launch_bounds__(1024) void grpo_prep_kernel(GrpoArgs a, GrpoTok* __restrict__ tok) {
+// One block per sequence b: len_b = sum_l mask[b, l], then the token records;
+// the per-token results start at zero (rows a launch skips keep them).
+__global__ __launch_bounds__(1024) void grpo_prep_kernel(GrpoArgs a, GrpoTok* __restrict__ tok,
+                                                         GrpoOut* __restrict__ res) {
   __shared__ float red[16];
   const int64_t b = blockIdx.x;
   float s = 0.f;
@@ -769,6 +786,7 @@ __global__ __launch_bounds__(1024) void grpo_prep_kernel(GrpoArgs a, GrpoTok* __
     t.m = a.mask ? load_mask(a.mask, a.mask_dt, b * a.mask_sB + l * a.mask_sL) : 1.f;
     t.gs = t.m * inv_len * a.inv_T;
     tok[b * a.L + l] = t;
+    res[b * a.L + l] = GrpoOut{0.f, 0.f, 0.f, 0.f};
   }
 }
 
@@ -825,6 +843,55 @@ __global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const G
     clip_out[0] = (float)(t[3] / d);
   }
 }
+
+// Stable compaction of the live rows of [0, rows): rowmap[0 .. n) lists them in
+// order, inv[r] is a row's place in that list (-1 when dead), *n_live = n. One
+// block: per 1024 rows, a wave ballot and an exclusive scan of the 16 wave counts.
+template <class Pred>
+__global__ __launch_bounds__(1024) void compact_rows_kernel(int* __restrict__ rowmap, int* __restrict__ inv,
+                                                            int* __restrict__ n_live, int64_t rows, Pred pred) {
+  __shared__ int wcount[16];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  int base = 0;  // live rows before this 1024-row step (every lane keeps the same value)
+  for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
+    const int64_t r = r0 + threadIdx.x;
+    const bool f = r < rows && pred(r);
+    const uint64_t bal = __ballot(f);
+    if (lane == 0) wcount[wave] = __popcll(bal);
+    __syncthreads();
+    int before = base, total = base;
+    for (int w = 0; w < 16; ++w) {
+      before += w < wave ? wcount[w] : 0;
+      total += wcount[w];
+    }
+    const int k = before + __popcll(bal & ((1ull << lane) - 1ull));
+    if (r < rows) {
+      inv[r] = f ? k : -1;
+      if (f) rowmap[k] = (int)r;
+    }
+    base = total;
+    __syncthreads();  // wcount is rewritten by the next step
+  }
+  if (threadIdx.x == 0) *n_live = base;
+}
+
+// CrossEntropy rows: live unless the target is the ignore index.
+struct CeLive {
+  const int64_t* targets;
+  int64_t ignore_index;
+  __device__ bool operator()(int64_t r) const { return targets[r] != ignore_index; }
+};
+
+// GRPO positions of the (B, L+1) rows: live when l < L and the mask is nonzero.
+struct GrpoLive {
+  const void* mask;
+  int mask_dt;
+  int64_t mask_sB, mask_sL, L;
+  __device__ bool operator()(int64_t r) const {
+    const int64_t b = r / (L + 1), l = r - b * (L + 1);
+    return l < L && (!mask || load_mask(mask, mask_dt, b * mask_sB + l * mask_sL) != 0.f);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // host-side configuration
@@ -950,14 +1017,17 @@ int grpo_check(const GrpoInputs& in) {
 
 int grpo_prep_launch(const GrpoInputs& in, void* scratch, hipStream_t st) {
   if (in.L == 0) return HK_OK;
-  hipLaunchKernelGGL(grpo_prep_kernel, dim3((unsigned)in.B), dim3(1024), 0, st, grpo_args(in), (GrpoTok*)scratch);
+  hipLaunchKernelGGL(grpo_prep_kernel, dim3((unsigned)in.B), dim3(1024), 0, st, grpo_args(in), (GrpoTok*)scratch,
+                     (GrpoOut*)((char*)scratch + (size_t)(in.B * in.L) * sizeof(GrpoTok)));
   return check_launch("grpo_prep_kernel");
 }
 
 int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nrows, const GrpoInputs& in,
-                     void* scratch, int dtype, hipStream_t st) {
+                     void* scratch, int dtype, hipStream_t st, const int* rowmap, const int* n_live) {
   if (nrows <= 0) return HK_OK;
   GrpoHot h{};
+  h.rowmap = rowmap;
+  h.nlim = n_live;
   h.tok = (const GrpoTok*)scratch;
   h.out = (GrpoOut*)((char*)scratch + (size_t)(in.B * in.L) * sizeof(GrpoTok));
   h.B = in.B;
@@ -1012,6 +1082,19 @@ int grpo_finalize_launch(const GrpoInputs& in, const void* scratch, float* loss_
   return check_launch("grpo_finalize_kernel");
 }
 
+int ce_compact_launch(int* rowmap, int* inv, int* n_live, const int64_t* targets, int64_t rows,
+                      int64_t ignore_index, hipStream_t st) {
+  hipLaunchKernelGGL(compact_rows_kernel<CeLive>, dim3(1), dim3(1024), 0, st, rowmap, inv, n_live, rows,
+                     CeLive{targets, ignore_index});
+  return check_launch("compact_rows_kernel");
+}
+
+int grpo_compact_launch(int* rowmap, int* inv, int* n_live, const GrpoInputs& in, hipStream_t st) {
+  hipLaunchKernelGGL(compact_rows_kernel<GrpoLive>, dim3(1), dim3(1024), 0, st, rowmap, inv, n_live,
+                     in.B * (in.L + 1), GrpoLive{in.mask, in.mask_dt, in.mask_sB, in.mask_sL, in.L});
+  return check_launch("compact_rows_kernel");
+}
+
 int count_valid_launch(int* n_valid, const int64_t* targets, int64_t rows, int64_t ignore_index, int has_ignore,
                        hipStream_t st) {
   hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, n_valid, targets, rows, ignore_index,
@@ -1026,10 +1109,13 @@ int sum_rows_launch(float* out, const float* v, int64_t n, const int* n_valid, i
 
 int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const int64_t* targets, int64_t rows,
                    int64_t V, int64_t ld_in, int64_t ld_out, int64_t ignore_index, int has_ignore, const int* n_valid,
-                   int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st) {
+                   int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st, const int* rows_lim,
+                   int64_t rows_off) {
   if (rows == 0) return HK_OK;
   const int es = esize(dtype);
   CeArgs a{};
+  a.rows_lim = rows_lim;
+  a.rows_off = rows_off;
   a.targets = targets;
   a.loss_rows = loss_rows;
   a.n_valid = n_valid;

@@ -138,3 +138,33 @@ def test_flce_c5_config():
     dh_ref = logits.grad.to(torch.bfloat16).double() @ wc.double()  # d(sum of rows) / dh for the sample
     assert_close(hg.grad[idx].float() * n_valid, dh_ref, name="dhidden rows * n_valid", **tol(torch.bfloat16))
     assert rel_fro(hg.grad[idx].float() * n_valid, dh_ref) < 1e-2
+
+
+@pytest.mark.parametrize("BT,H,V,chunk,dead", [
+    (600, 64, 520, 64, (100, 400)),    # several chunks wholly ignored; dW through the fp32 accumulator
+    (300, 128, 1000, 64, (64, 256)),   # the same with every chunk's D^T kept and one dW GEMM
+    (256, 64, 264, 128, (0, 256)),     # nothing live
+])
+def test_flce_dead_chunks(BT, H, V, chunk, dead):
+    """Ignored rows are compacted away before the GEMMs: whole chunks past the live rows, live rows that end
+    mid-chunk, and the two dW paths give the oracle's result with exact zeros on ignored rows."""
+    dtype = torch.bfloat16
+    h, w, t = _case(BT, H, V, dtype, BT + V, ignore_frac=0.1)
+    t[dead[0]:dead[1]] = -100
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, "sum")
+    dev = gpu()
+    loss, gi, gw, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "sum",
+                                                            compute_grad=True, chunk=chunk)
+    print(f"dead chunks BT={BT} H={H} V={V} chunk={chunk} dead={dead}", flush=True)
+    assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
+    tt = tol(dtype)
+    assert_close(gi, dh_ref, name="dhidden", **tt)
+    assert_close(gw, dw_ref, name="dweight", **tt)
+    if dw_ref.abs().sum() > 0:
+        assert rel_fro(gi, dh_ref) < 1e-2 and rel_fro(gw, dw_ref) < 1e-2
+    else:
+        assert torch.count_nonzero(gw).item() == 0
+    assert torch.count_nonzero(gi[(t == -100).to(dev)]).item() == 0
+    rows, _, _, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "none",
+                                                          compute_grad=False, chunk=chunk)
+    assert torch.count_nonzero(rows[(t == -100).to(dev)]).item() == 0

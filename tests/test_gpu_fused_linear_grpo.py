@@ -214,3 +214,26 @@ def test_fused_linear_grpo_f3_config():
         d = z.grad[0, 0] / (lens[b].item() * B)
         dh_ref = d.to(torch.bfloat16).float() @ wc
         assert rel_fro(gh[b, l].float().cpu(), dh_ref) < 1e-2, (b, l)
+
+
+@pytest.mark.parametrize("chunk", [16, 8192])
+def test_fused_linear_grpo_masked_sequences(chunk):
+    """A wholly masked sequence and masks that leave later chunks empty: only the live positions reach the
+    GEMMs, the rest get zero dhidden rows, and the loss matches the oracle."""
+    B, L, H, V = 4, 11, 64, 512
+    dtype = torch.bfloat16
+    h, w, ids, adv, old, ref, mask = _case(B, L, H, V, dtype, 91)
+    mask[1] = 0   # a sequence with no live token
+    mask[2:] = 0  # and everything after it
+    mask[0, 5:] = 0
+    outs, (dh_ref, dw_ref) = _oracle(h, w, ids, adv, old, ref, mask, 1.0, 0.1, 0.2, 0.2)
+    dev = gpu()
+    args = (ids.to(dev), adv.to(dev), old.to(dev), ref.to(dev), mask.to(dev), 1.0, 0.1, 0.2, 0.2)
+    loss, kl, clip, gh, gw, rows = flg.fused_linear_grpo_forward(h.to(dev), w.to(dev), *args, chunk=chunk)
+    assert_close(loss, outs[0], name="loss", rtol=2e-3, atol=2e-3)
+    assert_close(kl, outs[1], name="kl_mean", rtol=2e-3, atol=2e-3)
+    assert rel_fro(gh, dh_ref) < 1e-2 and rel_fro(gw, dw_ref) < 1e-2
+    live = torch.zeros(B, L + 1, dtype=torch.bool)
+    live[:, :L] = mask.bool()
+    assert torch.count_nonzero(gh.cpu()[~live]).item() == 0
+    assert torch.count_nonzero(rows[1].cpu()[~mask.bool()]).item() == 0

@@ -66,6 +66,68 @@ def test_argument_validation_without_gpu():
 
 
 @needs_lib
+def test_argument_validation_losses_without_gpu():
+    """The loss-family, fused-linear and AttnRes entry points reject bad arguments before any HIP call."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    ws = ctypes.c_void_p(1 << 20)
+    # CrossEntropy / GRPO
+    _expect_einval(lib.hk_cross_entropy_fwd_grad(p, p, p, p, p, 4, 8, 8, 8, -100, 1, 7, ws, 1 << 20, None), "dtype")
+    grpo = [p, p, None, p, p, p, p, p, p, p, 8, 1, p, None, 0, 0, None, 0, 0, None, 0, 0, 0, 2, 8, 16]
+    _expect_einval(lib.hk_grpo_loss_fwd(*grpo, 1.0, 0.1, 0.2, 0.2, 2, ws, 1 << 20, None), "ref_logp")
+    _expect_einval(lib.hk_grpo_loss_fwd(*grpo, 0.0, 0.0, 0.2, 0.2, 2, ws, 1 << 20, None), "temperature")
+    # KLDiv / JSD / GeGLU
+    _expect_einval(lib.hk_kl_div_fwd(p, p, p, p, 4, 8, 8, 8, 0, 1e-10, 9, 2, None), "reduction")
+    _expect_einval(lib.hk_kl_div_fwd(p, p, p, p, 4, 8, 4, 8, 0, 1e-10, 1, 2, None), "shape")
+    _expect_einval(lib.hk_jsd_fwd(p, p, p, p, p, None, -100, 1.5, 4, 8, 8, 8, 8, 2, ws, 1 << 20, None), "beta")
+    _expect_einval(lib.hk_geglu_fwd(p, p, p, -1, 2, None), "element count")
+    # FusedLinearCE: hidden [BT, H], weight [V, H]
+    flce = [p, p, p, p, p, p, p, None]
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 0, 0, ws, 1 << 20, None),
+                   "bf16 and fp16")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 60, 128, -100, 1, 2, 0, ws, 1 << 20, None),
+                   "multiples of 8")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 5, 2, 0, ws, 1 << 20, None),
+                   "reduction")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 2, 0, ws, 64, None),
+                   "workspace too small")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(p, p, p, None, p, p, p, None, 64, 64, 128, -100, 1, 2, 0, ws,
+                                                     1 << 20, None), "computed together")
+    # FusedLinear-GRPO: hidden (B, L+1, H), weight [V, H]
+    head = [p, p, p, p, p, p, p, p, p, p, p, p, 8, 1, p, None, 0, 0, None, 0, 0, None, 0, 0, 0, 2, 7]
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 0, 0, ws, 1 << 30, None),
+                   "bf16 and fp16")
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 100, 1.0, 0.0, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
+                   "multiples of 8")
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.1, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
+                   "ref_logp")
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, -1.0, 0.0, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
+                   "temperature")
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 2, 0, ws, 64, None),
+                   "workspace too small")
+    # AttnRes
+    _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 33, 16, 64, 1e-6, 2, None), "1..32 blocks")
+    _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 4, 16, 12, 1e-6, 2, None), "multiple of 8")
+    _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 4, 16, 8 * 256 * 8 + 8, 1e-6, 2, None), "at most")
+    _expect_einval(lib.hk_attn_res_bwd(p, p, p, p, p, p, p, p, p, 4, 16, 64, 2, ws, 8, None), "workspace too small")
+
+
+@needs_lib
+def test_fused_linear_workspace_queries():
+    lib = _lib.load()
+    # bf16/fp16 only; a gradient call needs more (transposed operands, D^T) than a loss-only call
+    assert lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 0, 1) == 0
+    fwd = lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 2, 0)
+    bwd = lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 2, 1)
+    assert 0 < fwd < bwd
+    # C5 keeps every chunk's D^T (4.2 GB) instead of one chunk's plus the 2.1 GB fp32 accumulator: no more memory
+    assert bwd < 12 * 2**30
+    assert lib.hk_fused_linear_grpo_workspace_size(16, 1023, 4096, 151936, 0, 2, 1) > 0
+    assert lib.hk_fused_linear_grpo_workspace_size(0, 1023, 4096, 151936, 0, 2, 1) == 0
+    assert lib.hk_attn_res_bwd_workspace_size(8192, 4096) % (2 * 4096 * 4) == 0
+
+
+@needs_lib
 def test_workspace_query_is_pure():
     lib = _lib.load()
     # atomic path: one [cols] fp64 row; partial path (bf16 -> fp32 accumulators): one row per row group
@@ -81,7 +143,23 @@ def test_workspace_query_is_pure():
 
 def test_ops_refuse_cpu_tensors():
     """No CPU path: every op raises on host tensors instead of computing there."""
-    from kernels import hilda_rms_norm, hilda_swiglu, hilda_rope, hilda_fused_add_rms_norm
+    from kernels import (hilda_rms_norm, hilda_swiglu, hilda_rope, hilda_fused_add_rms_norm, hilda_geglu,
+                         hilda_cross_entropy, hilda_grpo_loss, hilda_kl_div, hilda_jsd, hilda_attn_res,
+                         hilda_fused_linear_cross_entropy, hilda_fused_linear_jsd, hilda_fused_linear_grpo_loss)
+    bf = torch.bfloat16
+    lg = torch.randn(4, 16)
+    t = torch.zeros(4, dtype=torch.int64)
+    for call in (lambda: hilda_geglu(lg, lg), lambda: hilda_cross_entropy(lg, t),
+                 lambda: hilda_kl_div(lg, lg), lambda: hilda_jsd(lg, lg),
+                 lambda: hilda_grpo_loss(torch.randn(2, 3, 16), torch.zeros(2, 2, dtype=torch.int64),
+                                         torch.zeros(2)),
+                 lambda: hilda_attn_res(torch.randn(2, 1, 4, 16), torch.ones(16), torch.ones(16)),
+                 lambda: hilda_fused_linear_cross_entropy(lg.to(bf), lg.to(bf), t),
+                 lambda: hilda_fused_linear_jsd(lg.to(bf), lg.to(bf), lg.to(bf), lg.to(bf)),
+                 lambda: hilda_fused_linear_grpo_loss(torch.randn(2, 3, 16).to(bf), lg.to(bf),
+                                                      torch.zeros(2, 2, dtype=torch.int64), torch.zeros(2))):
+        with pytest.raises(RuntimeError, match="ROCm GPU"):
+            call()
     x = torch.randn(4, 8)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         hilda_rms_norm(x, torch.ones(8))

@@ -221,10 +221,12 @@ __global__ __launch_bounds__(kLogitLanes) void jsd_logits_kernel(float* __restri
                                                                  const int64_t* __restrict__ labels,
                                                                  int64_t ignore_index, const int* __restrict__ n_valid,
                                                                  int64_t n_all, float beta, float inv_temp,
-                                                                 int64_t cols, int64_t ld) {
+                                                                 int64_t cols, int64_t ld,
+                                                                 const int* __restrict__ rows_lim, int64_t rows_off) {
   constexpr int NW = kLogitLanes / kWave;
   __shared__ float red[2 * NW];
   const int64_t row = blockIdx.x;
+  if (rows_lim && row >= (int64_t)*rows_lim - rows_off) return;  // past a device-side bound (uniform)
   T* s = ls + row * ld;
   const T* t = lt + row * ld;
   if (labels != nullptr && labels[row] == ignore_index) {
@@ -328,7 +330,7 @@ int scaled_sum_launch(float* out, const float* v, int64_t n, float scale, hipStr
 
 int jsd_logits_launch(float* loss_rows, void* ls, const void* lt, const int64_t* labels, int64_t ignore_index,
                       const int* n_valid, int64_t n_all, float beta, float temperature, int64_t rows, int64_t cols,
-                      int64_t ld, int write, int dtype, hipStream_t st) {
+                      int64_t ld, int write, int dtype, hipStream_t st, const int* rows_lim, int64_t rows_off) {
   if (rows == 0) return HK_OK;
   return dispatch_t(dtype, [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
@@ -338,7 +340,7 @@ int jsd_logits_launch(float* loss_rows, void* ls, const void* lt, const int64_t*
     auto go = [&](auto vc, auto mc, auto wc) {
       hipLaunchKernelGGL((jsd_logits_kernel<T, decltype(vc)::value, decltype(mc)::value, decltype(wc)::value>),
                          dim3((unsigned)rows), dim3(kLogitLanes), 0, st, loss_rows, (T*)ls, (const T*)lt, labels,
-                         ignore_index, n_valid, n_all, beta, 1.0f / temperature, cols, ld);
+                         ignore_index, n_valid, n_all, beta, 1.0f / temperature, cols, ld, rows_lim, rows_off);
     };
     auto by_mode = [&](auto vc, auto wc) {
       if (mode == 0) go(vc, std::integral_constant<int, 0>{}, wc);

@@ -289,28 +289,28 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
   return L;
 }
 
+// FusedLinearJSD: the shared chunk engine's workspace, then the JSD pieces:
+// per-row losses (compacted order with labels), the teacher logits chunk, and
+// with labels the compacted teacher rows and labels.
 struct FljsdLayout {
-  size_t nvalid, rows, ls, lt, wt, xt, dt, dwacc, total;
+  FlceLayout base;
+  size_t lc, lt, xtc, labc, total;
 };
 
-FljsdLayout fljsd_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad) {
+FljsdLayout fljsd_layout(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int es, bool grad) {
   FljsdLayout L{};
-  size_t off = 0;
+  L.base = flce_layout(BT, H, V, chunk, es, grad);
+  size_t off = L.base.total;
   auto take = [&](size_t bytes) {
     const size_t o = off;
     off += align256(bytes);
     return o;
   };
-  L.nvalid = take(256);
-  L.rows = take((size_t)std::max<int64_t>(BT, 1) * 4);
-  L.ls = take((size_t)chunk * V * es);
+  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
+  L.lc = take(bt * 4);
   L.lt = take((size_t)chunk * V * es);
-  if (grad) {
-    L.wt = take((size_t)H * V * es);
-    L.xt = take((size_t)H * pad8(BT) * es);
-    L.dt = take((size_t)V * pad8(chunk) * es);
-    L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
-  }
+  L.xtc = take((size_t)pad8(BT) * Ht * es);
+  L.labc = take(bt * 8);
   L.total = off;
   return L;
 }
@@ -349,12 +349,13 @@ int64_t flce_chunk(int64_t BT, int64_t chunk) {
 // an fp32 accumulator, the result rounded once into dWo. X [BT, H] and W [V, H]
 // are K-contiguous.
 //
-// The rows are compacted first: X holds the live rows of the caller's hidden
-// states in order (rowmap[i] is row i's original row), zero rows after them,
-// and *n_live (device memory) is their count. Every GEMM is cut to the live
-// rows on the device (tiles past them exit, the dW GEMM's K stops at them),
-// and dX_c is stored straight into the original rows; the caller zeroes the
-// dead rows of dX.
+// With rowmap, the rows are compacted first: X holds the live rows of the
+// caller's hidden states in order (rowmap[i] is row i's original row), zero
+// rows after them, and *n_live (device memory) is their count. Every GEMM is
+// cut to the live rows on the device (tiles past them exit, the dW GEMM's K
+// stops at them), and dX_c is stored straight into the original rows; the
+// caller zeroes the dead rows of dX. Without rowmap (n_live null too) every
+// row of X is processed in place.
 template <typename T, class RowStep>
 int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, int64_t C, char* ws,
                     const FlceLayout& lay, bool grad, T* dX, T* dWo, const int* n_live, const int* rowmap,
@@ -383,8 +384,11 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
     if (rc) return rc;
     if (!grad) continue;
     // dX_c = D_c W, stored into the live rows' original places
-    rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiScatter<T>{dX, H, rowmap + r0}, st, n_live,
-                        (int)r0);
+    if (rowmap)
+      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiScatter<T>{dX, H, rowmap + r0}, st, n_live,
+                          (int)r0);
+    else
+      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{dX + r0 * H, H}, st);
     if (rc) return rc;
     if (lay.defer) {
       // D_c^T into columns [r0, r0 + cs) of D^T [V, BTp]; zeros past the live rows
@@ -510,9 +514,10 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
 }
 
 
-size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype, int with_grad) {
-  if (BT < 0 || H <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
-  return fljsd_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0).total;
+size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int dtype,
+                                          int with_grad) {
+  if (BT < 0 || H <= 0 || Ht <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
+  return fljsd_layout(BT, H, Ht, V, flce_chunk(BT, chunk), 2, with_grad != 0).total;
 }
 
 int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
@@ -534,78 +539,67 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
                  aligned_to(t_weight, 16) && (!grad || (aligned_to(dinput, 16) && aligned_to(dweight, 16))),
              "inputs, weights and gradients must be 16-byte aligned");
   const int64_t C = flce_chunk(BT, chunk);
-  const FljsdLayout lay = fljsd_layout(BT, H, V, C, 2, grad);
+  const FljsdLayout lay = fljsd_layout(BT, H, Ht, V, C, 2, grad);
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  int* n_valid = (int*)(ws + lay.nvalid);
-  float* loss_rows = (float*)(ws + lay.rows);
-  const int64_t BTp = pad8(BT);
+  const FlceLayout& lb = lay.base;
+  int* n_valid = (int*)(ws + lb.nvalid);
+  // with labels the ignored rows are compacted away (the engine's row map and live count)
+  int* n_live = labels ? (int*)(ws + lb.nlive) : nullptr;
+  int* rowmap = labels ? (int*)(ws + lb.rowmap) : nullptr;
+  int* inv = (int*)(ws + lb.inv);
+  float* lc = (float*)(ws + lay.lc);
+  int64_t* labc = (int64_t*)(ws + lay.labc);
 
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
     const T* Xs = (const T*)s_input;
-    const T* Ws = (const T*)s_weight;
     const T* Xt_in = (const T*)t_input;
     const T* Wt_in = (const T*)t_weight;
-    T* Ls = (T*)(ws + lay.ls);
     T* Lt = (T*)(ws + lay.lt);
+    T* Xtc = (T*)(ws + lay.xtc);
+    T* Xsc = (T*)(ws + lb.xc);
     int rc = HK_OK;
-    // n counts the labels that are not ignore_index over all BT rows (fused_linear_jsd.py:137-141)
-    if (labels && BT > 0) rc = count_valid_launch(n_valid, labels, BT, ignore_index, 1, st);
+    if (labels && BT > 0) {
+      // n counts the labels that are not ignore_index over all BT rows (fused_linear_jsd.py:137-141)
+      rc = count_valid_launch(n_valid, labels, BT, ignore_index, 1, st);
+      if (rc) return rc;
+      rc = ce_compact_launch(rowmap, inv, n_live, labels, BT, ignore_index, st);
+      if (rc) return rc;
+      rc = gather_rows<T>(Xsc, Xs, rowmap, n_live, BT, H, st);
+      if (rc) return rc;
+      rc = gather_rows<T>(Xtc, Xt_in, rowmap, n_live, BT, Ht, st);
+      if (rc) return rc;
+      hipLaunchKernelGGL(gather_ce_kernel, dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 1024)), dim3(256), 0, st,
+                         labc, nullptr, labels, nullptr, rowmap, n_live);
+      rc = check_launch("gather_ce_kernel");
+      if (rc) return rc;
+    }
+    float* lrows = labels ? lc : (float*)(ws + lay.lc);
+    // row step: the teacher logits of the chunk's rows (fused_linear_jsd.py:159-160), then the log-softmaxes,
+    // JSD and, with gradients, the student dlogits over the student logits (:163-199)
+    auto jsd_step = [&](T* Ls, int64_t r0, int64_t cs) {
+      const T* xt = (labels ? Xtc : Xt_in) + r0 * Ht;
+      int r = launch_gemm<T>(xt, Wt_in, (int)cs, (int)V, (int)Ht, Ht, Ht, EpiStore<T>{Lt, V}, st, n_live, (int)r0);
+      if (r) return r;
+      return jsd_logits_launch(lrows + r0, Ls, Lt, labels ? labc + r0 : nullptr, ignore_index, n_valid, BT, beta,
+                               temperature, cs, V, V, grad ? 1 : 0, dtype, st, n_live, r0);
+    };
+    rc = chunked_lm_head<T>(labels ? Xsc : Xs, (const T*)s_weight, BT, H, V, C, ws, lb, grad, (T*)dinput,
+                            (T*)dweight, n_live, rowmap, jsd_step, st);
     if (rc) return rc;
-    T* WsT = grad ? (T*)(ws + lay.wt) : nullptr;
-    T* XsT = grad ? (T*)(ws + lay.xt) : nullptr;
-    T* Dt = grad ? (T*)(ws + lay.dt) : nullptr;
-    float* dwacc = (grad && lay.dwacc) ? (float*)(ws + lay.dwacc) : nullptr;
-    if (grad) {
-      rc = launch_transpose<T>(WsT, Ws, V, V, H, H, V, st);  // Ws^T [H, V]
+    if (labels) {
+      // losses back in row order (ignored rows 0); ignored rows of dinput are zero
+      float* rows_out = (float*)(ws + lay.labc);  // the compacted labels are no longer needed
+      rc = finish_rows<T>(grad ? (T*)dinput : nullptr, rows_out, lc, inv, BT, H, st);
       if (rc) return rc;
-      rc = launch_transpose<T>(XsT, Xs, BT, BTp, H, H, BTp, st);  // Xs^T [H, BTp], zero padded
-      if (rc) return rc;
-    }
-    const int64_t nchunks = BT > 0 ? cdiv(BT, C) : 0;
-    for (int64_t ci = 0; ci < nchunks; ++ci) {
-      const int64_t r0 = ci * C;
-      const int64_t cs = std::min<int64_t>(C, BT - r0);
-      // student and teacher logits of the chunk (fused_linear_jsd.py:159-160)
-      rc = launch_gemm<T>(Xs + r0 * H, Ws, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Ls, V}, st);
-      if (rc) return rc;
-      rc = launch_gemm<T>(Xt_in + r0 * Ht, Wt_in, (int)cs, (int)V, (int)Ht, Ht, Ht, EpiStore<T>{Lt, V}, st);
-      if (rc) return rc;
-      // log-softmaxes, JSD and, with gradients, the student dlogits over Ls (:163-199)
-      rc = jsd_logits_launch(loss_rows + r0, Ls, Lt, labels ? labels + r0 : nullptr, ignore_index, n_valid, BT, beta,
-                             temperature, cs, V, V, grad ? 1 : 0, dtype, st);
-      if (rc) return rc;
-      if (!grad) continue;
-      // dX_c = D_c Ws (:201-202)
-      rc = launch_gemm<T>(Ls, WsT, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{(T*)dinput + r0 * H, H}, st);
-      if (rc) return rc;
-      // dWs += D_c^T X_c (:203), accumulated in fp32 across chunks
-      const int64_t csp = pad8(cs);
-      rc = launch_transpose<T>(Dt, Ls, cs, csp, V, V, csp, st);
-      if (rc) return rc;
-      auto dw_gemm = [&](auto epi) {
-        return launch_gemm<T>(Dt, XsT + r0, (int)V, (int)H, (int)csp, csp, BTp, epi, st);
-      };
-      T* dWo = (T*)dweight;
-      if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
-      else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
-      else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
-      else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
-      if (rc) return rc;
-    }
-    if (grad && nchunks == 0) {
-      const int64_t n16 = V * H * (int64_t)sizeof(T) / 16;
-      hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n16, 256), 4096)), dim3(256), 0, st,
-                         (u32x4*)dweight, n16);
-      rc = check_launch("zero16_kernel");
-      if (rc) return rc;
+      lrows = rows_out;
     }
     // the rows already carry 1/n (:190)
-    return scaled_sum_rows_launch(loss_out, loss_rows, BT, 1.0f, st);
+    return scaled_sum_rows_launch(loss_out, lrows, BT, 1.0f, st);
   };
   if (dtype == HK_BF16) return run(Tag<__bf16>{});
   return run(Tag<_Float16>{});

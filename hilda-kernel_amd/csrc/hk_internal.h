@@ -35,10 +35,12 @@ int scaled_sum_rows_launch(float* out, const float* v, int64_t n, float scale, h
 // lt (row stride ld, dtype of the ABI): loss_rows = JSD(beta) of the
 // temperature log-softmaxes / n, n = max(*n_valid, 1) with labels, else n_all;
 // with write, ls is overwritten with the student dlogits. Rows labelled
-// ignore_index get loss 0 and zero dlogits.
+// ignore_index get loss 0 and zero dlogits. rows_lim (nullable): a device-side
+// bound, only rows < *rows_lim - rows_off are processed.
 int jsd_logits_launch(float* loss_rows, void* ls, const void* lt, const int64_t* labels, int64_t ignore_index,
                       const int* n_valid, int64_t n_all, float beta, float temperature, int64_t rows, int64_t cols,
-                      int64_t ld, int write, int dtype, hipStream_t st);
+                      int64_t ld, int write, int dtype, hipStream_t st, const int* rows_lim = nullptr,
+                      int64_t rows_off = 0);
 
 // GRPO's per-call inputs (kernels/grpo_loss.py:241-297): ids, old/ref log-probs
 // (fp32, nullable) and mask (any HK_ dtype, nullable) with element strides;

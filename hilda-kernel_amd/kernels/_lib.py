@@ -49,7 +49,7 @@ SIGNATURES = {
     "hk_attn_res_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),
     "hk_attn_res_bwd_workspace_size": (_sz, [_i64, _i64]),
     "hk_attn_res_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _sz, _p]),
-    "hk_fused_linear_jsd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
+    "hk_fused_linear_jsd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
     "hk_fused_linear_jsd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
                                    _i64, _p, _sz, _p]),
     "hk_cross_entropy_workspace_size": (_sz, [_i64]),

@@ -55,7 +55,7 @@ def fused_linear_jsd_forward(student_input, student_weight, teacher_input, teach
     loss = torch.empty((), dtype=torch.float32, device=dev)
     grad_input = torch.empty_like(si) if compute_grad else None
     grad_weight = torch.empty_like(sw) if compute_grad else None
-    ws_bytes = _lib.load().hk_fused_linear_jsd_workspace_size(BT, H, V, chunk, dt, int(compute_grad))
+    ws_bytes = _lib.load().hk_fused_linear_jsd_workspace_size(BT, H, Ht, V, chunk, dt, int(compute_grad))
     ws = torch.empty(max(int(ws_bytes), 256), dtype=torch.uint8, device=dev)
     _lib.call("hk_fused_linear_jsd", loss.data_ptr(), _lib.ptr(grad_input), _lib.ptr(grad_weight), si.data_ptr(),
               sw.data_ptr(), ti.data_ptr(), tw.data_ptr(), _lib.ptr(lab), BT, H, Ht, V, int(ignore_index),

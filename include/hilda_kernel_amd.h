@@ -177,8 +177,9 @@ int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const
                int64_t ignore_index, float beta, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ld_dx,
                int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
-/* Bytes of device workspace hk_fused_linear_jsd needs (chunk <= 0: 8192). */
-size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype, int with_grad);
+/* Bytes of device workspace hk_fused_linear_jsd needs (chunk <= 0: 8192); Ht: the teacher's hidden size. */
+size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int dtype,
+                                          int with_grad);
 
 /* Replaces fused_linear_jsd_forward (fused_linear_jsd.py:114-205): per chunk of
  * `chunk` rows, student logits s_input[BT,H] * s_weight[V,H]^T and teacher

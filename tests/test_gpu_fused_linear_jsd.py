@@ -121,3 +121,29 @@ def test_fused_linear_jsd_all_ignored_and_types():
     assert torch.count_nonzero(sg.grad).item() == 0 and torch.count_nonzero(wg.grad).item() == 0
     with pytest.raises(TypeError):
         hilda_fused_linear_jsd(si.float().to(dev), sw.float().to(dev), ti.float().to(dev), tw.float().to(dev))
+
+
+@pytest.mark.parametrize("labels_kind,BT,chunk", [("dead_block", 600, 64), ("dead_block", 300, 64),
+                                                  ("none", 600, 64)])
+def test_fused_linear_jsd_compaction_and_chunks(labels_kind, BT, chunk):
+    """With labels the ignored rows are compacted away before the GEMMs (here whole chunks of them, on the fp32
+    dW accumulator path at BT 600 and the single-dW-GEMM path at BT 300); without labels every row runs in place."""
+    H, Ht, V = 64, 96, 520
+    dtype = torch.bfloat16
+    si, sw, ti, tw, labels = _case(BT, H, Ht, V, dtype, BT + 7, with_labels=labels_kind != "none")
+    if labels is not None:
+        labels[100:BT - 50] = -100
+    (l_ref,), (dh_ref, dw_ref) = _oracle(si, sw, ti, tw, labels, 0.5, 1.0)
+    dev = gpu()
+    print(f"FLJSD compaction {labels_kind} BT={BT} chunk={chunk}", flush=True)
+    loss, gi, gw = fj.fused_linear_jsd_forward(si.to(dev), sw.to(dev), ti.to(dev), tw.to(dev),
+                                               None if labels is None else labels.to(dev), 0.5, 1.0, -100,
+                                               compute_grad=True, chunk=chunk)
+    n = BT if labels is None else max(int((labels != -100).sum()), 1)
+    assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
+    tt = tol(dtype)
+    assert_close(gi.float() * n, dh_ref * n, name="dinput*n", **tt)
+    assert_close(gw.float() * n, dw_ref * n, name="dweight*n", **tt)
+    assert rel_fro(gi, dh_ref.to(dtype)) < 1e-2 and rel_fro(gw, dw_ref.to(dtype)) < 1e-2
+    if labels is not None:
+        assert torch.count_nonzero(gi[(labels == -100).to(dev)]).item() == 0

@@ -12,7 +12,8 @@ with HIP events and a 512 MiB cache flush between reps; C5 (FusedLinearCE)
 is reported in TFLOP/s of 6*n_valid*H*V. ``roofline`` is the
 dominant kernel of the step (SwiGLU backward), timed per launch with HIP
 events on its stream inside the timed region. ``cpu_baseline`` times the CPU
-PyTorch reference path (the oracle) on a quarter-size C2 sample.
+PyTorch reference path (the oracle) on the full C2 step, repeated for about
+10 s of CPU work.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -385,15 +386,16 @@ def bench_flgrpo(K, dev, reps, flush):
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (the reference's PyTorch path) on the host cores
 # ---------------------------------------------------------------------------
-def cpu_baseline(reps=3):
+def cpu_baseline(seconds=10.0):
+    """The oracle (the reference's PyTorch path) on the full C2 step, fwd+bwd, on every host core: one warm-up
+    step, then whole steps until `seconds` of CPU work (at least 3); throughput over all of them."""
     import oracle
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    scale = 4
-    fa = workloads.c2_fused_add_rms_norm(rows=8192 // scale, device="cpu")
-    rp = workloads.c2_rope(B=4 // scale, device="cpu")
-    sw = workloads.c2_swiglu(rows=8192 // scale, device="cpu")
+    fa = workloads.c2_fused_add_rms_norm(device="cpu")
+    rp = workloads.c2_rope(device="cpu")
+    sw = workloads.c2_swiglu(device="cpu")
     x, r, w = (fa[k].clone().requires_grad_(True) for k in ("x", "r", "w"))
     q = rp["q"].detach().requires_grad_(True)
     k = rp["k"].detach().requires_grad_(True)
@@ -411,11 +413,11 @@ def cpu_baseline(reps=3):
 
     step()
     times = []
-    for _ in range(reps):
+    while len(times) < 3 or sum(times) < seconds:
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    t = sum(times) / len(times)
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -426,8 +428,9 @@ def cpu_baseline(reps=3):
     except OSError:
         pass
     return {"value": round(work / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"C2 step on 1/{scale} of the tokens (FusedAddRMSNorm [2048,4096], RoPE B=1, "
-                      f"SwiGLU [2048,14336]), bf16 PyTorch reference path fwd+bwd, median of {reps}",
+            "sample": f"the full C2 step (FusedAddRMSNorm [8192,4096], RoPE q[4,2048,32,128] k[4,2048,8,128], "
+                      f"SwiGLU [8192,14336]), bf16 PyTorch reference path fwd+bwd: {len(times)} steps in "
+                      f"{sum(times):.1f} s after one warm-up step",
             "seconds_per_step": round(t, 4), "cpu_model": cpu_model}
 
 

@@ -8,10 +8,15 @@
 //   dX_c     = D_c  * (W^T)^T      A = D_c  [C,V],  B = W^T [H,V]
 //   dW      += D_c^T * X_c          A = D_c^T[V,C],  B = X^T [H,C] (columns of X^T)
 // W^T and X^T are transposed once per call, D_c^T once per chunk (tiled LDS
-// transposes, HBM-bound and small next to the GEMMs). dW accumulates in fp32
+// transposes, HBM-bound and small next to the GEMMs). dW is either one GEMM
+// over all rows after the chunk loop (every chunk's D_c^T kept side by side,
+// when that needs no more memory than the alternative) or accumulated in fp32
 // across chunks (the GEMM epilogue reads and writes the accumulator in
-// coalesced 16-byte chunks); the last chunk's epilogue writes the result in
-// the input dtype.
+// coalesced 16-byte chunks; the last chunk's epilogue writes the input dtype).
+//
+// Rows that need no logits (ignored targets or labels, masked GRPO positions)
+// are compacted away on the device first; the GEMMs, transposes and row
+// kernels read the live count from device memory, so the host never waits.
 #include "hk_common.h"
 #include "hk_internal.h"
 #include "gemm_nt.h"

@@ -10,8 +10,10 @@ gradient on the device, with no host synchronisation (the reference uses
 ``torch.equal`` at :197 and ``.item()`` at :121).
 
 Differences from the reference, by design:
-  * grad_weight is accumulated in fp32 across chunks and rounded once (the
-    reference accumulates in bf16, :118,161);
+  * grad_weight is summed in fp32 and rounded once (the reference
+    accumulates in bf16, :118,161);
+  * rows whose target is ignore_index are compacted away on the device
+    before the GEMMs, so they cost no FLOPs;
   * reduction='none' gets correct gradients: the forward computes only the
     per-row losses and the backward recomputes the chunks with each row's
     gradient scaled by its upstream gradient (the reference scales everything

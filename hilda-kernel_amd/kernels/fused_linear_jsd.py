@@ -15,8 +15,10 @@ Differences from the reference, by design:
   * the reference keeps fp32 copies of both logits chunks and of dX
     (:163-188); here the row kernel works from the 16-bit logits in
     registers, in fp32 arithmetic;
-  * grad_weight is accumulated in fp32 across chunks and rounded once (the
-    reference accumulates in the weight dtype, :203);
+  * grad_weight is summed in fp32 and rounded once (the reference
+    accumulates in the weight dtype, :203);
+  * rows labelled ignore_index are compacted away on the device before the
+    GEMMs, so they cost no FLOPs (the reference computes their logits);
   * the label count stays on the device (the reference reads it, :139);
   * bf16/fp16 only: the contractions run on MFMA (fp32 raises TypeError).
 """

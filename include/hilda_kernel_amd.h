@@ -187,7 +187,8 @@ size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int
  * temperature log-softmaxes, JSD(beta) per row divided by
  * max(#labels != ignore_index, 1) (BT without labels), and (dinput, dweight
  * non-null) the student dlogits contracted into dinput [BT,H] and dweight
- * [V,H] (fp32 accumulation across chunks, rounded once). The teacher gets no
+ * [V,H] (summed in fp32, rounded once). Rows labelled ignore_index are
+ * compacted away on the device before the GEMMs. The teacher gets no
  * gradient. *loss_out = the summed loss. Rows are contiguous, H, Ht and V
  * multiples of 8, pointers 16-byte aligned. */
 int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
@@ -322,7 +323,8 @@ size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64
  * rows. With dhidden/dweight (both or neither): the gradients of the reduced
  * loss at unit upstream gradient, each row's gradient further multiplied by
  * row_scale[r] when row_scale is given (reduction 'none' backward). Logits are
- * produced `chunk` rows at a time on bf16/fp16 MFMA; dW accumulates in fp32. */
+ * produced `chunk` rows at a time on bf16/fp16 MFMA, for the rows whose target
+ * is not ignore_index only (compacted on the device); dW is summed in fp32. */
 int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
                                   const void* weight, const int64_t* targets, const float* row_scale, int64_t BT,
                                   int64_t H, int64_t V, int64_t ignore_index, int reduction, int dtype, int64_t chunk,

@@ -37,17 +37,18 @@ constexpr int kNW = kNT / kWave;
 
 constexpr int kU = 4;           // blocks whose loads are in flight together
 
-template <int VEC>
-__device__ __forceinline__ int64_t col_of(int j) {  // column of pack j of this lane
-  return ((int64_t)j * kNT + threadIdx.x) * VEC;
+template <int VEC, int NT = kNT>
+__device__ __forceinline__ int64_t col_of(int j) {  // column of pack j of this lane (NT lanes per token)
+  return ((int64_t)j * NT + threadIdx.x) * VEC;
 }
 
 // Per-block sums over the token's lanes: each lane adds its part for block i
 // with add(i, part) (a wave reduction, then one LDS slot per wave and block);
 // finish(n, out) sums the waves into out[0..n) (LDS). Two barriers per pass,
 // whatever the block count.
-struct BlockSums {
-  float* red;  // kNW * kMaxBlocks floats of LDS
+template <int NW>
+struct BlockSumsT {
+  float* red;  // NW * kMaxBlocks floats of LDS
   __device__ __forceinline__ void add(int i, float part) const {
     part = wave_sum(part);
     if ((threadIdx.x & (kWave - 1)) == 0) red[(threadIdx.x / kWave) * kMaxBlocks + i] = part;
@@ -57,12 +58,13 @@ struct BlockSums {
     if ((int)threadIdx.x < n) {
       float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < kNW; ++w) t += red[w * kMaxBlocks + threadIdx.x];
+      for (int w = 0; w < NW; ++w) t += red[w * kMaxBlocks + threadIdx.x];
       out[threadIdx.x] = t;
     }
     __syncthreads();
   }
 };
+using BlockSums = BlockSumsT<kNW>;
 
 template <typename T, int VEC>
 __global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
@@ -334,8 +336,8 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, f
 // Register-resident forms, used when a token's N rows fit in NB*P packs per
 // lane (64 VGPRs at most): V is read once per direction, the passes work on
 // the registers. Same arithmetic, in the same order, as the streaming forms.
-template <typename T, int VEC, int NB, int P>
-__global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
+template <typename T, int VEC, int NB, int P, int NT>
+__global__ __launch_bounds__(NT) void attn_res_fwd_res_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
                                                                float* __restrict__ rstd_out, const T* __restrict__ V,
                                                                const T* __restrict__ wq, const T* __restrict__ wn,
                                                                int N, int64_t ntok, int64_t D, float eps) {
@@ -343,16 +345,16 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ o
   // token's loads with another's reductions (measured faster than a run of
   // tokens per workgroup with the next token's rows prefetched). The weights
   // are loaded with the rows, so the token costs one memory round trip.
-  __shared__ float red[kNW * kMaxBlocks];
+  __shared__ float red[NT / kWave * kMaxBlocks];
   __shared__ float rs[kMaxBlocks], al[kMaxBlocks];
-  const BlockSums bs{red};
+  const BlockSumsT<NT / kWave> bs{red};
   const int64_t tok = blockIdx.x;
   const int64_t bstride = ntok * D;
   const T* v0 = V + tok * D;
   Pack<T, VEC> pv[NB][P], qv[P], wv[P];
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-    const int64_t c = col_of<VEC>(j) < D ? col_of<VEC>(j) : 0;
+    const int64_t c = col_of<VEC, NT>(j) < D ? col_of<VEC, NT>(j) : 0;
     qv[j] = load_pack<T, VEC>(wq + c);
     wv[j] = load_pack<T, VEC>(wn + c);
   }
@@ -360,14 +362,14 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ o
   for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int j = 0; j < P; ++j)
-      if (i < N && col_of<VEC>(j) < D) pv[i][j] = load_pack<T, VEC>(v0 + i * bstride + col_of<VEC>(j));
+      if (i < N && col_of<VEC, NT>(j) < D) pv[i][j] = load_pack<T, VEC>(v0 + i * bstride + col_of<VEC, NT>(j));
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     if (i < N) {
       float part = 0.f;
 #pragma unroll
       for (int j = 0; j < P; ++j) {
-        if (col_of<VEC>(j) < D) {
+        if (col_of<VEC, NT>(j) < D) {
           float x[VEC];
           unpack(pv[i][j], x);
 #pragma unroll
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ o
       float part = 0.f;
 #pragma unroll
       for (int j = 0; j < P; ++j) {
-        if (col_of<VEC>(j) < D) {
+        if (col_of<VEC, NT>(j) < D) {
           float x[VEC], q[VEC], w[VEC];
           unpack(pv[i][j], x);
           unpack(qv[j], q);
@@ -416,7 +418,7 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ o
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-    const int64_t c = col_of<VEC>(j);
+    const int64_t c = col_of<VEC, NT>(j);
     if (c < D) {
       float h[VEC];
 #pragma unroll
@@ -436,16 +438,16 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_res_kernel(T* __restrict__ o
   }
 }
 
-template <typename T, int VEC, int NB, int P>
-__global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ dV, float* __restrict__ part,
+template <typename T, int VEC, int NB, int P, int NT>
+__global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV, float* __restrict__ part,
                                                                const T* __restrict__ dh, const T* __restrict__ V,
                                                                const T* __restrict__ wq, const T* __restrict__ wn,
                                                                const float* __restrict__ alpha,
                                                                const float* __restrict__ rstd, int N, int64_t ntok,
                                                                int64_t D, int64_t tpb) {
-  __shared__ float red[kNW * kMaxBlocks];
+  __shared__ float red[NT / kWave * kMaxBlocks];
   __shared__ float da[kMaxBlocks], kv[kMaxBlocks], ds[kMaxBlocks], al[kMaxBlocks], rs[kMaxBlocks];
-  const BlockSums bs{red};
+  const BlockSumsT<NT / kWave> bs{red};
   const int64_t bstride = ntok * D;
   Pack<T, VEC> qv[P], wv[P];
   float dwq[P][VEC], dwn[P][VEC];
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ d
   for (int j = 0; j < P; ++j) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) dwq[j][e] = dwn[j][e] = 0.f;
-    const int64_t c = col_of<VEC>(j) < D ? col_of<VEC>(j) : 0;
+    const int64_t c = col_of<VEC, NT>(j) < D ? col_of<VEC, NT>(j) : 0;
     qv[j] = load_pack<T, VEC>(wq + c);
     wv[j] = load_pack<T, VEC>(wn + c);
   }
@@ -463,7 +465,7 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ d
   // one token overlap the stores and reductions of the previous one
   Pack<T, VEC> pv[NB][P], gv[P];
   auto load_token = [&](int64_t t, int i, int j) {
-    const int64_t c = col_of<VEC>(j) < D ? col_of<VEC>(j) : 0;  // in-bounds address; unused when >= D
+    const int64_t c = col_of<VEC, NT>(j) < D ? col_of<VEC, NT>(j) : 0;  // in-bounds address; unused when >= D
     if (i < 0) gv[j] = load_pack<T, VEC>(dh + t * D + c);
     else pv[i][j] = load_pack<T, VEC>(V + i * bstride + t * D + c);
   };
@@ -488,7 +490,7 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ d
         float p = 0.f;
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-          if (col_of<VEC>(j) < D) {
+          if (col_of<VEC, NT>(j) < D) {
             float x[VEC], y[VEC];
             unpack(pv[i][j], x);
             unpack(gv[j], y);
@@ -512,7 +514,7 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ d
         float pk = 0.f;
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-          if (col_of<VEC>(j) < D) {
+          if (col_of<VEC, NT>(j) < D) {
             float x[VEC], q[VEC], w[VEC];
             unpack(pv[i][j], x);
             unpack(qv[j], q);
@@ -527,7 +529,7 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ d
     bs.finish(N, kv);
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-      const int64_t c = col_of<VEC>(j);
+      const int64_t c = col_of<VEC, NT>(j);
       float y[VEC], q[VEC], w[VEC];
       unpack(gv[j], y);
       unpack(qv[j], q);
@@ -558,7 +560,7 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_res_kernel(T* __restrict__ d
   float* pq = part + (int64_t)blockIdx.x * 2 * D;
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-    const int64_t c = col_of<VEC>(j);
+    const int64_t c = col_of<VEC, NT>(j);
     if (c < D) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
@@ -628,6 +630,25 @@ int dispatch_p(int P, F&& f) {
   return f(std::integral_constant<int, 8>{});
 }
 
+// The register-resident kernels hold NB x P 16-byte packs per lane; a token
+// spreads over NT lanes. f(NT, NB, P) for the first form that fits N blocks of
+// D columns, or -2 when none does (the streaming kernels then run).
+template <typename T, class F>
+int dispatch_resident(int N, int64_t D, F&& f) {
+  using std::integral_constant;
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t P256 = cdiv(D / VEC, 256), P512 = cdiv(D / VEC, 512);
+  if (N <= 8 && P256 <= 2)
+    return f(integral_constant<int, 256>{}, integral_constant<int, 8>{}, integral_constant<int, 2>{});
+  if (N <= 16 && P256 <= 1)
+    return f(integral_constant<int, 256>{}, integral_constant<int, 16>{}, integral_constant<int, 1>{});
+  if (N <= 8 && P512 <= 2)
+    return f(integral_constant<int, 512>{}, integral_constant<int, 8>{}, integral_constant<int, 2>{});
+  if (N <= 16 && P512 <= 1)
+    return f(integral_constant<int, 512>{}, integral_constant<int, 16>{}, integral_constant<int, 1>{});
+  return -2;
+}
+
 // workgroups walking runs of tokens: per_cu per CU (what the register use lets run at once)
 int64_t token_groups(int64_t ntok, int per_cu) {
   const int dev = current_device();
@@ -659,14 +680,13 @@ int hk_attn_res_fwd(void* out, float* alpha, float* rstd, const void* V, const v
     if (n_tokens == 0) return HK_OK;
     const int P = packs_per_lane<T>(D);
     const int N = (int)n_blocks;
-    auto resident = [&](auto nbc, auto pc) {
-      constexpr int NB = decltype(nbc)::value, PP = decltype(pc)::value;
-      hipLaunchKernelGGL((attn_res_fwd_res_kernel<T, VEC, NB, PP>), dim3((unsigned)n_tokens), dim3(kNT), 0, st,
+    const int rc = dispatch_resident<T>(N, D, [&](auto ntc, auto nbc, auto pc) {
+      constexpr int NT = decltype(ntc)::value, NB = decltype(nbc)::value, PP = decltype(pc)::value;
+      hipLaunchKernelGGL((attn_res_fwd_res_kernel<T, VEC, NB, PP, NT>), dim3((unsigned)n_tokens), dim3(NT), 0, st,
                          (T*)out, alpha, rstd, (const T*)V, (const T*)w_query, (const T*)w_norm, N, n_tokens, D, eps);
       return check_launch("attn_res_fwd_res_kernel");
-    };
-    if (N <= 8 && P <= 2) return resident(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
-    if (N <= 16 && P <= 1) return resident(std::integral_constant<int, 16>{}, std::integral_constant<int, 1>{});
+    });
+    if (rc != -2) return rc;
     hipLaunchKernelGGL((attn_res_fwd_kernel<T, VEC>), dim3((unsigned)n_tokens), dim3(kNT), 0, st, (T*)out, alpha,
                        rstd, (const T*)V, (const T*)w_query, (const T*)w_norm, N, P, n_tokens, D, eps);
     return check_launch("attn_res_fwd_kernel");
@@ -696,36 +716,37 @@ int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, con
     HK_REQUIRE(aligned_to(V, 16) && aligned_to(dV, 16) && aligned_to(dh, 16) && aligned_to(w_query, 16) &&
                    aligned_to(w_norm, 16),
                "16-byte aligned tensors expected");
-    const int64_t groups = bwd_groups(n_tokens);
-    const int64_t tpb = n_tokens > 0 ? cdiv(n_tokens, groups) : 0;
-    const int64_t used = n_tokens > 0 ? cdiv(n_tokens, tpb) : 1;
     float* part = (float*)workspace;
-    const int N = (int)n_blocks, Pl = packs_per_lane<T>(D);
-    auto resident = [&](auto nbc, auto pc) {
-      constexpr int NB = decltype(nbc)::value, PP = decltype(pc)::value;
-      hipLaunchKernelGGL((attn_res_bwd_res_kernel<T, VEC, NB, PP>), dim3((unsigned)used), dim3(kNT), 0, st, (T*)dV,
-                         part, (const T*)dh, (const T*)V, (const T*)w_query, (const T*)w_norm, alpha, rstd, N,
-                         n_tokens, D, tpb);
-      return check_launch("attn_res_bwd_res_kernel");
-    };
-    if (n_tokens > 0 && N <= 8 && Pl <= 2) {
-      const int rc = resident(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
-      if (rc) return rc;
-    } else if (n_tokens > 0 && N <= 16 && Pl <= 1) {
-      const int rc = resident(std::integral_constant<int, 16>{}, std::integral_constant<int, 1>{});
-      if (rc) return rc;
-    } else if (n_tokens > 0) {
-      const int rc = dispatch_p(packs_per_lane<T>(D), [&](auto pc) {
-        constexpr int PP = decltype(pc)::value;
-        hipLaunchKernelGGL((attn_res_bwd_kernel<T, VEC, PP>), dim3((unsigned)used), dim3(kNT), 0, st, (T*)dV, part,
-                           (const T*)dh, (const T*)V, (const T*)w_query, (const T*)w_norm, alpha, rstd,
-                           (int)n_blocks, n_tokens, D, tpb);
-        return check_launch("attn_res_bwd_kernel");
+    const int N = (int)n_blocks;
+    int64_t used = 0;  // partial dW rows written
+    if (n_tokens > 0) {
+      int rc = dispatch_resident<T>(N, D, [&](auto ntc, auto nbc, auto pc) {
+        constexpr int NT = decltype(ntc)::value, NB = decltype(nbc)::value, PP = decltype(pc)::value;
+        // the register use lets two 256-lane workgroups, or one 512-lane one, run per CU
+        const int64_t groups = token_groups(n_tokens, NT == 256 ? 2 : 1);
+        const int64_t tpb = cdiv(n_tokens, groups);
+        used = cdiv(n_tokens, tpb);
+        hipLaunchKernelGGL((attn_res_bwd_res_kernel<T, VEC, NB, PP, NT>), dim3((unsigned)used), dim3(NT), 0, st,
+                           (T*)dV, part, (const T*)dh, (const T*)V, (const T*)w_query, (const T*)w_norm, alpha, rstd,
+                           N, n_tokens, D, tpb);
+        return check_launch("attn_res_bwd_res_kernel");
       });
+      if (rc == -2) {
+        const int64_t groups = bwd_groups(n_tokens);
+        const int64_t tpb = cdiv(n_tokens, groups);
+        used = cdiv(n_tokens, tpb);
+        rc = dispatch_p(packs_per_lane<T>(D), [&](auto pc) {
+          constexpr int PP = decltype(pc)::value;
+          hipLaunchKernelGGL((attn_res_bwd_kernel<T, VEC, PP>), dim3((unsigned)used), dim3(kNT), 0, st, (T*)dV, part,
+                             (const T*)dh, (const T*)V, (const T*)w_query, (const T*)w_norm, alpha, rstd, N, n_tokens,
+                             D, tpb);
+          return check_launch("attn_res_bwd_kernel");
+        });
+      }
       if (rc) return rc;
     }
     hipLaunchKernelGGL((attn_res_reduce_kernel<T>), dim3((unsigned)cdiv(2 * D, 64)), dim3(1024), 0, st,
-                       (T*)dw_query, (T*)dw_norm, (const float*)part, n_tokens > 0 ? used : 0, D);
+                       (T*)dw_query, (T*)dw_norm, (const float*)part, used, D);
     return check_launch("attn_res_reduce_kernel");
   });
 }

@@ -3,8 +3,9 @@
 Follows benchmarks/bench_attn_res.py's forward and backward checks (its
 configs (N, B, T, D) = (4|8, 2, 64, 4096|8192) in fp16/bf16/fp32, lines 72-135,
 against pytorch_attn_res with autograd) and adds odd D, every block count
-bound (1, 8, 9, 17, 32), a list of blocks as input, w_norm != 1 and the
-module's parameters.
+bound (1, 8, 9, 16, 17, 32), a list of blocks as input, w_norm != 1 and the
+module's parameters. The shapes reach every kernel form: register-resident
+with 256 or 512 lanes per token (full and partial last packs) and streaming.
 """
 import pytest
 import torch
@@ -46,7 +47,8 @@ def _check(V, wq, wn, dh, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("N,D", [(1, 256), (4, 4096), (8, 4096), (9, 1000), (17, 520), (32, 2048), (8, 8192)])
+@pytest.mark.parametrize("N,D", [(1, 256), (4, 4096), (8, 4096), (9, 1000), (17, 520), (32, 2048), (8, 8192),
+                                 (16, 4096), (8, 6000), (16, 3000)])
 def test_attn_res(dtype, N, D):
     if dtype == torch.float32 and D > 8 * 256 * 4:
         pytest.skip("fp32 rows are limited to 8192 columns")

@@ -34,6 +34,29 @@ int cu_count(int device) {
   return g_cu_count[device];
 }
 
+int blocks_per_cu(const void* kernel, int block) {
+  // a handful of kernels ask; a linear table under one lock is enough
+  constexpr int kSlots = 256;
+  static std::mutex mu;
+  static const void* keys[kSlots];
+  static int vals[kSlots];
+  static int used = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (keys[i] == kernel) return vals[i];
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess || n < 1) {
+    (void)hipGetLastError();  // not a launch failure: fall back to one block a CU
+    n = 1;
+  }
+  if (used < kSlots) {
+    keys[used] = kernel;
+    vals[used] = n;
+    ++used;
+  }
+  return n;
+}
+
 int current_device() {
   int d = -1;
   hipError_t e = hipGetDevice(&d);

@@ -255,6 +255,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // ---------------------------------------------------------------------------
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int cu_count(int device);            // cached per device
+int blocks_per_cu(const void* kernel, int block);  // resident blocks a CU (occupancy), cached per kernel
 int current_device();                // -1 on failure (error recorded)
 int check_launch(const char* what);  // 0 or hipError_t after a launch
 

@@ -3,9 +3,11 @@
 // gradient fused into the forward pass.
 //
 // Row engine. One workgroup owns one vocabulary row at a time (persistent
-// grid, rows strided by gridDim.x). When the row fits, it is held in VGPRs:
-// NCH packed 16-byte vectors per lane over a 256- or 1024-lane workgroup
-// (a 128256-entry bf16 row is 16 vectors per lane of 1024 lanes, 64 VGPRs),
+// grid of exactly the blocks the CUs hold, rows strided by gridDim.x). When
+// the row fits, it is held in VGPRs: NCH packed 16-byte vectors per lane over
+// a 256-, 512- or 1024-lane workgroup, the smallest form that holds the row
+// (a 32000-entry bf16 row is 16 vectors per lane of 256 lanes, four blocks a
+// CU; a 128256-entry row 16 vectors per lane of 1024 lanes, 64 VGPRs),
 // so the row crosses HBM once: read, max, sum of 2^(x*c - m), then the
 // gradient (p - onehot) * g is written straight from the registers. Rows that
 // do not fit use a streaming variant that keeps a per-lane online (max, sum)
@@ -109,23 +111,24 @@ struct RowRegs {
     for (int j = 0; j < NCH; ++j) make_opaque(v[j]);
   }
 
-  // max over the row of x * c (c > 0)
-  __device__ __forceinline__ float local_max(int n, float c) const {
+  // This lane's (max, sum) of x*c in the log2 domain, computed exactly as
+  // lse2_to_exp does but leaving the registers as they are (a forward-only
+  // pass refills them with the next row right after).
+  __device__ __forceinline__ void lse2_local(int n, float c, float* m_out, float* s_out) {
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      if (j * kSpan < n) {  // uniform
+      if (j * kSpan < n) {
         float x[VEC];
         unpack(v[j], x);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) m = fmaxf(m, x[e]);
+        for (int e = 0; e + 1 < VEC; e += 2) m = max3(m, x[e], x[e + 1]);
+        if constexpr (VEC & 1) m = fmaxf(m, x[VEC - 1]);
       }
     }
-    return m * c;
-  }
-
-  // sum over the row of 2^(x*c - m2)
-  __device__ __forceinline__ float local_sumexp(int n, float c, float m2) const {
+    m *= c;
+    opaque();
+    const float mo = m == -INFINITY ? 0.f : m;
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -133,10 +136,12 @@ struct RowRegs {
         float x[VEC];
         unpack(v[j], x);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) s += exp2_fast(fmaf(x[e], c, -m2));
+        for (int e = 0; e < VEC; ++e) s += exp2_fast(fmaf(x[e], c, -mo));
       }
+      __builtin_amdgcn_sched_barrier(0);  // one vector's floats live at a time
     }
-    return s;
+    *m_out = m;
+    *s_out = s;
   }
 
   // This lane's (max, sum) of x*c in the log2 domain, m = max and
@@ -306,16 +311,6 @@ __device__ __forceinline__ float block_lse2(float m, float s, float* red, int pa
   return m + log2_fast(s);
 }
 
-// Row log-sum-exp in the log2 domain of (x * c), register-resident.
-template <typename T, int VEC, int NCH, int BLOCK>
-__device__ __forceinline__ float row_lse2(RowRegs<T, VEC, NCH, BLOCK>& r, int n, float c, float* red) {
-  const float m2 = block_max<BLOCK / kWave>(r.local_max(n, c), red);
-  r.opaque();
-  const float s = block_sum<BLOCK / kWave>(r.local_sumexp(n, c, m2), red);
-  r.opaque();
-  return m2 + log2_fast(s);
-}
-
 // Streaming row log-sum-exp (any length): per-lane online (max, sum), then a block combine.
 template <typename T, int VEC, int BLOCK>
 __device__ __forceinline__ float row_lse2_stream(const T* __restrict__ row, int n, float c, float* red) {
@@ -352,6 +347,37 @@ __device__ __forceinline__ void store_grad_stream(T* __restrict__ out, const T* 
       x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
     }
     store_pack_nt<T, VEC>(out + col, pack<T, VEC>(x));
+  }
+}
+
+// Forward-only row loop, register-resident: the block's rows (row, row + G,
+// ...) that next_live accepts, each held in VGPRs. A row's lanes reduce their
+// (max, sum) from the registers, then refill them with the next row before the
+// block-wide combine, so the next row's loads are in flight during the
+// exchange and the caller's per-row epilogue. emit(row, lse2) runs on every
+// lane with the row's log2-sum-exp of x * c; pre(row) runs before the row's
+// reduction (for loads that should overlap it).
+template <typename T, int VEC, int NCH, int BLOCK, class RowPtr, class NextLive, class Pre, class Emit>
+__device__ __forceinline__ void lse_rows_resident(int n, float c, int64_t rows, float* red, RowPtr row_ptr,
+                                                  NextLive next_live, Pre pre, Emit emit) {
+  int64_t row = next_live((int64_t)blockIdx.x);
+  if (row >= rows) return;
+  RowRegs<T, VEC, NCH, BLOCK> r;
+  r.load(row_ptr(row), n);
+  int parity = 0;
+  for (;;) {
+    const int64_t next = next_live(row + (int64_t)gridDim.x);
+    auto ctx = pre(row);
+    float m, s;
+    r.lse2_local(n, c, &m, &s);
+    r.opaque();
+    __builtin_amdgcn_sched_barrier(0);  // the refill may not start before the row is reduced (register reuse)
+    if (next < rows) r.load(row_ptr(next), n);
+    const float lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+    parity ^= 1;
+    emit(row, lse2, ctx);
+    if (next >= rows) break;
+    row = next;
   }
 }
 
@@ -461,22 +487,44 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
   }
 }
 
-// Inference forward (kernels/cross_entropy.py:32-65): lse and lse - x_t (0 if ignored).
-template <typename T, int VEC, int BLOCK>
+// Inference forward (kernels/cross_entropy.py:32-65): lse and lse - x_t (0 if
+// ignored, NaN for a target out of range). Every row's lse is computed,
+// ignored rows included.
+struct TargetLogit {
+  int64_t t;
+  float xt;
+};
+
+template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void ce_fwd_kernel(const T* __restrict__ logits, CeArgs a) {
-  __shared__ float red[BLOCK / kWave];
+  __shared__ float red[4 * (BLOCK / kWave)];
   ce_bound(a);
-  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
-    const T* in = logits + row * a.ld_in;
-    const float lse = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red) * kLn2;
+  auto target = [&](int64_t row) {
+    const int64_t t = a.targets[row];
+    const bool in_range = t >= 0 && t < a.V;
+    return TargetLogit{t, in_range ? to_f32<T>(logits[row * a.ld_in + t]) : 0.f};
+  };
+  auto emit = [&](int64_t row, float lse2, TargetLogit tx) {
     if (threadIdx.x == 0) {
-      const int64_t t = a.targets[row];
+      const float lse = lse2 * kLn2;
       float loss;
-      if (a.has_ignore && t == a.ignore_index) loss = 0.f;
-      else if (t < 0 || t >= a.V) loss = NAN;
-      else loss = lse - to_f32<T>(in[t]);
+      if (a.has_ignore && tx.t == a.ignore_index) loss = 0.f;
+      else if (tx.t < 0 || tx.t >= a.V) loss = NAN;
+      else loss = lse - tx.xt;
       if (a.lse_rows) a.lse_rows[row] = lse;
       a.loss_rows[row] = loss;
+    }
+  };
+  if constexpr (RESIDENT) {
+    lse_rows_resident<T, VEC, NCH, BLOCK>(
+        row_len(a.V), kLog2e, a.rows, red, [&](int64_t row) { return logits + row * a.ld_in; },
+        [](int64_t q) { return q; }, target, emit);
+  } else {
+    // the target logit is read after the row (its address waits on the target
+    // load, which would hold back the row's loads behind it)
+    for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+      const float lse2 = row_lse2_stream<T, VEC, BLOCK>(logits + row * a.ld_in, (int)a.V, kLog2e, red);
+      if (threadIdx.x == 0) emit(row, lse2, target(row));
     }
   }
 }
@@ -578,23 +626,45 @@ struct GrpoArgs {
 };
 
 // logp[b, l] = x[b, l, id] / T - logsumexp(x[b, l, :] / T) for unmasked l < L
-// (kernels/grpo_loss.py:29-62); logits are (B, L+1, V) contiguous.
-template <typename T, int VEC, int BLOCK>
+// (kernels/grpo_loss.py:29-62); logits are (B, L+1, V) contiguous. Masked
+// tokens get 0 and their rows are not read.
+template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void selective_log_softmax_kernel(const T* __restrict__ logits, GrpoArgs a) {
-  __shared__ float red[BLOCK / kWave];
+  __shared__ float red[4 * (BLOCK / kWave)];
   const int64_t rows = a.B * a.L;
   const float c = kLog2e * a.inv_T;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+  auto row_ptr = [&](int64_t r) {
     const int64_t b = r / a.L, l = r - b * a.L;
-    if (a.mask && load_mask(a.mask, a.mask_dt, b * a.mask_sB + l * a.mask_sL) == 0.f) {
-      if (threadIdx.x == 0) a.logp_out[r] = 0.f;
-      continue;
-    }
-    const T* in = logits + (b * (a.L + 1) + l) * a.V;
-    const float lse = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, c, red) * kLn2;
-    if (threadIdx.x == 0) {
-      const int64_t id = a.ids[b * a.ids_sB + l * a.ids_sL];
-      a.logp_out[r] = (id >= 0 && id < a.V) ? to_f32<T>(in[id]) * a.inv_T - lse : NAN;
+    return logits + (b * (a.L + 1) + l) * a.V;
+  };
+  auto masked = [&](int64_t r) {
+    const int64_t b = r / a.L, l = r - b * a.L;
+    return a.mask && load_mask(a.mask, a.mask_dt, b * a.mask_sB + l * a.mask_sL) == 0.f;
+  };
+  auto target = [&](int64_t r) {
+    const int64_t b = r / a.L, l = r - b * a.L;
+    const int64_t id = a.ids[b * a.ids_sB + l * a.ids_sL];
+    const bool in_range = id >= 0 && id < a.V;
+    return TargetLogit{id, in_range ? to_f32<T>(row_ptr(r)[id]) : 0.f};
+  };
+  auto emit = [&](int64_t r, float lse2, TargetLogit tx) {
+    if (threadIdx.x == 0)
+      a.logp_out[r] = (tx.t >= 0 && tx.t < a.V) ? tx.xt * a.inv_T - lse2 * kLn2 : NAN;
+  };
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x)
+    if (threadIdx.x == 0 && masked(r)) a.logp_out[r] = 0.f;
+  if constexpr (RESIDENT) {
+    const int64_t G = gridDim.x;
+    auto next_live = [&](int64_t q) {
+      while (q < rows && masked(q)) q += G;
+      return q;
+    };
+    lse_rows_resident<T, VEC, NCH, BLOCK>(row_len(a.V), c, rows, red, row_ptr, next_live, target, emit);
+  } else {
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+      if (masked(r)) continue;
+      const float lse2 = row_lse2_stream<T, VEC, BLOCK>(row_ptr(r), (int)a.V, c, red);
+      if (threadIdx.x == 0) emit(r, lse2, target(r));  // (after the row, as in the CE kernel)
     }
   }
 }
@@ -731,7 +801,35 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       if (next >= rows) break;
       row = next;
     }
+  } else if constexpr (RESIDENT && BLOCK < 1024) {
+    // forward only: the same (max, sum) arithmetic as the gradient path, so
+    // both give bitwise equal results; the next row loads during the combine
+    auto next_live = [&](int64_t from) {
+      int64_t q = from;
+      GrpoTok t{};
+      while (q < rows && !live(q, &t)) q += G;
+      return q;
+    };
+    struct Ctx {
+      GrpoTok tk;
+      float xid;
+    };
+    auto pre = [&](int64_t row) {
+      const GrpoTok tk = a.tok[token(row)];
+      return Ctx{tk, tk.id >= 0 ? to_f32<T>(logits[row * a.V + tk.id]) : 0.f};
+    };
+    auto emit = [&](int64_t row, float lse2, const Ctx& x) {
+      const float lse = lse2 * kLn2;
+      const float logp = x.tk.id >= 0 ? x.xid * a.inv_T - lse : NAN;
+      float dlogp;
+      const GrpoOut res = grpo_terms(a, x.tk, lse, logp, &dlogp);
+      if (threadIdx.x == 0) a.out[token(row)] = res;
+    };
+    lse_rows_resident<T, VEC, NCH, BLOCK>(
+        row_len(a.V), c, rows, red, [&](int64_t row) { return logits + row * a.V; }, next_live, pre, emit);
   } else {
+    // streaming, or forward only on 1024-lane rows: there the refill's extra
+    // register pressure spills, so each row loads after the previous one
     int parity = 0;
     for (int64_t row = blockIdx.x; row < rows; row += G) {
       GrpoTok tk{};
@@ -744,7 +842,6 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
       float lse2;
       if constexpr (RESIDENT) {
-        // the same reduction as the gradient path, so both give bitwise equal results
         RowRegs<T, VEC, NCH, BLOCK> r;
         r.load(in, n);
         float m, s;
@@ -920,12 +1017,11 @@ RowCfg choose_row_cfg(int64_t V, int esize, bool vec_ok) {
   RowCfg c{1024, 0, vec_ok ? 16 / esize : 1};
   if (!vec_ok) return c;
   const int64_t nv = V / c.vec;
-  static const int small[] = {1, 2, 4, 8};
-  for (int n : small)
-    if (nv <= 256LL * n) return RowCfg{256, n, c.vec};
-  static const int big[] = {12, 16, 20, 24};
-  for (int n : big)
-    if (nv <= 1024LL * n) return RowCfg{1024, n, c.vec};
+  static const RowCfg table[] = {{256, 1, 0},  {256, 2, 0},   {256, 4, 0},   {256, 8, 0},   {256, 12, 0},
+                                 {256, 16, 0}, {512, 12, 0},  {512, 16, 0},  {1024, 12, 0}, {1024, 16, 0},
+                                 {1024, 20, 0}, {1024, 24, 0}};
+  for (const RowCfg& t : table)
+    if (nv <= (int64_t)t.block * t.nch) return RowCfg{t.block, t.nch, c.vec};
   return c;
 }
 
@@ -939,6 +1035,13 @@ int dispatch_cfg(const RowCfg& c, F&& f) {
       case 2: return f(integral_constant<int, 256>{}, integral_constant<int, 2>{});
       case 4: return f(integral_constant<int, 256>{}, integral_constant<int, 4>{});
       case 8: return f(integral_constant<int, 256>{}, integral_constant<int, 8>{});
+      case 12: return f(integral_constant<int, 256>{}, integral_constant<int, 12>{});
+      case 16: return f(integral_constant<int, 256>{}, integral_constant<int, 16>{});
+    }
+  } else if (c.block == 512) {
+    switch (c.nch) {
+      case 12: return f(integral_constant<int, 512>{}, integral_constant<int, 12>{});
+      case 16: return f(integral_constant<int, 512>{}, integral_constant<int, 16>{});
     }
   } else {
     switch (c.nch) {
@@ -952,11 +1055,12 @@ int dispatch_cfg(const RowCfg& c, F&& f) {
   return HK_EINVAL;
 }
 
-int64_t persistent_grid(int64_t rows, int block) {
+// A persistent grid: as many blocks as the CUs hold at once for this kernel
+// (its occupancy), or one per row when there are fewer rows.
+int64_t resident_grid(const void* kernel, int64_t rows, int block) {
   const int dev = current_device();
   const int cu = dev >= 0 ? cu_count(dev) : 256;
-  const int64_t per_cu = block >= 1024 ? 2 : 8;
-  const int64_t g = (int64_t)(cu > 0 ? cu : 256) * per_cu;
+  const int64_t g = (int64_t)(cu > 0 ? cu : 256) * blocks_per_cu(kernel, block);
   return rows < g ? (rows > 0 ? rows : 1) : g;
 }
 
@@ -1048,20 +1152,16 @@ int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nr
     return dispatch_cfg(cfg, [&](auto blk, auto nch) {
       constexpr int BLOCK = decltype(blk)::value;
       constexpr int NCH = decltype(nch)::value;
-      const dim3 grid((unsigned)persistent_grid(nrows, BLOCK));
+      auto run = [&](auto kern, int block) {
+        const dim3 grid((unsigned)resident_grid((const void*)kern, nrows, block));
+        hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (T*)dlogits, (const T*)logits, h);
+        return check_launch("grpo_kernel");
+      };
       auto go = [&](auto grad_c) {
         constexpr bool GRAD = decltype(grad_c)::value;
-        if (cfg.vec == 1) {
-          hipLaunchKernelGGL((grpo_kernel<T, 1, 1, 1024, false, GRAD>), grid, dim3(1024), 0, st, (T*)dlogits,
-                             (const T*)logits, h);
-        } else if constexpr (NCH == 0) {
-          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>), grid, dim3(BLOCK), 0, st,
-                             (T*)dlogits, (const T*)logits, h);
-        } else {
-          hipLaunchKernelGGL((grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>), grid, dim3(BLOCK), 0, st,
-                             (T*)dlogits, (const T*)logits, h);
-        }
-        return check_launch("grpo_kernel");
+        if (cfg.vec == 1) return run(grpo_kernel<T, 1, 1, 1024, false, GRAD>, 1024);
+        if constexpr (NCH == 0) return run(grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>, BLOCK);
+        else return run(grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>, BLOCK);
       };
       if (dlogits) return go(std::true_type{});
       return go(std::false_type{});
@@ -1107,6 +1207,41 @@ int sum_rows_launch(float* out, const float* v, int64_t n, const int* n_valid, i
   return check_launch("sum_rows_kernel");
 }
 
+// Row configuration of a forward-only (read-only) row kernel: register-resident
+// rows on 256 lanes up to 2048 vectors a row (16384 16-bit logits), where the
+// next row's loads overlap the block combine; longer rows stream on 1024
+// lanes, which measured as fast or faster for them than holding the row (a
+// long resident row leaves few blocks a CU).
+RowCfg choose_read_cfg(int64_t V, int esize, bool vec_ok) {
+  const RowCfg c = choose_row_cfg(V, esize, vec_ok);
+  if (c.nch > 0 && c.block == 256 && c.nch <= 8) return c;
+  return RowCfg{1024, 0, c.vec};
+}
+
+// The inference forward over a.rows rows of a.V logits (row stride a.ld_in).
+int ce_lse_launch(const void* logits, const CeArgs& a, int dtype, hipStream_t st) {
+  const int es = esize(dtype);
+  const bool vec_ok = a.V % (16 / es) == 0 && aligned_to(logits, 16) && (a.ld_in * es) % 16 == 0;
+  const RowCfg cfg = choose_read_cfg(a.V, es, vec_ok);
+  return dispatch_t(dtype, [&](auto tt) {
+    using T = typename decltype(tt)::type;
+    return dispatch_cfg(cfg, [&](auto blk, auto nch) {
+      constexpr int BLOCK = decltype(blk)::value;
+      constexpr int NCH = decltype(nch)::value;
+      auto run = [&](auto kern, int block) {
+        const dim3 grid((unsigned)resident_grid((const void*)kern, a.rows, block));
+        hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (const T*)logits, a);
+        return check_launch("ce_fwd_kernel");
+      };
+      if (cfg.vec == 1) return run(ce_fwd_kernel<T, 1, 1, 1024, false>, 1024);
+      // (choose_read_cfg keeps resident rows on 256 lanes, 8 vectors at most)
+      constexpr bool kResident = NCH > 0 && BLOCK == 256 && NCH <= 8;
+      if constexpr (!kResident) return run(ce_fwd_kernel<T, 16 / sizeof(T), 1, 1024, false>, 1024);
+      else return run(ce_fwd_kernel<T, 16 / sizeof(T), NCH, 256, true>, 256);
+    });
+  });
+}
+
 int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const int64_t* targets, int64_t rows,
                    int64_t V, int64_t ld_in, int64_t ld_out, int64_t ignore_index, int has_ignore, const int* n_valid,
                    int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st, const int* rows_lim,
@@ -1128,16 +1263,7 @@ int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const in
   a.has_ignore = has_ignore;
   a.scale_by_n_valid = scale_by_n_valid;
   if (!dlogits) {  // loss rows only
-    const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (ld_in * es) % 16 == 0;
-    return dispatch_t(dtype, [&](auto tt) {
-      using T = typename decltype(tt)::type;
-      const dim3 grid((unsigned)persistent_grid(rows, 1024));
-      if (vec_ok)
-        hipLaunchKernelGGL((ce_fwd_kernel<T, 16 / sizeof(T), 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
-      else
-        hipLaunchKernelGGL((ce_fwd_kernel<T, 1, 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
-      return check_launch("ce_fwd_kernel");
-    });
+    return ce_lse_launch(logits, a, dtype, st);
   }
   const int vec = 16 / es;
   const bool vec_ok = V % vec == 0 && aligned_to(logits, 16) && aligned_to(dlogits, 16) && (ld_in * es) % 16 == 0 &&
@@ -1148,18 +1274,14 @@ int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const in
     return dispatch_cfg(cfg, [&](auto blk, auto nch) {
       constexpr int BLOCK = decltype(blk)::value;
       constexpr int NCH = decltype(nch)::value;
-      const dim3 grid((unsigned)persistent_grid(rows, BLOCK));
-      if (cfg.vec == 1) {
-        hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 1, 1, 1024, false>), grid, dim3(1024), 0, st, (T*)dlogits,
-                           (const T*)logits, a);
-      } else if constexpr (NCH == 0) {
-        hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>), grid, dim3(BLOCK), 0, st,
-                           (T*)dlogits, (const T*)logits, a);
-      } else {
-        hipLaunchKernelGGL((ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>), grid, dim3(BLOCK), 0, st,
-                           (T*)dlogits, (const T*)logits, a);
-      }
-      return check_launch("ce_fwd_grad_kernel");
+      auto run = [&](auto kern, int block) {
+        const dim3 grid((unsigned)resident_grid((const void*)kern, rows, block));
+        hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (T*)dlogits, (const T*)logits, a);
+        return check_launch("ce_fwd_grad_kernel");
+      };
+      if (cfg.vec == 1) return run(ce_fwd_grad_kernel<T, 1, 1, 1024, false>, 1024);
+      if constexpr (NCH == 0) return run(ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>, BLOCK);
+      else return run(ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>, BLOCK);
     });
   });
 }
@@ -1218,8 +1340,6 @@ int hk_cross_entropy_fwd(float* lse_rows, float* loss_rows, float* loss_out, con
   if (rows > 0) {
     int rc = count_valid_launch(n_valid, targets, rows, ignore_index, has_ignore, st);
     if (rc) return rc;
-    const int es = esize(dtype);
-    const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16) && (ld_logits * es) % 16 == 0;
     CeArgs a{};
     a.targets = targets;
     a.loss_rows = loss_rows;
@@ -1229,15 +1349,7 @@ int hk_cross_entropy_fwd(float* lse_rows, float* loss_rows, float* loss_out, con
     a.ld_in = ld_logits;
     a.ignore_index = ignore_index;
     a.has_ignore = has_ignore;
-    rc = dispatch_t(dtype, [&](auto tt) {
-      using T = typename decltype(tt)::type;
-      const dim3 grid((unsigned)persistent_grid(rows, 1024));
-      if (vec_ok)
-        hipLaunchKernelGGL((ce_fwd_kernel<T, 16 / sizeof(T), 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
-      else
-        hipLaunchKernelGGL((ce_fwd_kernel<T, 1, 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
-      return check_launch("ce_fwd_kernel");
-    });
+    rc = ce_lse_launch(logits, a, dtype, st);
     if (rc) return rc;
   }
   if (loss_out)
@@ -1304,16 +1416,24 @@ int hk_selective_log_softmax(float* logp, const void* logits, const int64_t* ids
   a.logp_out = logp;
   const int es = esize(dtype);
   const bool vec_ok = V % (16 / es) == 0 && aligned_to(logits, 16);
+  const RowCfg cfg = choose_read_cfg(V, es, vec_ok);
   hipStream_t st = (hipStream_t)stream;
   return dispatch_t(dtype, [&](auto tt) {
     using T = typename decltype(tt)::type;
-    const dim3 grid((unsigned)persistent_grid(B * L, 1024));
-    if (vec_ok)
-      hipLaunchKernelGGL((selective_log_softmax_kernel<T, 16 / sizeof(T), 1024>), grid, dim3(1024), 0, st,
-                         (const T*)logits, a);
-    else
-      hipLaunchKernelGGL((selective_log_softmax_kernel<T, 1, 1024>), grid, dim3(1024), 0, st, (const T*)logits, a);
-    return check_launch("selective_log_softmax_kernel");
+    return dispatch_cfg(cfg, [&](auto blk, auto nch) {
+      constexpr int BLOCK = decltype(blk)::value;
+      constexpr int NCH = decltype(nch)::value;
+      auto run = [&](auto kern, int block) {
+        const dim3 grid((unsigned)resident_grid((const void*)kern, B * L, block));
+        hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (const T*)logits, a);
+        return check_launch("selective_log_softmax_kernel");
+      };
+      if (cfg.vec == 1) return run(selective_log_softmax_kernel<T, 1, 1, 1024, false>, 1024);
+      // (choose_read_cfg keeps resident rows on 256 lanes, 8 vectors at most)
+      constexpr bool kResident = NCH > 0 && BLOCK == 256 && NCH <= 8;
+      if constexpr (!kResident) return run(selective_log_softmax_kernel<T, 16 / sizeof(T), 1, 1024, false>, 1024);
+      else return run(selective_log_softmax_kernel<T, 16 / sizeof(T), NCH, 256, true>, 256);
+    });
   });
 }
 

@@ -15,10 +15,13 @@
 // two groups per CU), accumulating its dW contribution in registers: fp32 for
 // 16-bit inputs, fp64 for fp32 inputs (a sum over thousands of rows in fp32
 // drifts by ~1e-4, more than the 1e-5 fp32 tolerance allows). The groups'
-// accumulators then go either into fp64 atomics on one [cols] accumulator or
-// into one fp32 partial row per group (a run of rows rounds once), summed in
-// fp64 by a separate pass; the choice follows the reference rule "atomic when
-// rows <= 8 * CU count" (rms_norm.py:325-326).
+// accumulators then go either into one fp32 partial row per group (a run of
+// rows rounds once), summed in fp64 by a separate pass, or into fp64 atomics
+// on one [cols] accumulator. HK_DW_AUTO always takes the partial rows. The
+// reference switches to atomics when rows <= 8 * CU count (rms_norm.py:325-326);
+// here the groups' device-scope fp64 atomics on the one row measured 1.7-9x
+// slower than the partial rows at every size tried (16 to 4096 rows, H 1024 to
+// 8192), so atomics run only when HK_DW_ATOMIC asks for them.
 #include "hk_common.h"
 #include "../../include/hilda_kernel_amd.h"
 
@@ -394,7 +397,7 @@ struct BwdPlan {
 bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int cu, BwdPlan* p) {
   if (!choose_geom(cols, es, vec_ok, &p->g)) return false;
   const int64_t ncu = cu > 0 ? cu : 256;
-  p->atomic = dw_mode == HK_DW_ATOMIC || (dw_mode == HK_DW_AUTO && rows <= 8 * ncu);
+  p->atomic = dw_mode == HK_DW_ATOMIC;
   // about two row groups per CU: long runs of rows keep the accumulator rows
   // (partials or atomics) few; more groups were not faster
   const int64_t target = (p->atomic ? 1 : 2) * ncu * p->g.rpb;

@@ -44,7 +44,7 @@ extern "C" {
 #define HK_REDUCTION_BATCHMEAN 3 /* KLDiv only: sum / rows */
 
 /* dW reduction path for the norm backward passes */
-#define HK_DW_AUTO 0    /* atomic when rows <= 8 * CU count, else partial */
+#define HK_DW_AUTO 0    /* partial (faster than atomic at every size)     */
 #define HK_DW_ATOMIC 1  /* fp64 atomics into one [cols] accumulator       */
 #define HK_DW_PARTIAL 2 /* per-row-group partial rows + a reduction pass  */
 

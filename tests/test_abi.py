@@ -139,6 +139,10 @@ def test_workspace_query_is_pure():
     part32 = lib.hk_rms_norm_bwd_workspace_size(8192, 4096, 0, 0, _lib.DW_PARTIAL, 0)
     assert part32 == part
     assert lib.hk_rms_norm_bwd_workspace_size(-1, 4096, 2, 2, 0, 0) == 0
+    # the default mode takes the partial rows at every row count (no atomics for few rows)
+    for rows in (16, 2048, 8192):
+        assert (lib.hk_rms_norm_bwd_workspace_size(rows, 4096, 2, 2, _lib.DW_AUTO, 0) ==
+                lib.hk_rms_norm_bwd_workspace_size(rows, 4096, 2, 2, _lib.DW_PARTIAL, 0))
 
 
 def test_ops_refuse_cpu_tensors():

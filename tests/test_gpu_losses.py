@@ -2,8 +2,8 @@
 
 Mirrors benchmarks/bench_cross_entropy.py (loss, dlogits, ignored-row gradient,
 tightened to exactly zero) and benchmarks/bench_grpo.py (loss, gradient) and
-adds: every row-engine variant (register-resident 256/1024-lane, streaming,
-unvectorised), reductions, ignore_index=-1, all-ignored, upstream grads != 1,
+adds: row-engine variants (register-resident 256/512/1024-lane, streaming,
+unvectorised; test_gpu_row_engine.py reaches every form), reductions, ignore_index=-1, all-ignored, upstream grads != 1,
 repeated backward, masks of several dtypes, temperature, and the full C3/C4
 shapes (row slices against the oracle plus size-independent properties).
 
@@ -37,8 +37,8 @@ def _ce_case(N, V, dtype, ignore_frac, seed, scale=2.0):
     return logits, t
 
 
-# V values cover: 256-lane resident (1000, 4096), 1024-lane resident (32000, 128256),
-# streaming (200000 > resident limit), unvectorised (1001)
+# V values cover: 256-lane resident (1000, 4096; 32000 in 16-bit), 512-lane resident (32000 fp32),
+# 1024-lane resident (128256 in 16-bit), streaming (128256 fp32, 200000), unvectorised (1001)
 @pytest.mark.parametrize("V", [1000, 1001, 4096, 32000, 128256, 200000])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])

@@ -11,11 +11,12 @@
 // memory latency, not two.
 //
 // Backward saves only rstd (the forward's [rows] fp32 output) and recomputes
-// the normalised row. Each row group walks a run of R consecutive rows (about
-// two groups per CU), accumulating its dW contribution in registers: fp32 for
-// 16-bit inputs, fp64 for fp32 inputs (a sum over thousands of rows in fp32
-// drifts by ~1e-4, more than the 1e-5 fp32 tolerance allows). The groups'
-// accumulators then go either into one fp32 partial row per group (a run of
+// the normalised row. Each row group walks a run of R consecutive rows,
+// accumulating its dW contribution in registers: fp32 for 16-bit inputs, fp64
+// for fp32 inputs (a sum over thousands of rows in fp32 drifts by ~1e-4, more
+// than the 1e-5 fp32 tolerance allows). A 1024-lane block holds several groups
+// (4 at H = 4096), one block a CU; their accumulators are summed in LDS in a
+// fixed order and go either into one fp32 partial row per block (a run of
 // rows rounds once), summed in fp64 by a separate pass, or into fp64 atomics
 // on one [cols] accumulator. HK_DW_AUTO always takes the partial rows. The
 // reference switches to atomics when rows <= 8 * CU count (rms_norm.py:325-326);
@@ -204,18 +205,47 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
     }
   }
 
+  if (rpb == 1) {
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int col = (j * gl + lr) * VEC;
-    if (col < cols) {
+    for (int j = 0; j < NCH; ++j) {
+      const int col = (j * gl + lr) * VEC;
+      if (col < cols) {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        if (atomic) {
-          if (row0 < rows) unsafeAtomicAdd(static_cast<double*>(dw_ws) + col + i, (double)acc[j][i]);
-        } else {
-          static_cast<float*>(dw_ws)[group * cols + col + i] = (float)acc[j][i];
+        for (int i = 0; i < VEC; ++i) {
+          if (atomic) {
+            if (row0 < rows) unsafeAtomicAdd(static_cast<double*>(dw_ws) + col + i, (double)acc[j][i]);
+          } else {
+            static_cast<float*>(dw_ws)[group * cols + col + i] = (float)acc[j][i];
+          }
         }
       }
+    }
+    return;
+  }
+  // Several row groups a block: their accumulators are summed in LDS, group by
+  // group in a fixed order, and the block writes one partial row (or adds it
+  // atomically), so the dW pass reads rpb times fewer rows.
+  extern __shared__ __align__(16) unsigned char dyn_lds[];
+  A* buf = reinterpret_cast<A*>(dyn_lds);
+  for (int r = 0; r < rpb; ++r) {
+    if (rib == r) {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int col = (j * gl + lr) * VEC;
+        if (col < cols) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) buf[col + i] = r == 0 ? acc[j][i] : buf[col + i] + acc[j][i];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const bool any_row = (int64_t)blockIdx.x * rpb * rows_per_group < rows;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+    if (atomic) {
+      if (any_row) unsafeAtomicAdd(static_cast<double*>(dw_ws) + c, (double)buf[c]);
+    } else {
+      static_cast<float*>(dw_ws)[(int64_t)blockIdx.x * cols + c] = (float)buf[c];
     }
   }
 }
@@ -387,26 +417,43 @@ int fwd_impl(void* y, void* s, float* rstd, const void* x, const void* r, const 
 // workspace query.
 struct BwdPlan {
   Geom g;
-  int64_t groups;     // row groups (one accumulator row each)
+  int block;          // threads a block: rpb row groups of g.wpr waves
+  int rpb;            // row groups a block
+  size_t lds;         // dynamic LDS for summing the groups of a block (rpb > 1)
+  int64_t groups;     // row groups
   int64_t rpg;        // rows per group
   int64_t grid;       // blocks
+  int64_t parts;      // partial rows: one per block (rpb > 1) or per group
   bool atomic;
   size_t total;
 };
+
+constexpr size_t kBwdLdsMax = 32 * 1024;
 
 bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int cu, BwdPlan* p) {
   if (!choose_geom(cols, es, vec_ok, &p->g)) return false;
   const int64_t ncu = cu > 0 ? cu : 256;
   p->atomic = dw_mode == HK_DW_ATOMIC;
-  // about two row groups per CU: long runs of rows keep the accumulator rows
-  // (partials or atomics) few; more groups were not faster
-  const int64_t target = (p->atomic ? 1 : 2) * ncu * p->g.rpb;
+  // 1024-lane blocks of several row groups whose dW accumulators meet in LDS:
+  // the partial rows (the dW pass's traffic) are one per block, not one per group
+  const size_t acc_bytes = es == 4 ? sizeof(double) : sizeof(float);
+  const int rpb = std::max(1, 1024 / (p->g.wpr * kWave));
+  const bool combine = rpb > 1 && (size_t)cols * acc_bytes <= kBwdLdsMax;
+  p->block = (combine ? rpb : 1) * p->g.wpr * kWave;  // without the LDS sum: one group a block
+  p->rpb = p->block / (p->g.wpr * kWave);
+  p->lds = combine ? (size_t)cols * acc_bytes : 0;
+  // Long runs of rows keep the partial rows few. One 1024-lane block a CU (the
+  // 16-bit H = 4096 form needs ~100 VGPRs, so a second would not be resident);
+  // without the LDS sum, two blocks of one group each.
+  const int64_t blocks = (combine ? 1 : 2) * ncu;
+  const int64_t target = blocks * p->rpb;
   p->groups = std::max<int64_t>(1, std::min<int64_t>(rows, target));
   p->rpg = rows > 0 ? cdiv(rows, p->groups) : 0;
   p->groups = rows > 0 ? cdiv(rows, p->rpg) : 1;
-  p->grid = cdiv(p->groups, (int64_t)p->g.rpb);
-  p->groups = p->grid * p->g.rpb;  // every launched group owns an accumulator row
-  p->total = p->atomic ? (size_t)cols * 8 : (size_t)p->groups * cols * sizeof(float);
+  p->grid = cdiv(p->groups, (int64_t)p->rpb);
+  p->groups = p->grid * p->rpb;  // every launched group has a (possibly empty) run of rows
+  p->parts = p->rpb > 1 ? p->grid : p->groups;
+  p->total = p->atomic ? (size_t)cols * 8 : (size_t)p->parts * cols * sizeof(float);
   return true;
 }
 
@@ -449,15 +496,16 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
     if (rows > 0) {
       int rc = dispatch_nch(p.g.nch, [&](auto nch_c) {
         constexpr int NCH = decltype(nch_c)::value;
-        return dispatch_lb(p.g.block, [&](auto lb_c) {
+        return dispatch_lb(p.block, [&](auto lb_c) {
           constexpr int LB = decltype(lb_c)::value;
           auto launch = [&](auto vec_c) {
             constexpr int VEC = decltype(vec_c)::value;
             auto go = [&](auto hds_c) {
               constexpr bool HDS = decltype(hds_c)::value;
               hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, W, A, VEC, NCH, HDS, LB>), dim3((unsigned)p.grid),
-                                 dim3(p.g.block), 0, st, (T*)dx, part, (int)p.atomic, (const T*)dy, (const T*)ds, (const T*)x, (const W*)w, rstd, rows,
-                                 (int)cols, ld_dy, ld_ds, ld_x, ld_dx, p.g.wpr, p.rpg);
+                                 dim3(p.block), p.lds, st, (T*)dx, part, (int)p.atomic, (const T*)dy, (const T*)ds,
+                                 (const T*)x, (const W*)w, rstd, rows, (int)cols, ld_dy, ld_ds, ld_x, ld_dx, p.g.wpr,
+                                 p.rpg);
               return check_launch("rmsnorm_bwd_kernel");
             };
             if (ds) return go(std::true_type{});
@@ -476,7 +524,7 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
     }
     // (no rows: zero groups are summed and dW comes out zero)
     hipLaunchKernelGGL((reduce_partial_kernel<W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
-                       (const float*)part, rows > 0 ? p.groups : 0, (int)cols);
+                       (const float*)part, rows > 0 ? p.parts : 0, (int)cols);
     return check_launch("reduce_partial_kernel");
   });
 }

@@ -57,14 +57,16 @@ def test_rms_norm_fwd_bwd(shape, dtype, w_fp32):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows", [100, 3000])
-def test_rms_norm_dw_paths_agree(dtype, rows):
-    """Atomic and partial dW reductions give the same dW (and the same dX)."""
+@pytest.mark.parametrize("rows,H", [(100, 2048), (3000, 2048), (5001, 4096), (777, 8192)])
+def test_rms_norm_dw_paths_agree(dtype, rows, H):
+    """Atomic and partial dW reductions give the same dW (and the same dX).
+    The shapes give several rows a group and a last block with empty groups
+    (H = 4096: four groups a 1024-lane block summed in LDS; H = 8192: two)."""
     g = torch.Generator().manual_seed(rows)
     dev = gpu()
-    x = torch.randn(rows, 2048, generator=g).to(dtype).to(dev)
-    w = (1 + 0.1 * torch.randn(2048, generator=g)).to(dtype).to(dev)
-    dy = torch.randn(rows, 2048, generator=g).to(dtype).to(dev)
+    x = torch.randn(rows, H, generator=g).to(dtype).to(dev)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dtype).to(dev)
+    dy = torch.randn(rows, H, generator=g).to(dtype).to(dev)
     _, xf, rstd = rn.rms_norm_forward(x, w)
     dxa, dwa = rn.rms_norm_backward(dy, xf, w, rstd, dw_mode=_lib.DW_ATOMIC)
     dxp, dwp = rn.rms_norm_backward(dy, xf, w, rstd, dw_mode=_lib.DW_PARTIAL)

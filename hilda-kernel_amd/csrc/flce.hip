@@ -213,13 +213,103 @@ __global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, con
   }
 }
 
+// The dX GEMM's epilogue when it may split K. Unsplit (the GEMM's split count
+// is 1), it stores the tile like EpiScatter / EpiStore, 4 columns a chunk; split,
+// split s stores fp32 partial sums at part + (s * m + row) * ld, m the GEMM's
+// bounded row count, and splitk_sum_kernel adds them up.
+template <typename T>
+struct EpiDx {
+  using Stage = float;
+  using Prior = NoPrior;
+  static constexpr bool kReads = false;
+  T* C;
+  int64_t ldc;       // a multiple of 8
+  const int* rows;   // nullable: GEMM row r goes to row rows[r] of C
+  float* part;
+  int64_t ld;        // a multiple of 4
+  int split = 0, nsplit = 1, m = 0;
+  __device__ __forceinline__ void set_split(int s, int ns, int bounded_m) {
+    split = s;
+    nsplit = ns;
+    m = bounded_m;
+  }
+  __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
+  __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior&) const {
+    if (nsplit == 1) {
+      T* p = C + (int64_t)(rows ? rows[row] : row) * ldc + col;
+      if (n == 4) {
+        *reinterpret_cast<u32x2*>(p) = u32x2{gemm::pack2<T>(v[0], v[1]), gemm::pack2<T>(v[2], v[3])};
+      } else {
+        for (int e = 0; e < n; ++e) p[e] = from_f32<T>(v[e]);
+      }
+      return;
+    }
+    float* p = part + ((int64_t)split * m + row) * ld + col;
+    if (n == 4) {
+      *reinterpret_cast<f32x4_t*>(p) = f32x4_t{v[0], v[1], v[2], v[3]};
+    } else {
+      for (int e = 0; e < n; ++e) p[e] = v[e];
+    }
+  }
+};
+
+// C[rows ? rows[r] : r] = sum over the splits of the partials (rounded once to
+// T), 8 columns a thread, for r below the device-bounded M. The split count is
+// the GEMM's own (auto_splits of its bounded tiles); unsplit, the GEMM stored
+// C itself and this returns at once.
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_sum_kernel(T* __restrict__ C, int64_t ldc, const int* __restrict__ rows,
+                                                         const float* __restrict__ part, int M, int N, int KT,
+                                                         int max_s, const int* lim, int lim_off) {
+  if (lim) M = min(M, max(0, *lim - lim_off));
+  const int S = gemm::auto_splits(((M + 255) / 256) * ((N + 255) / 256), KT, max_s);
+  if (S == 1) return;
+  const int n8 = N / 8;
+  const int64_t total = (int64_t)M * n8, stride = (int64_t)M * N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int r = (int)(i / n8), c = (int)(i - (int64_t)r * n8) * 8;
+    const float* p = part + (int64_t)r * N + c;
+    f32x4_t a = *reinterpret_cast<const f32x4_t*>(p), b = *reinterpret_cast<const f32x4_t*>(p + 4);
+    for (int s = 1; s < S; ++s) {
+      a += *reinterpret_cast<const f32x4_t*>(p + s * stride);
+      b += *reinterpret_cast<const f32x4_t*>(p + s * stride + 4);
+    }
+    const u32x4 o{gemm::pack2<T>(a[0], a[1]), gemm::pack2<T>(a[2], a[3]), gemm::pack2<T>(b[0], b[1]),
+                  gemm::pack2<T>(b[2], b[3])};
+    *reinterpret_cast<u32x4*>(C + (int64_t)(rows ? rows[r] : r) * ldc + c) = o;
+  }
+}
+
 template <typename T> struct Tag { using type = T; };
 
 // lim (nullable): a device-side bound on M (or K with lim_k), see gemm::Shape
 template <typename T, class Epi>
 int launch_gemm(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
-                const int* lim = nullptr, int lim_off = 0, bool lim_k = false) {
-  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st, lim, lim_off, lim_k);
+                const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1) {
+  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st, lim, lim_off, lim_k, ksplit);
+}
+
+// Most K splits the dX GEMM (M = chunk rows, N = H, K = V) may take; the
+// kernel picks auto_splits() of the tiles left after the live-row bound, so a
+// short or mostly ignored chunk (a 2048-row chunk at H = 4096 is 128 output
+// tiles) still fills the chip. 1: never split.
+int dx_max_splits(int64_t H, int64_t V) {
+  if (V % 64 != 0 || H % 8 != 0) return 1;
+  return (int)std::min<int64_t>(8, V / 64 / 16);
+}
+
+// fp32 partial-sum bytes the dX GEMM of a chunk of up to C rows can need: the
+// largest splits x rows over the row counts it may be cut to.
+size_t dx_part_bytes(int64_t C, int64_t H, int64_t V) {
+  const int smax = dx_max_splits(H, V);
+  if (smax <= 1) return 0;
+  size_t best = 0;
+  const int64_t ntn = cdiv(H, 256), kt = V / 64;
+  for (int64_t mt = 1; mt <= cdiv(C, 256); ++mt) {
+    const int s = gemm::auto_splits((int)(mt * ntn), (int)kt, smax);
+    if (s > 1) best = std::max(best, (size_t)s * (size_t)std::min<int64_t>(C, mt * 256) * H * 4);
+  }
+  return best;
 }
 
 template <typename T>
@@ -246,6 +336,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct FlceLayout {
   size_t wt, xt, lg, dt, dwacc, nvalid, extra, total;
+  int ksplit;   // most K splits of the dX GEMM (dx_max_splits), their fp32 partial sums at `part`
+  size_t part;
   bool defer;  // the whole D^T [V, BTp] is kept and dW is one GEMM after the chunk loop
   // the compaction of the live rows: row map, inverse map, live count, compacted hidden rows;
   // for CrossEntropy also the compacted targets, row scales and losses
@@ -288,6 +380,9 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
       L.dt = take((size_t)V * ld_t(chunk) * es);
       L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
     }
+    const size_t pb = dx_part_bytes(chunk, H, V);
+    L.ksplit = pb ? dx_max_splits(H, V) : 1;
+    L.part = pb ? take(pb) : 0;
   }
   L.extra = extra ? take(extra) : 0;
   L.total = off;
@@ -388,12 +483,25 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
     rc = row_step(Lg, r0, cs);
     if (rc) return rc;
     if (!grad) continue;
-    // dX_c = D_c W, stored into the live rows' original places
-    if (rowmap)
+    // dX_c = D_c W, stored into the live rows' original places; a short chunk
+    // splits K (= V) and sums the splits' fp32 partials in a second pass
+    if (lay.ksplit > 1) {
+      float* part = (float*)(ws + lay.part);
+      T* dst = rowmap ? dX : dX + r0 * H;
+      const int* map = rowmap ? rowmap + r0 : nullptr;
+      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiDx<T>{dst, H, map, part, H}, st, n_live,
+                          (int)r0, false, lay.ksplit);
+      if (rc) return rc;
+      const int64_t work = cs * (H / 8);
+      hipLaunchKernelGGL((splitk_sum_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(work, 256), 8192)), dim3(256),
+                         0, st, dst, H, map, part, (int)cs, (int)H, (int)(V / 64), lay.ksplit, n_live, (int)r0);
+      rc = check_launch("splitk_sum_kernel");
+    } else if (rowmap) {
       rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiScatter<T>{dX, H, rowmap + r0}, st, n_live,
                           (int)r0);
-    else
+    } else {
       rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{dX + r0 * H, H}, st);
+    }
     if (rc) return rc;
     if (lay.defer) {
       // D_c^T into columns [r0, r0 + cs) of D^T [V, BTp]; zeros past the live rows

@@ -60,7 +60,33 @@ struct Shape {
   const int* lim = nullptr;
   int lim_off = 0;
   int lim_k = 0;
+  // split-K (gemm_kk_kernel only): at most ksplit workgroups per output tile.
+  // The kernel takes auto_splits() of the tiles left after the bound, so a GEMM
+  // cut short on the device still fills the chip; split s sums K tiles
+  // [s * per, (s + 1) * per), per = ceil(K / BK / splits), and the epilogue is
+  // told (Epi::set_split) its split, the split count and the bounded M.
+  int ksplit = 1;
 };
+
+// Splits for a GEMM of `tiles` output tiles and `kt` K tiles, at most max_s:
+// about 512 workgroups (two a CU), every split at least 16 K tiles and non-empty.
+__host__ __device__ inline int auto_splits(int tiles, int kt, int max_s) {
+  if (max_s <= 1 || tiles >= 256 || tiles <= 0) return 1;
+  int s = min(max_s, (512 + tiles - 1) / tiles);
+  s = min(s, kt / 16);
+  while (s > 1 && (kt + s - 1) / s * (s - 1) >= kt) --s;
+  return s < 1 ? 1 : s;
+}
+
+// Gives a split-K epilogue its split, the split count and the bounded M; other
+// epilogues have no set_split.
+template <class Epi>
+__device__ __forceinline__ auto apply_split(Epi& e, int s, int ns, int m, int) -> decltype(e.set_split(s, ns, m),
+                                                                                          void()) {
+  e.set_split(s, ns, m);
+}
+template <class Epi>
+__device__ __forceinline__ void apply_split(Epi&, int, int, int, long) {}
 
 // Applies Shape::lim (a uniform scalar load); kq: the K granule of the kernel.
 __device__ __forceinline__ void apply_bound(Shape& g, int kq) {
@@ -134,10 +160,9 @@ __device__ __forceinline__ int swz(int row, int kc) {
 }
 
 template <int GROUP_M>
-__device__ __forceinline__ void tile_of_block(int nbm, int nbn, int* tm, int* tn) {
+__device__ __forceinline__ void tile_of_block(int pid, int nbm, int nbn, int* tm, int* tn) {
   constexpr int kXcds = 8;
   const int total = nbm * nbn;
-  const int pid = blockIdx.x;
   const int q = total / kXcds, r = total % kXcds;
   const int xcd = pid % kXcds, local = pid / kXcds;
   const int logical = xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
@@ -380,7 +405,7 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
   if ((int)blockIdx.x >= nbm * nbn) return;  // uniform: past a device-side bound
   int tm, tn;
-  tile_of_block<C::GROUP_M>(nbm, nbn, &tm, &tn);
+  tile_of_block<C::GROUP_M>((int)blockIdx.x, nbm, nbn, &tm, &tn);
   const int m0 = tm * C::BM, n0 = tn * C::BN;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -515,9 +540,12 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
 
   apply_bound(g, C::BK);
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
-  if ((int)blockIdx.x >= nbm * nbn) return;  // uniform: past a device-side bound
+  const int tiles = nbm * nbn;
+  const int nsplit = auto_splits(tiles, g.K / C::BK, g.ksplit);
+  if ((int)blockIdx.x >= tiles * nsplit) return;  // uniform: past a device-side bound
+  const int split = (int)blockIdx.x / tiles;
   int tm, tn;
-  tile_of_block<C::GROUP_M>(nbm, nbn, &tm, &tn);
+  tile_of_block<C::GROUP_M>((int)blockIdx.x - split * tiles, nbm, nbn, &tm, &tn);
   const int m0 = tm * C::BM, n0 = tn * C::BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -532,7 +560,12 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int KT = g.K / C::BK;
+  int KT = g.K / C::BK, kt0 = 0;
+  if (nsplit > 1) {  // this split's K tiles (auto_splits keeps every split non-empty)
+    const int per = (KT + nsplit - 1) / nsplit;
+    kt0 = split * per;
+    KT = min(per, KT - kt0);
+  }
 
   // Fragment (ks, row R + 32 i) of the MFMA layout: lane l reads row R + 32 i + l%32,
   // 16-byte chunk 2 ks + l/32, stored at chunk (2 ks + l/32) ^ swz_xor(row). With R a
@@ -565,9 +598,10 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     const int q = (wave * IB + i) * 64 + lane, r = q / 8;
     vb[i] = (uint32_t)(r * g.ldb + (((q % 8) ^ swz_xor<C::BK>(r)) << 3)) * (uint32_t)sizeof(T);
   }
-  const T* const pa = A + (int64_t)m0 * g.lda;
-  const T* const pb = B + (int64_t)n0 * g.ldb;
-  // buffer ranges: the panel's rows inside the matrix (rows past it read zero)
+  const T* const pa = A + (int64_t)m0 * g.lda + kt0 * C::BK;
+  const T* const pb = B + (int64_t)n0 * g.ldb + kt0 * C::BK;
+  // buffer ranges: the panel's rows inside the matrix (rows past it read zero;
+  // with a split's K offset the range still ends where the panel's last row can reach)
   const int nra = (int)(min(C::BM, g.M - m0) * g.lda * (int64_t)sizeof(T));
   const int nrb = (int)(min(C::BN, g.N - n0) * g.ldb * (int64_t)sizeof(T));
 
@@ -671,7 +705,9 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
   mma(LB, 0, C::TM * C::TN);
   wait_vmcnt<0>();  // the trailing zero-length loads target LDS: drain them before it is reused
   barrier();
-  epilogue<T, C>(acc, lds_raw, m0, n0, g, epi);
+  Epi e = epi;
+  apply_split(e, split, nsplit, g.M, 0);
+  epilogue<T, C>(acc, lds_raw, m0, n0, g, e);
 }
 
 // Returns 0, or -1 with the error set for shapes the kernel does not take.
@@ -680,10 +716,14 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
 // whichever layout is used.
 template <typename T, class C = DefaultCfg, bool AMN = false, bool BMN = false, class Epi>
 int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
-           const int* lim = nullptr, int lim_off = 0, bool lim_k = false) {
+           const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1) {
   if (M == 0 || N == 0) return 0;
   if (K <= 0) {
     set_error("gemm: K (%d) must be positive", K);
+    return -1;
+  }
+  if (ksplit > 1 && (AMN || BMN || K % C::BK != 0 || lim_k)) {
+    set_error("gemm: split-K needs K-contiguous operands and K (%d) a multiple of %d", K, C::BK);
     return -1;
   }
   auto check = [&](bool mn, int rows, int64_t ld, const char* name) {
@@ -710,13 +750,17 @@ int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb
     return true;
   };
   if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
-  Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0};
-  const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
+  Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0, ksplit < 1 ? 1 : ksplit};
+  const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN) * g.ksplit;
   if constexpr (!AMN && !BMN && C::STAGES == 2 && C::BK == 64) {
     if (K % C::BK == 0) {
       hipLaunchKernelGGL((gemm_kk_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);
       return check_launch("gemm_kk_kernel");
     }
+  }
+  if (g.ksplit > 1) {
+    set_error("gemm: split-K runs on the two-stage K-contiguous kernel only");
+    return -1;
   }
   hipLaunchKernelGGL((gemm_nt_kernel<T, C, AMN, BMN, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g,
                      epi);

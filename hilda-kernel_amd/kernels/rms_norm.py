@@ -3,8 +3,10 @@
 Drop-in for ``kernels/rms_norm.py`` of the reference (rms_norm.py:261-413):
 same functional name, autograd Function, module and argument meaning. The
 forward saves only the per-row fp32 ``rstd``; the backward recomputes the
-normalised row from ``x`` and picks the dW reduction (fp32 atomics or
-partial rows) by the CU count, as rms_norm.py:325-326 does.
+normalised row from ``x`` and sums dW through fp32 partial rows, one per
+1024-lane block (the reference switches to atomics for few rows,
+rms_norm.py:325-326; here ``dw_mode=DW_ATOMIC`` asks for fp64 atomics, which
+measured slower at every size).
 """
 from __future__ import annotations
 

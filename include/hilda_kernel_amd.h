@@ -55,8 +55,9 @@ typedef void* hk_stream_t;
 /* ----------------------------------------------------------------------- */
 int hk_abi_version(void);
 const char* hk_last_error(void);
-/* Number of compute units of `device` (cached). Used for the dW path choice
- * that rms_norm.py:325-326 makes with multi_processor_count. */
+/* Number of compute units of `device` (cached): the persistent grids and the
+ * RMSNorm backward's row groups are sized by it (the reference reads
+ * multi_processor_count for its dW path choice, rms_norm.py:325-326). */
 int hk_device_cu_count(int device);
 
 /* ----------------------------------------------------------------------- */

@@ -3,7 +3,7 @@
 // gradient fused into the forward pass.
 //
 // Row engine. One workgroup owns one vocabulary row at a time (persistent
-// grid of exactly the blocks the CUs hold, rows strided by gridDim.x). When
+// grid of the blocks the CUs hold, rows strided by gridDim.x). When
 // the row fits, it is held in VGPRs: NCH packed 16-byte vectors per lane over
 // a 256-, 512- or 1024-lane workgroup, the smallest form that holds the row
 // (a 32000-entry bf16 row is 16 vectors per lane of 256 lanes, four blocks a
@@ -1055,12 +1055,17 @@ int dispatch_cfg(const RowCfg& c, F&& f) {
   return HK_EINVAL;
 }
 
-// A persistent grid: as many blocks as the CUs hold at once for this kernel
-// (its occupancy), or one per row when there are fewer rows.
-int64_t resident_grid(const void* kernel, int64_t rows, int block) {
+// A persistent grid: `rounds` times the blocks the CUs hold at once for this
+// kernel (its occupancy), or one per row when there are fewer rows. With two
+// rounds, the second round's blocks start as the first round's finish, which
+// evens out rows of uneven cost: GRPO's prefix-masked positions, strided over
+// the grid, give some blocks a third more live rows than others (C4 1.70 ms
+// with one round, 1.65 with two). Rows of even cost keep one round, where each
+// block's next-row prefetch covers more rows (CE 2048 x 32000: 64 against 70 us).
+int64_t resident_grid(const void* kernel, int64_t rows, int block, int rounds = 1) {
   const int dev = current_device();
   const int cu = dev >= 0 ? cu_count(dev) : 256;
-  const int64_t g = (int64_t)(cu > 0 ? cu : 256) * blocks_per_cu(kernel, block);
+  const int64_t g = (int64_t)(cu > 0 ? cu : 256) * blocks_per_cu(kernel, block) * rounds;
   return rows < g ? (rows > 0 ? rows : 1) : g;
 }
 
@@ -1153,7 +1158,7 @@ int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nr
       constexpr int BLOCK = decltype(blk)::value;
       constexpr int NCH = decltype(nch)::value;
       auto run = [&](auto kern, int block) {
-        const dim3 grid((unsigned)resident_grid((const void*)kern, nrows, block));
+        const dim3 grid((unsigned)resident_grid((const void*)kern, nrows, block, 2));
         hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (T*)dlogits, (const T*)logits, h);
         return check_launch("grpo_kernel");
       };
@@ -1424,7 +1429,7 @@ int hk_selective_log_softmax(float* logp, const void* logits, const int64_t* ids
       constexpr int BLOCK = decltype(blk)::value;
       constexpr int NCH = decltype(nch)::value;
       auto run = [&](auto kern, int block) {
-        const dim3 grid((unsigned)resident_grid((const void*)kern, B * L, block));
+        const dim3 grid((unsigned)resident_grid((const void*)kern, B * L, block, 2));
         hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (const T*)logits, a);
         return check_launch("selective_log_softmax_kernel");
       };

@@ -14,11 +14,12 @@
 // the normalised row. Each row group walks a run of R consecutive rows,
 // accumulating its dW contribution in registers: fp32 for 16-bit inputs, fp64
 // for fp32 inputs (a sum over thousands of rows in fp32 drifts by ~1e-4, more
-// than the 1e-5 fp32 tolerance allows). A 1024-lane block holds several groups
-// (4 at H = 4096), one block a CU; their accumulators are summed in LDS in a
-// fixed order and go either into one fp32 partial row per block (a run of
-// rows rounds once), summed in fp64 by a separate pass, or into fp64 atomics
-// on one [cols] accumulator. HK_DW_AUTO always takes the partial rows. The
+// than the 1e-5 fp32 tolerance allows). For 16-bit inputs a 1024-lane block
+// holds several groups (4 at H = 4096), one block a CU, and their accumulators
+// are summed in LDS in a fixed order; fp32 inputs run one group a block, two
+// blocks a CU. Each block's sum goes either into one fp32 partial row (a run
+// of rows rounds once), summed in fp64 by a separate pass, or into fp64
+// atomics on one [cols] accumulator. HK_DW_AUTO always takes the partial rows. The
 // reference switches to atomics when rows <= 8 * CU count (rms_norm.py:325-326);
 // here the groups' device-scope fp64 atomics on the one row measured 1.7-9x
 // slower than the partial rows at every size tried (16 to 4096 rows, H 1024 to
@@ -438,7 +439,9 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   // the partial rows (the dW pass's traffic) are one per block, not one per group
   const size_t acc_bytes = es == 4 ? sizeof(double) : sizeof(float);
   const int rpb = std::max(1, 1024 / (p->g.wpr * kWave));
-  const bool combine = rpb > 1 && (size_t)cols * acc_bytes <= kBwdLdsMax;
+  // (fp32 inputs keep one group a block: their fp64 accumulators make the
+  // 1024-lane form spill, and C1 measured 4% slower with it)
+  const bool combine = rpb > 1 && es != 4 && (size_t)cols * acc_bytes <= kBwdLdsMax;
   p->block = (combine ? rpb : 1) * p->g.wpr * kWave;  // without the LDS sum: one group a block
   p->rpb = p->block / (p->g.wpr * kWave);
   p->lds = combine ? (size_t)cols * acc_bytes : 0;

@@ -449,6 +449,138 @@ def copy_ceiling(work, dev, reps, flush):
     return 2 * n / (ms * 1e-3) / 1e9
 
 
+# ---------------------------------------------------------------------------
+# the reference's own benchmark shapes, each op against a copy of its bytes
+# ---------------------------------------------------------------------------
+def reference_configs(dev, reps):
+    """Every HBM-bound op on the shapes the reference's benchmarks time, fwd and bwd separately, with the
+    algorithmic bytes of each call over a device copy of the same bytes; the fused-linear ops in TFLOP/s.
+    Prints a markdown table. Shapes from triton-kernels/benchmarks: bench_rms_norm.py:169,
+    bench_fused_add_rms_norm.py:198, bench_rope.py:263, bench_swiglu.py:196, bench_geglu.py:191,
+    bench_cross_entropy.py:257, bench_grpo.py:204, bench_kl_div.py:156, bench_jsd.py:173,
+    bench_attn_res.py:205, bench_fused_linear_ce.py:245, bench_fused_linear_jsd.py:163."""
+    from kernels import (rms_norm as rn, fused_add_rms_norm as fa, rope, swiglu as sw, geglu as gg,
+                         cross_entropy as ce, grpo_loss as gl, kl_div as kl, jsd as js, attn_res as ar,
+                         fused_linear_cross_entropy as flce, fused_linear_jsd as fljsd)
+    flush = Flusher(dev)
+    F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *shape, dt=F32: torch.randn(*shape, generator=gen, device=dev).to(dt)  # noqa: E731
+    dname = {F16: "fp16", BF16: "bf16", F32: "fp32"}
+    rows = []
+
+    def hbm(op, shape, dt, fn, nbytes):
+        ms = statistics.median(time_events(fn, reps, flush))
+        cc = copy_ceiling(nbytes, dev, reps, flush)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append(f"| {op} | {shape} | {dname[dt]} | {ms * 1e3:.1f} us | {gbs:.0f} GB/s | {cc:.0f} GB/s | "
+                    f"{gbs / cc:.0%} |")
+        log(rows[-1])
+
+    for B, T, H, dt in ((4, 512, 4096, F16), (8, 1024, 4096, F16), (4, 2048, 4096, F16), (8, 2048, 4096, F16),
+                        (4, 1024, 8192, F16), (4, 1024, 4096, BF16)):
+        R, es = B * T, torch.tensor([], dtype=dt).element_size()
+        x, w, dy = rnd(R, H, dt=dt), rnd(H, dt=dt), rnd(R, H, dt=dt)
+        _, xf, rs = rn.rms_norm_forward(x, w)
+        hbm("RMSNorm fwd", f"{B}x{T}x{H}", dt, lambda: rn.rms_norm_forward(x, w), 2 * R * H * es)
+        hbm("RMSNorm bwd", f"{B}x{T}x{H}", dt, lambda: rn.rms_norm_backward(dy, xf, w, rs), 3 * R * H * es)
+        del x, dy, xf
+    for B, T, H, dt in ((4, 2048, 4096, F16), (4, 2048, 5120, F16), (4, 2048, 8192, F16), (4, 2048, 4096, BF16),
+                        (2, 1024, 4096, F16)):
+        R, es = B * T, torch.tensor([], dtype=dt).element_size()
+        x, r, w, dy, ds = rnd(R, H, dt=dt), rnd(R, H, dt=dt), rnd(H, dt=dt), rnd(R, H, dt=dt), rnd(R, H, dt=dt)
+        _, s_, rs = fa.fused_add_rms_norm_forward(x, r, w)
+        hbm("FusedAddRMSNorm fwd", f"{B}x{T}x{H}", dt, lambda: fa.fused_add_rms_norm_forward(x, r, w), 4 * R * H * es)
+        hbm("FusedAddRMSNorm bwd", f"{B}x{T}x{H}", dt, lambda: fa.fused_add_rms_norm_backward(dy, ds, s_, w, rs),
+            4 * R * H * es)
+        del x, r, dy, ds, s_
+    for B, T, nq, nk, hd, dt in ((4, 2048, 32, 8, 128, F16), (4, 2048, 32, 32, 128, F16), (4, 2048, 64, 8, 128, F16),
+                                 (8, 2048, 32, 8, 128, F16), (4, 2048, 32, 8, 128, BF16), (4, 512, 32, 8, 128, F16)):
+        q, k = rnd(B, nq, T, hd, dt=dt), rnd(B, nk, T, hd, dt=dt)
+        cos, sin = rnd(1, T, hd // 2, dt=dt), rnd(1, T, hd // 2, dt=dt)
+        nb = 2 * (q.numel() + k.numel()) * q.element_size()
+        hbm("RoPE fwd", f"{B}x{T} q{nq} k{nk}", dt, lambda: rope.rope_forward(q, k, cos, sin), nb)
+        hbm("RoPE bwd", f"{B}x{T} q{nq} k{nk}", dt, lambda: rope.rope_backward(q, k, cos, sin), nb)
+        del q, k
+    for name, mod in (("SwiGLU", sw), ("GeGLU", gg)):
+        fwd = mod.swiglu_forward if mod is sw else mod.geglu_forward
+        bwd = mod.swiglu_backward if mod is sw else mod.geglu_backward
+        for N, D, dt in ((8192, 11008, F16), (8192, 14336, F16), (8192, 28672, F16), (8192, 14336, BF16),
+                         (2048, 14336, F16)):
+            a, b, dc = rnd(N, D, dt=dt), rnd(N, D, dt=dt), rnd(N, D, dt=dt)
+            hbm(f"{name} fwd", f"{N}x{D}", dt, lambda: fwd(a, b), 3 * N * D * 2)
+            hbm(f"{name} bwd", f"{N}x{D}", dt, lambda: bwd(a, b, dc), 5 * N * D * 2)
+            del a, b, dc
+    for N, V, dt in ((8192, 32000, F16), (8192, 128256, F16), (8192, 32000, BF16), (8192, 128256, BF16),
+                     (2048, 32000, F16)):
+        x = rnd(N, V, dt=dt)
+        t = torch.randint(0, V, (N,), generator=gen, device=dev)
+        es = x.element_size()
+        hbm("CrossEntropy fwd+grad", f"{N}x{V}", dt, lambda: ce.cross_entropy_forward(x, t, needs_grad=True),
+            2 * N * V * es)
+        hbm("CrossEntropy fwd", f"{N}x{V}", dt, lambda: ce.cross_entropy_forward(x, t), N * V * es)
+        del x
+    for B, L, V, beta in ((8, 512, 32000, 0.0), (8, 512, 32000, 0.1), (4, 1024, 32000, 0.0), (4, 512, 128256, 0.0)):
+        x = rnd(B, L + 1, V, dt=BF16)
+        ids = torch.randint(0, V, (B, L), generator=gen, device=dev)
+        adv, old, ref = rnd(B), rnd(B, L) - 5, rnd(B, L) - 5
+        mask = torch.ones(B, L, dtype=torch.int32, device=dev)
+        kw = dict(old_logp=old, ref_logp=ref if beta else None, completion_mask=mask, beta=beta)
+        nb = B * L * V * 2
+        hbm("GRPO fwd+grad", f"{B}x{L}x{V} beta {beta}", BF16,
+            lambda: gl.grpo_loss_forward(x, ids, adv, compute_grad=True, **kw), 2 * nb)
+        hbm("GRPO fwd", f"{B}x{L}x{V} beta {beta}", BF16, lambda: gl.grpo_loss_forward(x, ids, adv, **kw), nb)
+        hbm("selective log-softmax", f"{B}x{L}x{V}", BF16,
+            lambda: gl.fused_selective_log_softmax(x, ids, 1.0, mask), nb)
+        del x
+    for N, V, dt in ((8192, 32000, F16), (8192, 128256, F16), (8192, 32000, BF16), (2048, 32000, F16)):
+        yp, yt = rnd(N, V).log_softmax(-1).to(dt), rnd(N, V).softmax(-1).to(dt)
+        g1 = torch.ones((), device=dev)
+        es = yp.element_size()
+        hbm("KLDiv fwd", f"{N}x{V}", dt, lambda: kl.kl_div_forward(yp, yt), 2 * N * V * es)
+        hbm("KLDiv bwd", f"{N}x{V}", dt, lambda: kl.kl_div_backward(yt, g1), 2 * N * V * es)
+        del yp, yt
+    for N, V, dt in ((8192, 32000, F16), (4096, 128256, F16), (8192, 32000, BF16)):
+        X, Y = rnd(N, V).log_softmax(-1).to(dt), rnd(N, V).log_softmax(-1).to(dt)
+        hbm("JSD fwd+grad", f"{N}x{V}", dt, lambda: js.jsd_forward(X, Y, 0.5), 3 * N * V * X.element_size())
+        del X, Y
+    for n, D, dt in ((4, 4096, F16), (8, 4096, F16), (8, 8192, F16), (16, 4096, F16), (8, 4096, BF16)):
+        ntok = 4 * 2048
+        Vb, wq, wn, dh = rnd(n, ntok, D, dt=dt), (0.02 * rnd(D)).to(dt), rnd(D, dt=dt), rnd(ntok, D, dt=dt)
+        _, V3, alpha, rs = ar.attn_res_forward(Vb, wq, wn)
+        hbm("AttnRes fwd", f"N {n}, 4x2048x{D}", dt, lambda: ar.attn_res_forward(Vb, wq, wn), (n + 1) * ntok * D * 2)
+        hbm("AttnRes bwd", f"N {n}, 4x2048x{D}", dt, lambda: ar.attn_res_backward(dh, V3, wq, wn, alpha, rs),
+            (2 * n + 1) * ntok * D * 2)
+        del Vb, dh, V3
+    mm = []
+    for N, H, V, dt in ((8192, 4096, 32000, F16), (8192, 4096, 128256, F16), (8192, 4096, 32000, BF16),
+                        (2048, 4096, 32000, F16)):
+        x, w = (0.5 * rnd(N, H)).to(dt), (0.02 * rnd(V, H)).to(dt)
+        t = torch.randint(0, V, (N,), generator=gen, device=dev)
+        ms = statistics.median(time_events(lambda: flce.fused_linear_cross_entropy_forward(x, w, t), 4, flush))
+        tf = 6 * N * H * V / (ms * 1e-3) / 1e12
+        mm.append(f"| FusedLinearCE fwd+grad | {N}x{H}x{V} | {dname[dt]} | {ms:.2f} ms | {tf:.0f} TFLOP/s | "
+                  f"{tf / BF16_PEAK_TFLOPS:.1%} |")
+        log(mm[-1])
+        del x, w
+    for N, H, V, dt in ((4096, 4096, 32000, F16), (2048, 4096, 128256, F16), (4096, 4096, 32000, BF16)):
+        xs, xt = (0.5 * rnd(N, H)).to(dt), (0.5 * rnd(N, H)).to(dt)
+        ws, wt = (0.02 * rnd(V, H)).to(dt), (0.02 * rnd(V, H)).to(dt)
+        ms = statistics.median(time_events(lambda: fljsd.fused_linear_jsd_forward(xs, ws, xt, wt), 4, flush))
+        tf = 8 * N * H * V / (ms * 1e-3) / 1e12
+        mm.append(f"| FusedLinearJSD fwd+grad | {N}x{H}x{V} | {dname[dt]} | {ms:.2f} ms | {tf:.0f} TFLOP/s | "
+                  f"{tf / BF16_PEAK_TFLOPS:.1%} |")
+        log(mm[-1])
+        del xs, ws, xt, wt
+    print("| Op | Shape | dtype | Time | Achieved | Copy of the same bytes | Op / copy |")
+    print("|---|---|---|---|---|---|---|")
+    print("\n".join(rows))
+    print()
+    print("| Op | Shape | dtype | Time | Achieved | of 2.5 PFLOP/s bf16 dense |")
+    print("|---|---|---|---|---|---|")
+    print("\n".join(mm))
+
+
 def load_traffic(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -473,6 +605,8 @@ def main(argv=None):
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="finish with three plain 1 GiB device-to-device copies (reference kernel of known "
                          "traffic for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
+    ap.add_argument("--reference-configs", action="store_true",
+                    help="instead of the step: every op on the reference benchmarks' own shapes, as a markdown table")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -488,6 +622,9 @@ def main(argv=None):
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.reference_configs:
+        reference_configs(dev, max(3, args.op_reps // 2))
+        return 0
     log(f"device: {torch.cuda.get_device_name(dev)}")
     c2 = C2Step(K, dev)
 

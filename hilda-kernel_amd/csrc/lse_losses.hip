@@ -901,20 +901,37 @@ __global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const G
     return v;
   };
   double loss = 0.0, msum = 0.0, kls = 0.0, clips = 0.0;
+  constexpr int U = 4;  // tokens a lane loads before it adds: four loads in flight, not one
   for (int64_t b = wave; b < a.B; b += 16) {
     double ls = 0.0, ms = 0.0, ks = 0.0, cs = 0.0;
-    for (int64_t l = lane; l < a.L; l += kWave) {
-      const int64_t o = b * a.L + l;
-      const double m = tok[o].m;
-      const GrpoOut r = res[o];
-      ls += m * r.loss;
-      ms += m;
-      ks += m * r.kl;
-      cs += m * r.clip;
-      a.lse_rows[o] = r.lse;
-      a.loss_rows[o] = r.loss;
-      a.kl_rows[o] = r.kl;
-      a.clip_rows[o] = r.clip;
+    for (int64_t l0 = lane; l0 < a.L; l0 += U * kWave) {
+      float mv[U];
+      GrpoOut rv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t l = l0 + u * kWave;
+        if (l < a.L) {
+          mv[u] = tok[b * a.L + l].m;
+          rv[u] = res[b * a.L + l];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t l = l0 + u * kWave;
+        if (l < a.L) {
+          const int64_t o = b * a.L + l;
+          const double m = mv[u];
+          const GrpoOut r = rv[u];
+          ls += m * r.loss;
+          ms += m;
+          ks += m * r.kl;
+          cs += m * r.clip;
+          a.lse_rows[o] = r.lse;
+          a.loss_rows[o] = r.loss;
+          a.kl_rows[o] = r.kl;
+          a.clip_rows[o] = r.clip;
+        }
+      }
     }
     ls = wsum(ls);
     ms = wsum(ms);

@@ -135,9 +135,10 @@ def test_workspace_query_is_pure():
     atom = lib.hk_rms_norm_bwd_workspace_size(8192, 4096, 2, 2, _lib.DW_ATOMIC, 0)
     assert atom == 4096 * 8
     assert part >= 4096 * 4 and part % (4096 * 4) == 0
-    # fp32 inputs accumulate in fp64 registers but store fp32 partial rows too
+    # fp32 inputs accumulate in fp64 registers but store fp32 partial rows too, one per row group (16-bit
+    # inputs sum a 1024-lane block's groups in LDS first, so they store fewer rows)
     part32 = lib.hk_rms_norm_bwd_workspace_size(8192, 4096, 0, 0, _lib.DW_PARTIAL, 0)
-    assert part32 == part
+    assert part32 % (4096 * 4) == 0 and part32 >= part
     assert lib.hk_rms_norm_bwd_workspace_size(-1, 4096, 2, 2, 0, 0) == 0
     # the default mode takes the partial rows at every row count (no atomics for few rows)
     for rows in (16, 2048, 8192):

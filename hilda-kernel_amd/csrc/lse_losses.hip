@@ -9,9 +9,13 @@
 // (a 32000-entry bf16 row is 16 vectors per lane of 256 lanes, four blocks a
 // CU; a 128256-entry row 16 vectors per lane of 1024 lanes, 64 VGPRs),
 // so the row crosses HBM once: read, max, sum of 2^(x*c - m), then the
-// gradient (p - onehot) * g is written straight from the registers. Rows that
-// do not fit use a streaming variant that keeps a per-lane online (max, sum)
-// and reads the row a second time for the gradient.
+// gradient p * g is written straight from the registers, p recomputed in fp32
+// and rounded once as the reference does. The target column is left out of
+// the reduction and its term added from the target logit afterwards, so its
+// gradient -(1 - p_t) * g is formed from the other columns' mass instead of
+// p_t - 1 (which cancels in fp32 when p_t is near 1). Rows that do not fit use
+// a streaming variant that keeps a per-lane online (max, sum) and reads the
+// row a second time for the gradient.
 //
 // All exponentials run on v_exp_f32 (2^x) with log2(e)/T folded into one
 // multiply-add per element; log-sum-exp is kept in the log2 domain and
@@ -35,39 +39,6 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   float r;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
-}
-
-// Storage of exp values in a row's registers: fp32 stays fp32; for 16-bit rows
-// the values (all in [0, 1]) are kept as fp16, whose 11-bit significand is
-// finer than the bf16 the gradient is finally rounded to.
-template <typename T, int VEC>
-__device__ __forceinline__ Pack<T, VEC> pack_e(const float (&x)[VEC]) {
-  if constexpr (sizeof(T) == 4) {
-    return pack<T, VEC>(x);
-  } else {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    Pack<T, VEC> r;
-#pragma unroll
-    for (int k = 0; k < VEC / 2; ++k)
-      r.w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x[2 * k], x[2 * k + 1]}), h2));
-    return r;
-  }
-}
-
-template <typename T, int VEC>
-__device__ __forceinline__ void unpack_e(const Pack<T, VEC>& p, float (&x)[VEC]) {
-  if constexpr (sizeof(T) == 4) {
-    unpack(p, x);
-  } else {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-    for (int k = 0; k < VEC / 2; ++k) {
-      const h2 h = __builtin_bit_cast(h2, p.w[k]);
-      x[2 * k] = (float)h.x;
-      x[2 * k + 1] = (float)h.y;
-    }
-  }
 }
 
 template <typename T, int VEC, int NCH, int BLOCK>
@@ -111,50 +82,27 @@ struct RowRegs {
     for (int j = 0; j < NCH; ++j) make_opaque(v[j]);
   }
 
-  // This lane's (max, sum) of x*c in the log2 domain, computed exactly as
-  // lse2_to_exp does but leaving the registers as they are (a forward-only
-  // pass refills them with the next row right after).
-  __device__ __forceinline__ void lse2_local(int n, float c, float* m_out, float* s_out) {
+  // The reduction of this lane, leaving out the element at column `target`
+  // (< 0: none): m = max of x*c (log2 domain) and s = sum 2^(x*c - m) over the
+  // lane's other elements; the registers keep x. The caller adds the target's
+  // own term from its logit after the block reduction (target_merge), which
+  // gives 1 - p_t without the cancellation of computing it from p_t in fp32
+  // when p_t is close to 1. The target's vector is a uniform test, and only
+  // that vector's unpacked floats are masked (rewriting the registers would
+  // make the compiler carry every vector through phi copies).
+  __device__ __forceinline__ void reduce_lane(int n, float c, int target, float* m_out, float* s_out) {
+    const int jt = target >= 0 ? target / kSpan : -1;  // uniform
+    const int rel = target - jt * kSpan - lane_col();  // in [0, VEC) in the owning lane only
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       if (j * kSpan < n) {
         float x[VEC];
         unpack(v[j], x);
+        if (j == jt) {
 #pragma unroll
-        for (int e = 0; e + 1 < VEC; e += 2) m = max3(m, x[e], x[e + 1]);
-        if constexpr (VEC & 1) m = fmaxf(m, x[VEC - 1]);
-      }
-    }
-    m *= c;
-    opaque();
-    const float mo = m == -INFINITY ? 0.f : m;
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      if (j * kSpan < n) {
-        float x[VEC];
-        unpack(v[j], x);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) s += exp2_fast(fmaf(x[e], c, -mo));
-      }
-      __builtin_amdgcn_sched_barrier(0);  // one vector's floats live at a time
-    }
-    *m_out = m;
-    *s_out = s;
-  }
-
-  // This lane's (max, sum) of x*c in the log2 domain, m = max and
-  // s = sum 2^(x*c - m); the registers are overwritten with e = 2^(x*c - m)
-  // (see pack_e), so the gradient needs one multiply per element, not a
-  // second exponential. Padding (-inf) becomes 0.
-  __device__ __forceinline__ void lse2_to_exp(int n, float c, float* m_out, float* s_out) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      if (j * kSpan < n) {
-        float x[VEC];
-        unpack(v[j], x);
+          for (int e = 0; e < VEC; ++e) x[e] = e == rel ? -INFINITY : x[e];
+        }
 #pragma unroll
         for (int e = 0; e + 1 < VEC; e += 2) m = max3(m, x[e], x[e + 1]);
         if constexpr (VEC & 1) m = fmaxf(m, x[VEC - 1]);
@@ -169,12 +117,12 @@ struct RowRegs {
       if (j * kSpan < n) {
         float x[VEC];
         unpack(v[j], x);
+        if (j == jt) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          x[e] = exp2_fast(fmaf(x[e], c, -mo));
-          s += x[e];
+          for (int e = 0; e < VEC; ++e) x[e] = e == rel ? -INFINITY : x[e];
         }
-        v[j] = pack_e<T, VEC>(x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += exp2_fast(fmaf(x[e], c, -mo));
       }
       __builtin_amdgcn_sched_barrier(0);  // one vector's floats live at a time
     }
@@ -182,11 +130,15 @@ struct RowRegs {
     *s_out = s;
   }
 
-  // Gradient from the exp registers, (e * f) with f = 2^(m_lane - lse2) * g,
-  // without the one-hot term (the caller patches the target element), then
-  // the row at `next` loaded into the same registers vector by vector, so the
-  // row's stores and the next row's loads are in flight together.
-  __device__ __forceinline__ void store_exp_grad_then_load(T* out, int n, float f, const T* next) {
+  // Gradient of the row, p_j * g = 2^(x_j*c - lse2) * g computed in fp32 and
+  // rounded once to T (the arithmetic of kernels/cross_entropy.py:159-166),
+  // without the one-hot term (the caller patches the target element); then the
+  // row at `next` loaded into the same registers vector by vector, so the row's
+  // stores and the next row's loads are in flight together. Recomputing the
+  // exponential here instead of keeping 2^(x*c - m) from the sum pass measured
+  // as fast (the sum pass, which runs while HBM idles, writes no registers).
+  __device__ __forceinline__ void store_prob_grad_then_load(T* out, int n, float c, float lse2, float g,
+                                                            const T* next) {
     const int tc = lane_col();
     const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
 #pragma unroll
@@ -194,9 +146,9 @@ struct RowRegs {
       const int lim = n - j * kSpan;  // uniform
       if (lim > 0) {
         float x[VEC];
-        unpack_e<T, VEC>(v[j], x);
+        unpack(v[j], x);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) x[e] *= f;
+        for (int e = 0; e < VEC; ++e) x[e] = exp2_fast(fmaf(x[e], c, -lse2)) * g;
         if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
         if (lim >= kSpan) {
           v[j] = load_pack<T, VEC>(next + off(j, tc));
@@ -206,58 +158,6 @@ struct RowRegs {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-  // Gradient of this row, then the row at `next` loaded into the same
-  // registers vector by vector: each vector is refilled right after its
-  // gradient is stored, so the row's stores and the next row's loads are in
-  // flight together.
-  __device__ __forceinline__ void store_grad_then_load(T* out, int n, float c, float lse2, int target, float g,
-                                                       const T* next) {
-    const int tc = lane_col();
-    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int lim = n - j * kSpan;  // uniform
-      if (lim > 0) {
-        float x[VEC];
-        unpack(v[j], x);
-        const int rel = (target - j * kSpan) - tc;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float p = exp2_fast(fmaf(x[e], c, -lse2));
-          x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
-        }
-        if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
-        if (lim >= kSpan) {
-          v[j] = load_pack<T, VEC>(next + off(j, tc));
-        } else {
-          const Pack<T, VEC> y = load_pack<T, VEC>(next + off(j, tc < lim ? tc : 0));
-          v[j] = tc < lim ? y : ninf;
-        }
-      }
-    }
-  }
-
-  // out[j] = (2^(x*c - lse2) - [j == target]) * g   (target < 0: no one-hot)
-  __device__ __forceinline__ void store_grad(T* __restrict__ out, int n, float c, float lse2, int target,
-                                             float g) const {
-    const int tc = lane_col();
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int lim = n - j * kSpan;  // uniform
-      if (lim > 0) {
-        float x[VEC];
-        unpack(v[j], x);
-        const int rel = (target - j * kSpan) - tc;  // one compare base per vector
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float p = exp2_fast(fmaf(x[e], c, -lse2));
-          x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
-        }
-        if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
-      }
     }
   }
 };
@@ -288,11 +188,12 @@ __device__ __forceinline__ void lse2_merge(float& m, float& s, float m2, float s
   s = a + b;
 }
 
-// Block-wide log2-sum-exp from per-lane (m, s) pairs: one LDS exchange. `red`
-// holds 2*NW floats per parity; alternating `parity` between consecutive calls
-// lets the exchange go without a trailing barrier.
+// Block-wide (max, sum) of per-lane (m, s) pairs, one LDS exchange: *M the
+// block max, *S the sum scaled to it. `red` holds 2*NW floats per parity;
+// alternating `parity` between consecutive calls lets the exchange go without
+// a trailing barrier.
 template <int NW>
-__device__ __forceinline__ float block_lse2(float m, float s, float* red, int parity) {
+__device__ __forceinline__ void block_lse2_ms(float m, float s, float* red, int parity, float* M, float* S) {
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) lse2_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
   if constexpr (NW > 1) {
@@ -308,13 +209,33 @@ __device__ __forceinline__ float block_lse2(float m, float s, float* red, int pa
 #pragma unroll
     for (int i = 1; i < NW; ++i) lse2_merge(m, s, r[i], r[NW + i]);
   }
-  return m + log2_fast(s);
+  *M = m;
+  *S = s;
 }
 
-// Streaming row log-sum-exp (any length): per-lane online (max, sum), then a block combine.
-template <typename T, int VEC, int BLOCK>
-__device__ __forceinline__ float row_lse2_stream(const T* __restrict__ row, int n, float c, float* red) {
-  float m = -INFINITY, s = 0.f;
+// The row's log2-sum-exp from the (max, sum) of every column but the target,
+// (M, R), and the target's x*c, xtc: the target's term 2^(xtc) joins the sum,
+// and *rest = R / S is 1 - p_t, the mass outside the target, exact where
+// 1 - 2^(xtc - lse2) would cancel. has_target false: lse2 of (M, R), rest 1.
+// Both results are uniform: they are returned through readfirstlane so they
+// sit in scalar registers, off the row's VGPR budget.
+__device__ __forceinline__ float target_merge(float M, float R, float xtc, bool has_target, float* rest) {
+  float m = M, s = R;
+  if (has_target) lse2_merge(m, s, xtc, 1.f);
+  const float r = M == -INFINITY ? 0.f : R * exp2_fast(M - m);
+  const float q = s > 0.f ? r * rcp_fast(s) : 0.f;  // (v_rcp_f32: 1 ulp)
+  *rest = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, q)));
+  const float lse2 = m + log2_fast(s);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, lse2)));
+}
+
+// Streaming row log-sum-exp (any length): per-lane online (max, sum), then a
+// block combine. With REST, *rest = 1 - p_target from a second sum that leaves
+// the target column out (see reduce_lane).
+template <typename T, int VEC, int BLOCK, bool REST = false>
+__device__ __forceinline__ float row_lse2_stream(const T* __restrict__ row, int n, float c, float* red,
+                                                 int target = -1, float* rest = nullptr) {
+  float m = -INFINITY, s = 0.f, r = 0.f;
   for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC) {
     float x[VEC];
     unpack(load_pack<T, VEC>(row + col), x);
@@ -322,21 +243,34 @@ __device__ __forceinline__ float row_lse2_stream(const T* __restrict__ row, int 
 #pragma unroll
     for (int e = 1; e < VEC; ++e) tm = fmaxf(tm, x[e]);
     const float mn = fmaxf(m, tm * c);
-    float add = 0.f;
+    const float sc = m == -INFINITY ? 0.f : exp2_fast(m - mn);
+    float add = 0.f, add_r = 0.f;
+    const int rel = target - col;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) add += exp2_fast(fmaf(x[e], c, -mn));
-    s = (m == -INFINITY ? 0.f : s * exp2_fast(m - mn)) + add;
+    for (int e = 0; e < VEC; ++e) {
+      const float p = exp2_fast(fmaf(x[e], c, -mn));
+      add += p;
+      if constexpr (REST) add_r += e == rel ? 0.f : p;
+    }
+    s = s * sc + add;
+    if constexpr (REST) r = r * sc + add_r;
     m = mn;
   }
   const float M = block_max<BLOCK / kWave>(m, red);
-  const float sc = (m == -INFINITY) ? 0.f : s * exp2_fast(m - M);
-  const float S = block_sum<BLOCK / kWave>(sc, red);
+  const float f = (m == -INFINITY) ? 0.f : exp2_fast(m - M);
+  const float S = block_sum<BLOCK / kWave>(s * f, red);
+  if constexpr (REST) {
+    const float R = block_sum<BLOCK / kWave>(r * f, red);
+    *rest = S > 0.f ? R / S : 0.f;
+  }
   return M + log2_fast(S);
 }
 
+// out[j] = p_j * g with p_j = 2^(x_j*c - lse2), and at the target column
+// -rest * g (= (p_t - 1) * g, rest from row_lse2_stream<REST>).
 template <typename T, int VEC, int BLOCK>
 __device__ __forceinline__ void store_grad_stream(T* __restrict__ out, const T* __restrict__ row, int n, float c,
-                                                  float lse2, int target, float g) {
+                                                  float lse2, int target, float rest, float g) {
   for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC) {
     float x[VEC];
     unpack(load_pack<T, VEC>(row + col), x);
@@ -344,22 +278,36 @@ __device__ __forceinline__ void store_grad_stream(T* __restrict__ out, const T* 
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float p = exp2_fast(fmaf(x[e], c, -lse2));
-      x[e] = (p - (e == rel ? 1.f : 0.f)) * g;
+      x[e] = (e == rel ? -rest : p) * g;
     }
     store_pack_nt<T, VEC>(out + col, pack<T, VEC>(x));
   }
 }
 
+// The target column of a row (col < 0: none) and its logit times c.
+struct RowTarget {
+  int col;
+  float xtc;
+};
+struct NoTarget {
+  template <class Ctx>
+  __device__ RowTarget operator()(const Ctx&) const { return RowTarget{-1, 0.f}; }
+};
+
 // Forward-only row loop, register-resident: the block's rows (row, row + G,
 // ...) that next_live accepts, each held in VGPRs. A row's lanes reduce their
 // (max, sum) from the registers, then refill them with the next row before the
 // block-wide combine, so the next row's loads are in flight during the
-// exchange and the caller's per-row epilogue. emit(row, lse2) runs on every
-// lane with the row's log2-sum-exp of x * c; pre(row) runs before the row's
-// reduction (for loads that should overlap it).
-template <typename T, int VEC, int NCH, int BLOCK, class RowPtr, class NextLive, class Pre, class Emit>
+// exchange and the caller's per-row epilogue. emit(row, lse2, ctx) runs on
+// every lane with the row's log2-sum-exp of x * c; ctx = pre(row) runs before
+// the row's reduction (for loads that should overlap it). target_of(ctx)
+// names a column that the reduction leaves out and adds back afterwards
+// (target_merge), exactly as the gradient kernels do, so a forward-only call
+// returns bitwise the same results as the gradient form.
+template <typename T, int VEC, int NCH, int BLOCK, class RowPtr, class NextLive, class Pre, class TargetOf,
+          class Emit>
 __device__ __forceinline__ void lse_rows_resident(int n, float c, int64_t rows, float* red, RowPtr row_ptr,
-                                                  NextLive next_live, Pre pre, Emit emit) {
+                                                  NextLive next_live, Pre pre, TargetOf target_of, Emit emit) {
   int64_t row = next_live((int64_t)blockIdx.x);
   if (row >= rows) return;
   RowRegs<T, VEC, NCH, BLOCK> r;
@@ -368,12 +316,15 @@ __device__ __forceinline__ void lse_rows_resident(int n, float c, int64_t rows, 
   for (;;) {
     const int64_t next = next_live(row + (int64_t)gridDim.x);
     auto ctx = pre(row);
+    const RowTarget tg = target_of(ctx);
     float m, s;
-    r.lse2_local(n, c, &m, &s);
+    r.reduce_lane(n, c, tg.col, &m, &s);
     r.opaque();
     __builtin_amdgcn_sched_barrier(0);  // the refill may not start before the row is reduced (register reuse)
     if (next < rows) r.load(row_ptr(next), n);
-    const float lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+    float M, S, rest;
+    block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &S);
+    const float lse2 = target_merge(M, S, tg.xtc, tg.col >= 0, &rest);
     parity ^= 1;
     emit(row, lse2, ctx);
     if (next >= rows) break;
@@ -447,9 +398,10 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
       const int64_t next = next_live(row + G);
       const float xt = to_f32<T>(in[t]);
       const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
-      float m, s;
-      r.lse2_to_exp(n, kLog2e, &m, &s);
-      const float lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+      float m, s, M, R, rest;
+      r.reduce_lane(n, kLog2e, (int)t, &m, &s);
+      block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R);
+      const float lse2 = target_merge(M, R, xt * kLog2e, true, &rest);
       parity ^= 1;
       r.opaque();
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
@@ -457,12 +409,11 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
       // registers carry one definition around the loop
       const T* src = next < a.rows ? logits + next * a.ld_in : in;
       T* out = dlogits + row * a.ld_out;
-      const float f = m == -INFINITY ? 0.f : exp2_fast(m - lse2) * gscale;
-      r.store_exp_grad_then_load(out, n, f, src);
-      // the target element: (p_t - 1) * g, from x_t in fp32, stored after (and
+      r.store_prob_grad_then_load(out, n, kLog2e, lse2, gscale, src);
+      // the target element: (p_t - 1) * g = -(1 - p_t) * g, stored after (and
       // over) the vector store of the same thread
       if ((int)threadIdx.x == (int)(t % RowRegs<T, VEC, NCH, BLOCK>::kSpan) / VEC)
-        out[t] = from_f32<T>((exp2_fast(fmaf(xt, kLog2e, -lse2)) - 1.f) * gscale);
+        out[t] = from_f32<T>(-rest * gscale);
       if (next >= a.rows) break;
       row = next;
     }
@@ -480,9 +431,10 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
       }
       const float xt = to_f32<T>(in[t]);
       const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
-      const float lse2 = row_lse2_stream<T, VEC, BLOCK>(in, (int)a.V, kLog2e, red1);
+      float rest;
+      const float lse2 = row_lse2_stream<T, VEC, BLOCK, true>(in, (int)a.V, kLog2e, red1, (int)t, &rest);
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
-      store_grad_stream<T, VEC, BLOCK>(out, in, (int)a.V, kLog2e, lse2, (int)t, gscale);
+      store_grad_stream<T, VEC, BLOCK>(out, in, (int)a.V, kLog2e, lse2, (int)t, rest, gscale);
     }
   }
 }
@@ -518,7 +470,7 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_kernel(const T* __restrict__ log
   if constexpr (RESIDENT) {
     lse_rows_resident<T, VEC, NCH, BLOCK>(
         row_len(a.V), kLog2e, a.rows, red, [&](int64_t row) { return logits + row * a.ld_in; },
-        [](int64_t q) { return q; }, target, emit);
+        [](int64_t q) { return q; }, target, NoTarget{}, emit);
   } else {
     // the target logit is read after the row (its address waits on the target
     // load, which would hold back the row's loads behind it)
@@ -659,7 +611,8 @@ __global__ __launch_bounds__(BLOCK) void selective_log_softmax_kernel(const T* _
       while (q < rows && masked(q)) q += G;
       return q;
     };
-    lse_rows_resident<T, VEC, NCH, BLOCK>(row_len(a.V), c, rows, red, row_ptr, next_live, target, emit);
+    lse_rows_resident<T, VEC, NCH, BLOCK>(row_len(a.V), c, rows, red, row_ptr, next_live, target, NoTarget{},
+                                          emit);
   } else {
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
       if (masked(r)) continue;
@@ -727,8 +680,12 @@ __device__ __forceinline__ GrpoOut grpo_terms(const GrpoHot& a, const GrpoTok& t
 }
 
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT, bool GRAD>
-__global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, const T* __restrict__ logits,
-                                                     GrpoHot a) {
+__global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits, GrpoHot a) {
+  // dlogits may alias logits (FusedLinear-GRPO writes the gradient over the
+  // chunk's logits): the id logit is read before the row's reduction barriers,
+  // every other element is read by the thread that later overwrites it, and a
+  // row's stores are issued before the next row's loads of the same vector, so
+  // the pointers are not declared __restrict__.
   __shared__ float red[4 * (BLOCK / kWave)];
   const int64_t rows =
       a.nlim ? min(a.nrows, max((int64_t)0, (int64_t)*a.nlim - a.row0)) : a.nrows;  // row below: local to the launch
@@ -780,9 +737,10 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       tk.gs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.gs)));
       const int64_t next = next_live(row + G);
       const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
-      float m, s;
-      r.lse2_to_exp(n, c, &m, &s);
-      const float lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+      float m, s, M, R, rest;
+      r.reduce_lane(n, c, tk.id, &m, &s);
+      block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R);
+      const float lse2 = target_merge(M, R, xid * c, tk.id >= 0, &rest);
       parity ^= 1;
       r.opaque();
       const float lse = lse2 * kLn2;
@@ -794,10 +752,10 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       const float g = -dlogp * tk.gs;
       T* out = dlogits + row * a.V;
       const T* src = next < rows ? logits + next * a.V : in;  // unconditional refill (see the CE kernel)
-      const float f = m == -INFINITY ? 0.f : exp2_fast(m - lse2) * g;
-      r.store_exp_grad_then_load(out, n, f, src);
+      r.store_prob_grad_then_load(out, n, c, lse2, g, src);
+      // the id element: (p_id - 1) * g = -(1 - p_id) * g (see reduce_lane)
       if (tk.id >= 0 && (int)threadIdx.x == (tk.id % RowRegs<T, VEC, NCH, BLOCK>::kSpan) / VEC)
-        out[tk.id] = from_f32<T>((exp2_fast(fmaf(xid, c, -lse2)) - 1.f) * g);
+        out[tk.id] = from_f32<T>(-rest * g);
       if (next >= rows) break;
       row = next;
     }
@@ -825,8 +783,10 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       const GrpoOut res = grpo_terms(a, x.tk, lse, logp, &dlogp);
       if (threadIdx.x == 0) a.out[token(row)] = res;
     };
+    auto target_of = [&](const Ctx& x) { return RowTarget{x.tk.id, x.xid * c}; };
     lse_rows_resident<T, VEC, NCH, BLOCK>(
-        row_len(a.V), c, rows, red, [&](int64_t row) { return logits + row * a.V; }, next_live, pre, emit);
+        row_len(a.V), c, rows, red, [&](int64_t row) { return logits + row * a.V; }, next_live, pre, target_of,
+        emit);
   } else {
     // streaming, or forward only on 1024-lane rows: there the refill's extra
     // register pressure spills, so each row loads after the previous one
@@ -840,23 +800,24 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* __restrict__ dlogits, co
       // the id logit is read before the reduction's barriers: dlogits may alias
       // logits, and no lane stores before every lane has passed them
       const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
-      float lse2;
-      if constexpr (RESIDENT) {
+      float lse2, rest = 0.f;
+      if constexpr (RESIDENT) {  // (forward only: the gradient form's arithmetic, see lse_rows_resident)
         RowRegs<T, VEC, NCH, BLOCK> r;
         r.load(in, n);
-        float m, s;
-        r.lse2_to_exp(n, c, &m, &s);
-        lse2 = block_lse2<BLOCK / kWave>(m, s, red, parity);
+        float m, s, M, S;
+        r.reduce_lane(n, c, tk.id, &m, &s);
+        block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &S);
+        lse2 = target_merge(M, S, xid * c, tk.id >= 0, &rest);
         parity ^= 1;
       } else {
-        lse2 = row_lse2_stream<T, VEC, BLOCK>(in, n, c, red);
+        lse2 = row_lse2_stream<T, VEC, BLOCK, GRAD>(in, n, c, red, tk.id, &rest);
       }
       const float lse = lse2 * kLn2;
       const float logp = tk.id >= 0 ? xid * a.inv_T - lse : NAN;
       float dlogp;
       const GrpoOut res = grpo_terms(a, tk, lse, logp, &dlogp);
       if (threadIdx.x == 0) a.out[token(row)] = res;
-      if constexpr (GRAD) store_grad_stream<T, VEC, BLOCK>(out, in, n, c, lse2, tk.id, -dlogp * tk.gs);
+      if constexpr (GRAD) store_grad_stream<T, VEC, BLOCK>(out, in, n, c, lse2, tk.id, rest, -dlogp * tk.gs);
     }
   }
 }

@@ -34,6 +34,9 @@ retyping its formula:
                           dlogits = -A_b/(len_b*B) * (onehot - p); ref = logp -> kl = 0;
                           brute-force python loop of the per-token objective
   linear_ce_ref           fp64 brute force (explicit dot products) on tiny shapes
+  exact_target_grad       equals fp64 autograd on ordinary rows; on a peaked row it matches the closed form
+                          -(e^-a + e^-b) / (1 + e^-a + e^-b) of a 3-logit row [0, -a, -b] written out by hand,
+                          where autograd's p_t - 1 is exactly 0
   fused_linear_grpo_ref   fp64 brute force: grpo_loss_ref on logits from explicit dot products; the
                           on-policy closed form (loss = -mean(A), dlogits = -A_b/(len_b*B) * (onehot - p) / T)
                           carried through the lm_head by explicit loops for dhidden and dweight
@@ -46,6 +49,7 @@ import torch
 import torch.nn.functional as F
 
 __all__ = [
+    "exact_target_grad",
     "rms_norm_ref", "rms_norm_bwd_closed_form", "fused_add_rms_norm_ref", "rope_tables", "rotate_half",
     "rope_ref", "swiglu_ref", "geglu_ref", "kl_div_ref", "jsd_ref", "fused_linear_jsd_ref", "attn_res_ref", "cross_entropy_ref", "selective_log_softmax_ref", "grpo_loss_ref",
     "linear_ce_ref", "fused_linear_grpo_ref", "fwd_bwd",
@@ -321,6 +325,27 @@ def fused_linear_grpo_ref(hidden, weight, completion_ids, advantages, old_logp=N
 # ---------------------------------------------------------------------------
 # helpers
 # ---------------------------------------------------------------------------
+def exact_target_grad(d, targets, ignore_index=-100):
+    """The gradient of a per-row log-softmax loss with each row's target entry formed exactly.
+
+    For rows of the form g * (p - onehot(t)) (the CrossEntropy and GRPO gradients of
+    kernels/cross_entropy.py:159-166 and kernels/grpo_loss.py:229-234) the entries sum to zero,
+    so the target entry is -(sum of the row's other entries). Autograd forms it as (p_t - 1) * g,
+    which cancels to 0 even in fp64 once 1 - p_t < 1e-16 (a logit 40 above the rest). d (..., V)
+    and targets (...): rows whose target is ignore_index or out of range are left as they are.
+    Returns a new tensor.
+    """
+    out = d.clone()
+    V = d.shape[-1]
+    flat = out.reshape(-1, V)
+    t = targets.reshape(-1)
+    for r in torch.nonzero((t != ignore_index) & (t >= 0) & (t < V)).flatten().tolist():
+        c = int(t[r])
+        row = flat[r]
+        flat[r, c] = -(row[:c].sum() + row[c + 1:].sum())
+    return out
+
+
 def fwd_bwd(fn, inputs, grads=None, dtype=torch.float32, differentiable=None):
     """Run ``fn`` on fp32 (or ``dtype``) CPU copies of ``inputs`` and backprop.
 

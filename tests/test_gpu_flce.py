@@ -138,6 +138,35 @@ def test_flce_c5_config():
     dh_ref = logits.grad.to(torch.bfloat16).double() @ wc.double()  # d(sum of rows) / dh for the sample
     assert_close(hg.grad[idx].float() * n_valid, dh_ref, name="dhidden rows * n_valid", **tol(torch.bfloat16))
     assert rel_fro(hg.grad[idx].float() * n_valid, dh_ref) < 1e-2
+    # <X, dX> = <W, dW>: both equal sum_{r,v} D_rv Z_rv (Z = X W^T, D the logits gradient), so a
+    # dropped chunk, a wrong scale or mispaired rows in either GEMM breaks the equality
+    ip_x = (h.detach().double() * hg.grad.double()).sum().item()
+    ip_w = (w.detach().double() * wg.grad.double()).sum().item()
+    assert math.isclose(ip_x, ip_w, rel_tol=1e-2), (ip_x, ip_w)
+    # sampled vocabulary rows of dW against the oracle summed over all 16384 rows: each live row's
+    # log-sum-exp from CPU fp32 logits (bf16 products summed in fp32, rounded to bf16 as the GEMM
+    # returns them), then D[:, v] and dW[v] = D[:, v]^T X in fp64
+    hc = h.detach().cpu()
+    tc = t.cpu()
+    live = (tc != -100).nonzero().squeeze(1)
+    wf = wc.float()
+    lse = torch.zeros(16384, dtype=torch.float64)
+    for i in range(0, live.numel(), 1024):
+        rows = live[i:i + 1024]
+        z = (hc[rows].float() @ wf.T).to(torch.bfloat16).float()
+        lse[rows] = torch.logsumexp(z, dim=1).double()
+    del wf
+    gen = torch.Generator().manual_seed(55)
+    hit = tc[live][torch.randperm(live.numel(), generator=gen)[:16]]
+    vs = torch.cat([hit, torch.randint(0, 128256, (16,), generator=gen)]).unique()
+    zv = (hc.double() @ wc[vs].double().T).to(torch.bfloat16).double()  # [BT, len(vs)]
+    d = torch.exp(zv - lse[:, None]) - (tc[:, None] == vs[None, :]).double()
+    d[tc == -100] = 0.0
+    dw_ref = d.T @ hc.double()  # sum-reduction gradient rows
+    got = wg.grad[vs.to(dev)].float().cpu() * n_valid
+    print(f"C5 dW rows {vs.tolist()}", flush=True)
+    assert_close(got, dw_ref, name="dW rows * n_valid", **tol(torch.bfloat16))
+    assert rel_fro(got, dw_ref) < 1e-2
 
 
 @pytest.mark.parametrize("BT,H,V,chunk,dead", [
@@ -168,3 +197,58 @@ def test_flce_dead_chunks(BT, H, V, chunk, dead):
     rows, _, _, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "none",
                                                           compute_grad=False, chunk=chunk)
     assert torch.count_nonzero(rows[(t == -100).to(dev)]).item() == 0
+
+
+def _int_case(BT, H, V, dtype, seed):
+    """hidden and weight with entries in {-1, 0, 1}: every logit is an integer below 2^8, exact in the
+    GEMM's fp32 sums and in bf16/fp16, so the oracle sees the same logits as the kernels. Logits are
+    ~N(0, 9) for H = 192; rows 3 and 40 are peaked (hidden = sign(weight[v]), logit ~128 at v)."""
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randint(-1, 2, (BT, H), generator=g).float()
+    w = torch.randint(-1, 2, (V, H), generator=g).float()
+    t = torch.randint(0, V, (BT,), generator=g)
+    t[torch.rand(BT, generator=g) < 0.1] = -100
+    for r, v in ((3, 11), (40, V - 2)):
+        h[r] = torch.where(w[v] == 0, torch.ones_like(w[v]), w[v])
+        t[r] = v
+    return h.to(dtype), w.to(dtype), t
+
+
+def _rows_check(name, actual, expected, slack):
+    """Every row whose oracle norm exceeds `slack` within 2% relative Frobenius error plus `slack`."""
+    a = actual.detach().to("cpu", torch.float64)
+    e = expected.detach().to("cpu", torch.float64)
+    n = e.norm(dim=1)
+    err = (a - e).norm(dim=1)
+    sel = n > max(slack, 1e-30)
+    assert sel.any()
+    bad = int((err[sel] > 2e-2 * n[sel] + slack).sum())
+    worst = (err[sel] / n[sel]).max().item()
+    assert bad == 0, f"{name}: {bad} of {int(sel.sum())} rows off, worst rel {worst:.3e}, " \
+                     f"{int((a.norm(dim=1)[sel] == 0).sum())} zero rows"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("BT,V", [(256, 4096), (256, 32000), (64, 128256)])
+def test_flce_wide_logits(dtype, BT, V):
+    """Wide and peaked logits through the chunk engine: every dW row (most of them sums of small
+    probabilities only) and every dhidden row within 2% of the oracle. The oracle contracts the
+    logits gradient rounded to the compute dtype, as the reference does (it stores the gradient
+    over its bf16/fp16 chunk logits, fused_linear_cross_entropy.py:76, and contracts that at
+    :158,161); for fp16 each row may also be off by one subnormal step (2^-24) per element."""
+    H = 192
+    h, w, t = _int_case(BT, H, V, dtype, BT + V)
+    print(f"wide FLCE BT={BT} V={V} {dtype}", flush=True)
+    z = (h.double() @ w.double().T).requires_grad_(True)  # exact integers
+    loss_ref = oracle.cross_entropy_ref(z, t, -100, "sum")
+    loss_ref.backward()
+    d = oracle.exact_target_grad(z.grad, t).to(dtype).double()  # the peaked rows' targets formed exactly
+    dh_ref, dw_ref = d @ w.double(), d.T @ h.double()
+    dev = gpu()
+    loss, gi, gw, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "sum",
+                                                            compute_grad=True, chunk=128)
+    assert_close(loss, loss_ref, name="loss", rtol=2e-3, atol=2e-3)
+    slack = 2.0 ** -24 * math.sqrt(BT * V) if dtype == torch.float16 else 0.0
+    _rows_check("dweight", gw, dw_ref, 2.0 ** -24 * math.sqrt(BT * H) if dtype == torch.float16 else 0.0)
+    _rows_check("dhidden", gi, dh_ref, slack)
+    assert torch.count_nonzero(gi[(t == -100).to(dev)]).item() == 0

@@ -121,6 +121,71 @@ def test_cross_entropy_upstream_grad_and_retain_graph():
     assert_close(lg2.grad, d2, name="per-row grad", rtol=1e-5, atol=1e-5)
 
 
+def _strict_tail(actual, expected, dtype, scale, name):
+    """Every gradient element the reference keeps (|expected| * scale > 1e-30) within the relative
+    tolerance and with no absolute slack, so a flushed or coarsened tail of small probabilities
+    fails. fp32: rtol 5e-5, since 2^(x*log2(e) - lse) of logits |x| ~ 60 carries the rounding of
+    a ~100-magnitude exponent (a few 1e-6), which the reference's fp32 exp shares. fp16: the
+    reference's own output is fp16, so elements below fp16's normal range (6.1e-5) are compared
+    with one subnormal step (2^-24) of slack."""
+    a = actual.detach().to("cpu", torch.float64) * scale
+    e = expected.detach().to("cpu", torch.float64) * scale
+    sel = e.abs() > 1e-30
+    assert sel.any()
+    rtol = {torch.float32: 5e-5, torch.bfloat16: 1.6e-2, torch.float16: 1.6e-2}[dtype]
+    if dtype == torch.float16:
+        a, e = actual.detach().to("cpu", torch.float64), expected.detach().to("cpu", torch.float64)
+        sel = e.abs() > 1e-30 / scale
+        err = (a - e).abs()[sel]
+        bound = rtol * e.abs()[sel] + 2.0 ** -24
+    else:
+        err = (a - e).abs()[sel]
+        bound = rtol * e.abs()[sel]
+    bad = int((err > bound).sum())
+    if bad:
+        rel = err / e.abs()[sel]
+        k = int(rel.argmax())
+        where = tuple(int(i) for i in torch.nonzero(sel)[k])
+        raise AssertionError(f"{name}: {bad} of {int(sel.sum())} elements off, worst at {where}: "
+                             f"{a[sel][k].item():.6e} vs {e[sel][k].item():.6e} (rel {rel[k].item():.3e}); "
+                             f"zeros where the oracle is nonzero: {int((a[sel] == 0).sum())}")
+
+
+def _wide_ce_case(N, V, dtype, seed):
+    """Logits ~ N(0, 8) (trained-LM width) with row 1 peaked (one logit 30 above the row's max)."""
+    logits, t = _ce_case(N, V, torch.float32, 0.15, seed, scale=8.0)
+    logits[1, 777] = logits[1].max() + 30.0
+    t[1] = 5
+    t[0] = -100
+    return logits.to(dtype), t
+
+
+# V: 256-lane resident (32000), 1024-lane resident (128256, 151936), streaming (200000)
+@pytest.mark.parametrize("V", [32000, 128256, 151936, 200000])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_cross_entropy_wide_logits(V, dtype, reduction):
+    """Wide and peaked rows: the gradient's small probabilities (down to 1e-30) match the oracle
+    (kernels/cross_entropy.py:159-166 computes exp in fp32 and rounds once to the logits dtype);
+    target entries against oracle.exact_target_grad."""
+    N = 12
+    logits, t = _wide_ce_case(N, V, dtype, V + 3)
+    print(f"wide CE V={V} {dtype} {reduction}", flush=True)
+    (l_ref,), (d_ref,) = oracle.fwd_bwd(lambda z: oracle.cross_entropy_ref(z, t, -100, reduction), [logits],
+                                        dtype=torch.float64)
+    d_ref = oracle.exact_target_grad(d_ref, t)
+    lg = logits.to(gpu()).requires_grad_(True)
+    loss = hilda_cross_entropy(lg, t.to(gpu()), -100, reduction)
+    loss.backward()
+    lt = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
+    assert_close(loss, l_ref, name="loss", **lt)
+    n_valid = int((t != -100).sum())
+    s = n_valid if reduction == "mean" else 1
+    assert_close(lg.grad, d_ref, name="dlogits", **tol(dtype))
+    _strict_tail(lg.grad, d_ref, dtype, s, "dlogits tail")
+    assert torch.count_nonzero(lg.grad[(t == -100).to(gpu())]).item() == 0
+
+
 def test_cross_entropy_c3_config():
     """C3: logits [8192, 128256] bf16 ~ N(0,2), 10% ignored, mean; generated on the GPU.
 
@@ -231,6 +296,43 @@ def test_grpo_loss(case, dtype):
     assert torch.count_nonzero(lg.grad[:, -1]).item() == 0
     if mask is not None:
         assert torch.count_nonzero(lg.grad[:, :-1][mask.to(dev) == 0]).item() == 0
+
+
+@pytest.mark.parametrize("V", [32000, 151936])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_grpo_loss_wide_logits(V, dtype):
+    """GRPO's gradient rows on N(0, 8) logits with one peaked position (its id the peak, so
+    1 - p_id ~ 1e-13): the small probabilities and the id entries match the oracle with no
+    absolute slack (kernels/grpo_loss.py:229-234); the oracle's id entries are formed exactly
+    (oracle.exact_target_grad), since fp64 autograd's p_id - 1 loses them."""
+    B, L = 2, 6
+    g = torch.Generator().manual_seed(V + 17)
+    logits = 8 * torch.randn(B, L + 1, V, generator=g)
+    logits[0, 2, 99] = logits[0, 2].max() + 30.0
+    logits = logits.to(dtype)
+    ids = torch.randint(0, V, (B, L), generator=g)
+    ids[0, 2] = 99
+    adv = torch.randn(B, generator=g)
+    logp = oracle.selective_log_softmax_ref(logits.double(), ids)
+    old = (logp + 0.05 * torch.randn(B, L, generator=g, dtype=torch.float64)).float()
+    ref = (logp + 0.1 * torch.randn(B, L, generator=g, dtype=torch.float64)).float()
+    mask = torch.ones(B, L, dtype=torch.int32)
+    mask[1, 4:] = 0
+    print(f"wide GRPO V={V} {dtype}", flush=True)
+    outs, (d_ref,) = oracle.fwd_bwd(
+        lambda z: oracle.grpo_loss_ref(z, ids, adv.double(), old.double(), ref.double(), mask, 1.0, 0.1, 0.2, 0.2),
+        [logits],
+        dtype=torch.float64)
+    dev = gpu()
+    lg = logits.to(dev).requires_grad_(True)
+    loss, _, _ = hilda_grpo_loss(lg, ids.to(dev), adv.to(dev), old.to(dev), ref.to(dev), mask.to(dev), 1.0, 0.1,
+                                 0.2, 0.2)
+    loss.backward()
+    lt = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1.6e-2, atol=1e-2)
+    assert_close(loss, outs[0], name="loss", **lt)
+    d_ref = torch.cat([oracle.exact_target_grad(d_ref[:, :L], ids), d_ref[:, L:]], dim=1)
+    _strict_tail(lg.grad, d_ref, dtype, B * L, "dlogits tail")
+    assert torch.count_nonzero(lg.grad[:, -1]).item() == 0
 
 
 def test_grpo_on_policy_closed_form_and_module():

@@ -327,6 +327,32 @@ def test_cross_entropy_ref_special_cases():
     assert torch.allclose(xr.grad, exp, atol=1e-14)
 
 
+def test_exact_target_grad():
+    # ordinary rows: the same as fp64 autograd (and ignored rows untouched)
+    x = (3 * torch.randn(6, 50, generator=_g(60), dtype=torch.float64)).requires_grad_(True)
+    t = torch.randint(0, 50, (6,), generator=_g(61))
+    t[2] = -100
+    oracle.cross_entropy_ref(x, t, -100, "sum").backward()
+    fixed = oracle.exact_target_grad(x.grad, t)
+    assert torch.allclose(fixed, x.grad, rtol=1e-12, atol=1e-15)
+    assert torch.equal(fixed[2], x.grad[2])
+    # a peaked row [0, -a, -b] with target 0: autograd's p_0 - 1 is exactly 0 in fp64,
+    # the closed form -(e^-a + e^-b) / (1 + e^-a + e^-b) is not
+    a, b = 45.0, 52.0
+    z = torch.tensor([[0.0, -a, -b]], dtype=torch.float64, requires_grad=True)
+    tz = torch.tensor([0])
+    oracle.cross_entropy_ref(z, tz, -100, "sum").backward()
+    assert z.grad[0, 0].item() == 0.0
+    ea, eb = math.exp(-a), math.exp(-b)
+    want = -(ea + eb) / (1.0 + ea + eb)
+    got = oracle.exact_target_grad(z.grad, tz)[0, 0].item()
+    assert math.isclose(got, want, rel_tol=1e-12)
+    # leading batch dimensions (GRPO's (B, L, V)), and a row scale g carried through
+    d = torch.tensor([[[0.5 * ea, 0.5 * eb, 0.0]]], dtype=torch.float64)
+    assert math.isclose(oracle.exact_target_grad(d, torch.tensor([[2]]))[0, 0, 2].item(), -0.5 * (ea + eb),
+                        rel_tol=1e-12)
+
+
 # ---------------------------------------------------------------- GRPO
 def test_selective_log_softmax_brute_force():
     B, L, V = 2, 3, 7

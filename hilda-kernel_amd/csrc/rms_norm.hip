@@ -28,6 +28,7 @@
 #include "../../include/hilda_kernel_amd.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -460,9 +461,10 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   return true;
 }
 
-int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, const void* w, const float* rstd,
-             int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_ds, int64_t ld_x, int64_t ld_dx, int dt_x,
-             int dt_w, int dw_mode, void* workspace, size_t ws_bytes, hk_stream_t stream) {
+// Argument checks of the backward entry points (no HIP call).
+int bwd_check(void* dx, void* dw, const void* dy, const void* ds, const void* x, const void* w, const float* rstd,
+              int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_ds, int64_t ld_x, int64_t ld_dx, int dt_x,
+              int dt_w, int dw_mode) {
   HK_REQUIRE(valid_dtype(dt_x) && valid_dtype(dt_w), "invalid dtype code (x=%d, w=%d)", dt_x, dt_w);
   HK_REQUIRE(rows >= 0 && cols > 0, "invalid shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
   HK_REQUIRE(cols <= (1 << 30), "cols=%lld too large", (long long)cols);
@@ -471,6 +473,15 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
   HK_REQUIRE(dw_mode == HK_DW_AUTO || dw_mode == HK_DW_ATOMIC || dw_mode == HK_DW_PARTIAL, "invalid dw_mode %d",
              dw_mode);
   HK_REQUIRE(dx && dw && dy && x && w && rstd, "null pointer argument");
+  return HK_OK;
+}
+
+int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, const void* w, const float* rstd,
+             int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_ds, int64_t ld_x, int64_t ld_dx, int dt_x,
+             int dt_w, int dw_mode, void* workspace, size_t ws_bytes, hk_stream_t stream) {
+  if (const int rc = bwd_check(dx, dw, dy, ds, x, w, rstd, rows, cols, ld_dy, ld_ds, ld_x, ld_dx, dt_x, dt_w,
+                               dw_mode))
+    return rc;
   const int es = dtype_size(dt_x), wsz = dtype_size(dt_w);
   const int vec = 16 / es;
   bool vec_ok = cols % vec == 0 && rows_aligned(dy, ld_dy, es) && rows_aligned(x, ld_x, es) &&
@@ -532,6 +543,40 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
   });
 }
 
+// ------------------------------------------------------------------------
+// allocation-free backward: the dW scratch in a file-scope device array
+// ------------------------------------------------------------------------
+// hk_rms_norm_bwd_noalloc keeps its dW partial rows (or fp64 accumulator) here
+// instead of in caller workspace. Every GPU the library runs on holds its own
+// copy, at its own address, until the process ends. Host code never uses the
+// array's name as a device address: scratch_ptr() looks the address up once
+// per device with hipGetSymbolAddress and kernels receive that pointer.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+
+// The device address of `scratch` on `device`, which must be the current
+// device; looked up on the first call for that device. nullptr on failure
+// (the error text is set).
+void* scratch_ptr(int device) {
+  static std::once_flag once[kMaxScratchDevices];
+  static void* ptr[kMaxScratchDevices];
+  static hipError_t err[kMaxScratchDevices];
+  if (device < 0 || device >= kMaxScratchDevices) {
+    set_error("device %d out of range for the scratch table", device);
+    return nullptr;
+  }
+  std::call_once(once[device], [device] {
+    void* p = nullptr;
+    err[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    ptr[device] = err[device] == hipSuccess ? p : nullptr;
+  });
+  if (!ptr[device]) set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                              hipGetErrorString(err[device]));
+  return ptr[device];
+}
+
 }  // namespace
 }  // namespace hk
 
@@ -569,6 +614,25 @@ int hk_rms_norm_bwd(void* dx, void* dw, const void* dy, const void* x, const voi
                     void* workspace, size_t workspace_bytes, hk_stream_t stream) {
   return bwd_impl(dx, dw, dy, nullptr, x, w, rstd, rows, cols, ld_dy, ld_dy, ld_x, ld_dx, dtype_x, dtype_w, dw_mode,
                   workspace, workspace_bytes, stream);
+}
+
+int hk_rms_norm_bwd_noalloc(void* dx, void* dw, const void* dy, const void* x, const void* w, const float* rstd,
+                            int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_x, int64_t ld_dx, int dtype_x,
+                            int dtype_w, int dw_mode, hk_stream_t stream) {
+  if (const int rc = bwd_check(dx, dw, dy, nullptr, x, w, rstd, rows, cols, ld_dy, ld_dy, ld_x, ld_dx, dtype_x,
+                               dtype_w, dw_mode))
+    return rc;
+  const int dev = current_device();
+  if (dev < 0) return (int)hipErrorNoDevice;
+  const size_t need = hk_rms_norm_bwd_workspace_size(rows, cols, dtype_x, dtype_w, dw_mode, dev);
+  HK_REQUIRE(need <= kNoAllocScratchBytes,
+             "rows=%lld cols=%lld need %zu bytes of dW scratch, more than the %zu this entry point holds "
+             "(use hk_rms_norm_bwd with a workspace)",
+             (long long)rows, (long long)cols, need, kNoAllocScratchBytes);
+  void* ws = scratch_ptr(dev);
+  if (!ws) return (int)hipErrorInvalidSymbol;
+  return bwd_impl(dx, dw, dy, nullptr, x, w, rstd, rows, cols, ld_dy, ld_dy, ld_x, ld_dx, dtype_x, dtype_w, dw_mode,
+                  ws, kNoAllocScratchBytes, stream);
 }
 
 int hk_fused_add_rms_norm_bwd(void* dx, void* dw, const void* dy, const void* ds_out, const void* s, const void* w,

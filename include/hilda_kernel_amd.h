@@ -79,6 +79,19 @@ int hk_rms_norm_bwd(void* dx, void* dw, const void* dy, const void* x, const voi
                     int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_x, int64_t ld_dx, int dtype_x,
                     int dtype_w, int dw_mode, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
+/* No counterpart in the reference. hk_rms_norm_bwd for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same kernels and result, with the dW scratch in a
+ * device array the library holds for each GPU it runs on (16 MiB, until the
+ * process ends) instead of a workspace argument. Calls whose
+ * hk_rms_norm_bwd_workspace_size exceeds 16 MiB are rejected with HK_EINVAL
+ * (e.g. fp32 rows wider than 8192 columns on a 256-CU GPU). Allocates nothing.
+ * Every call on one GPU uses that GPU's one array: calls that overlap on one
+ * GPU (on different streams, or from host threads without ordering) race. */
+int hk_rms_norm_bwd_noalloc(void* dx, void* dw, const void* dy, const void* x, const void* w, const float* rstd,
+                            int64_t rows, int64_t cols, int64_t ld_dy, int64_t ld_x, int64_t ld_dx, int dtype_x,
+                            int dtype_w, int dw_mode, hk_stream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* FusedAddRMSNorm                                                         */
 /* ----------------------------------------------------------------------- */

@@ -1,6 +1,6 @@
 // FusedLinearCrossEntropy, FusedLinearJSD and FusedLinear-GRPO for gfx950:
-// lm_head GEMMs on bf16/fp16 MFMA with the loss gradient produced chunk by
-// chunk, so the full (BT, V) logits never exist.
+// lm_head GEMMs on MFMA (bf16/fp16, or fp32 for fp32 inputs) with the loss
+// gradient produced chunk by chunk, so the full (BT, V) logits never exist.
 //
 // Every contraction is one "NT" GEMM (gemm_nt.h), C[M,N] = A[M,K] * B[N,K]^T
 // with both operands K-contiguous, the layout the MFMA operand fetch wants:
@@ -31,7 +31,18 @@ namespace {
 using gemm::f32x4_t;
 struct NoPrior {};
 
-// C (T) = acc, in 16-byte chunks of 8 columns.
+// Stores n (<= 4) fp32 values at p in T, one 8- or 16-byte store when n == 4.
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float* v, int n) {
+  if (n == 4) {
+    if constexpr (sizeof(T) == 4) *reinterpret_cast<f32x4_t*>(p) = f32x4_t{v[0], v[1], v[2], v[3]};
+    else *reinterpret_cast<u32x2*>(p) = u32x2{gemm::pack2<T>(v[0], v[1]), gemm::pack2<T>(v[2], v[3])};
+  } else {
+    for (int e = 0; e < n; ++e) p[e] = from_f32<T>(v[e]);
+  }
+}
+
+// C (T) = acc, in 16-byte chunks (8 columns of a 16-bit type, 4 of fp32).
 template <typename T>
 struct EpiStore {
   using Stage = T;
@@ -42,7 +53,7 @@ struct EpiStore {
   __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
   __device__ __forceinline__ void store(int row, int col, const T* v, int n, const Prior&) const {
     T* p = C + (int64_t)row * ldc + col;
-    if (n == 8) {
+    if (n == 16 / (int)sizeof(T)) {
       *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(v);
     } else {
       for (int e = 0; e < n; ++e) p[e] = v[e];
@@ -51,7 +62,7 @@ struct EpiStore {
 };
 
 // C (T) = acc with GEMM row r stored at row rows[r] of C (the live rows of a
-// compacted operand back in place), in 16-byte chunks of 8 columns.
+// compacted operand back in place), in 16-byte chunks.
 template <typename T>
 struct EpiScatter {
   using Stage = T;
@@ -63,7 +74,7 @@ struct EpiScatter {
   __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
   __device__ __forceinline__ void store(int row, int col, const T* v, int n, const Prior&) const {
     T* p = C + (int64_t)rows[row] * ldc + col;
-    if (n == 8) {
+    if (n == 16 / (int)sizeof(T)) {
       *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(v);
     } else {
       for (int e = 0; e < n; ++e) p[e] = v[e];
@@ -94,11 +105,7 @@ struct EpiAccum {
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = MODE == 0 ? v[e] : x[e] + v[e];
     if constexpr (MODE == 2) {
-      if (n == 4) {
-        *reinterpret_cast<u32x2*>(out + o) = u32x2{gemm::pack2<T>(r[0], r[1]), gemm::pack2<T>(r[2], r[3])};
-      } else {
-        for (int e = 0; e < n; ++e) out[o + e] = from_f32<T>(r[e]);
-      }
+      store4<T>(out + o, r, n);
     } else {
       if (n == 4) {
         *reinterpret_cast<f32x4_t*>(acc + o) = f32x4_t{r[0], r[1], r[2], r[3]};
@@ -213,6 +220,44 @@ __global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, con
   }
 }
 
+// The fp32 form of transpose_kernel (same arguments and zero padding): 64x64
+// tiles of 16-byte (4-element) loads and stores, staged in LDS with a pitch of
+// 65 floats so the column reads of a wave fall in distinct banks.
+__global__ __launch_bounds__(256) void transpose32_kernel(float* __restrict__ out, const float* __restrict__ in,
+                                                          int64_t rows, int64_t rows_pad, int64_t cols, int64_t ld_in,
+                                                          int64_t ld_out, const int* __restrict__ lim,
+                                                          int64_t lim_off) {
+  constexpr int P = 65;
+  __shared__ float tile[64 * P];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  if (lim) {
+    const int64_t n = *lim, v = n - lim_off;
+    rows = std::max<int64_t>(0, std::min<int64_t>(rows, v));
+    const int64_t z = std::max<int64_t>(64, std::max<int64_t>((v + 63) / 64 * 64, (n + 63) / 64 * 64 - lim_off));
+    rows_pad = std::min<int64_t>(rows_pad, z);
+    if (r0 >= rows_pad) return;  // uniform
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int rr = t / 16 + 16 * k, cc = (t % 16) * 4;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+    if (r < rows && c < cols) v = *reinterpret_cast<const f32x4_t*>(in + r * ld_in + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[rr * P + cc + e] = v[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int oc = t / 16 + 16 * k, oq = (t % 16) * 4;
+    const int64_t c = c0 + oc, r = r0 + oq;
+    if (c < cols && r < rows_pad)
+      *reinterpret_cast<f32x4_t*>(out + c * ld_out + r) =
+          f32x4_t{tile[oq * P + oc], tile[(oq + 1) * P + oc], tile[(oq + 2) * P + oc], tile[(oq + 3) * P + oc]};
+  }
+}
+
 // The dX GEMM's epilogue when it may split K. Unsplit (the GEMM's split count
 // is 1), it stores the tile like EpiScatter / EpiStore, 4 columns a chunk; split,
 // split s stores fp32 partial sums at part + (s * m + row) * ld, m the GEMM's
@@ -236,12 +281,7 @@ struct EpiDx {
   __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
   __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior&) const {
     if (nsplit == 1) {
-      T* p = C + (int64_t)(rows ? rows[row] : row) * ldc + col;
-      if (n == 4) {
-        *reinterpret_cast<u32x2*>(p) = u32x2{gemm::pack2<T>(v[0], v[1]), gemm::pack2<T>(v[2], v[3])};
-      } else {
-        for (int e = 0; e < n; ++e) p[e] = from_f32<T>(v[e]);
-      }
+      store4<T>(C + (int64_t)(rows ? rows[row] : row) * ldc + col, v, n);
       return;
     }
     float* p = part + ((int64_t)split * m + row) * ld + col;
@@ -274,13 +314,12 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(T* __restrict__ C, int6
       a += *reinterpret_cast<const f32x4_t*>(p + s * stride);
       b += *reinterpret_cast<const f32x4_t*>(p + s * stride + 4);
     }
-    const u32x4 o{gemm::pack2<T>(a[0], a[1]), gemm::pack2<T>(a[2], a[3]), gemm::pack2<T>(b[0], b[1]),
-                  gemm::pack2<T>(b[2], b[3])};
-    *reinterpret_cast<u32x4*>(C + (int64_t)(rows ? rows[r] : r) * ldc + c) = o;
+    T* o = C + (int64_t)(rows ? rows[r] : r) * ldc + c;
+    const float va[4] = {a[0], a[1], a[2], a[3]}, vb[4] = {b[0], b[1], b[2], b[3]};
+    store4<T>(o, va, 4);
+    store4<T>(o + 4, vb, 4);
   }
 }
-
-template <typename T> struct Tag { using type = T; };
 
 // lim (nullable): a device-side bound on M (or K with lim_k), see gemm::Shape
 template <typename T, class Epi>
@@ -293,18 +332,19 @@ int launch_gemm(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_
 // kernel picks auto_splits() of the tiles left after the live-row bound, so a
 // short or mostly ignored chunk (a 2048-row chunk at H = 4096 is 128 output
 // tiles) still fills the chip. 1: never split.
-int dx_max_splits(int64_t H, int64_t V) {
-  if (V % 64 != 0 || H % 8 != 0) return 1;
-  return (int)std::min<int64_t>(8, V / 64 / 16);
+// bk: the GEMM's stage depth (K elements per K tile) for the input type.
+int dx_max_splits(int64_t H, int64_t V, int bk) {
+  if (V % bk != 0 || H % 8 != 0) return 1;
+  return (int)std::min<int64_t>(8, V / bk / 16);
 }
 
 // fp32 partial-sum bytes the dX GEMM of a chunk of up to C rows can need: the
 // largest splits x rows over the row counts it may be cut to.
-size_t dx_part_bytes(int64_t C, int64_t H, int64_t V) {
-  const int smax = dx_max_splits(H, V);
+size_t dx_part_bytes(int64_t C, int64_t H, int64_t V, int bk) {
+  const int smax = dx_max_splits(H, V, bk);
   if (smax <= 1) return 0;
   size_t best = 0;
-  const int64_t ntn = cdiv(H, 256), kt = V / 64;
+  const int64_t ntn = cdiv(H, 256), kt = V / bk;
   for (int64_t mt = 1; mt <= cdiv(C, 256); ++mt) {
     const int s = gemm::auto_splits((int)(mt * ntn), (int)kt, smax);
     if (s > 1) best = std::max(best, (size_t)s * (size_t)std::min<int64_t>(C, mt * 256) * H * 4);
@@ -320,12 +360,31 @@ int launch_transpose(T* out, const T* in, int64_t rows, int64_t rows_pad, int64_
                  aligned_to(out, 16),
              "transpose: 16-byte rows and chunks expected");
   const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows_pad, 64));
-  hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out, lim,
-                     lim_off);
-  return check_launch("transpose_kernel");
+  if constexpr (sizeof(T) == 4) {
+    hipLaunchKernelGGL(transpose32_kernel, grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out, lim,
+                       lim_off);
+    return check_launch("transpose32_kernel");
+  } else {
+    hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out,
+                       lim, lim_off);
+    return check_launch("transpose_kernel");
+  }
 }
 
 int64_t pad8(int64_t x) { return (x + 7) & ~(int64_t)7; }
+
+// Input dtypes of the fused-linear ops: bf16 and fp16 (16-bit MFMA) and fp32 (fp32 MFMA).
+bool fl_dtype_ok(int dt) { return dt == HK_BF16 || dt == HK_F16 || dt == HK_F32; }
+int fl_esize(int dt) { return dt == HK_F32 ? 4 : 2; }
+
+// f(Tag<T>) for the dtype (checked by fl_dtype_ok)
+template <typename T> struct Tag { using type = T; };
+template <typename F>
+int fl_dispatch(int dt, F&& f) {
+  if (dt == HK_BF16) return f(Tag<__bf16>{});
+  if (dt == HK_F16) return f(Tag<_Float16>{});
+  return f(Tag<float>{});
+}
 
 // Leading dimension of the transposed GEMM operands (X^T, D^T): 128 bytes past
 // the K extent, so the rows of a tile's panel do not all start at the same
@@ -380,8 +439,9 @@ FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, 
       L.dt = take((size_t)V * ld_t(chunk) * es);
       L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
     }
-    const size_t pb = dx_part_bytes(chunk, H, V);
-    L.ksplit = pb ? dx_max_splits(H, V) : 1;
+    const int bk = es == 4 ? gemm::F32Cfg::BK : gemm::DefaultCfg::BK;
+    const size_t pb = dx_part_bytes(chunk, H, V, bk);
+    L.ksplit = pb ? dx_max_splits(H, V, bk) : 1;
     L.part = pb ? take(pb) : 0;
   }
   L.extra = extra ? take(extra) : 0;
@@ -494,7 +554,8 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, in
       if (rc) return rc;
       const int64_t work = cs * (H / 8);
       hipLaunchKernelGGL((splitk_sum_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(work, 256), 8192)), dim3(256),
-                         0, st, dst, H, map, part, (int)cs, (int)H, (int)(V / 64), lay.ksplit, n_live, (int)r0);
+                         0, st, dst, H, map, part, (int)cs, (int)H, (int)(V / gemm::CfgFor<T>::BK), lay.ksplit,
+                         n_live, (int)r0);
       rc = check_launch("splitk_sum_kernel");
     } else if (rowmap) {
       rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiScatter<T>{dX, H, rowmap + r0}, st, n_live,
@@ -546,16 +607,15 @@ extern "C" {
 
 size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype,
                                                     int with_grad) {
-  if (BT < 0 || H <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
-  return flce_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0, 0, true).total;
+  if (BT < 0 || H <= 0 || V <= 0 || !fl_dtype_ok(dtype)) return 0;
+  return flce_layout(BT, H, V, flce_chunk(BT, chunk), fl_esize(dtype), with_grad != 0, 0, true).total;
 }
 
 int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
                                   const void* weight, const int64_t* targets, const float* row_scale, int64_t BT,
                                   int64_t H, int64_t V, int64_t ignore_index, int reduction, int dtype, int64_t chunk,
                                   void* workspace, size_t workspace_bytes, hk_stream_t stream) {
-  HK_REQUIRE(dtype == HK_BF16 || dtype == HK_F16, "fused linear cross entropy supports bf16 and fp16 (got %d)",
-             dtype);
+  HK_REQUIRE(fl_dtype_ok(dtype), "fused linear cross entropy supports fp32, bf16 and fp16 (got %d)", dtype);
   HK_REQUIRE(BT >= 0 && H > 0 && V > 0, "invalid shape BT=%lld H=%lld V=%lld", (long long)BT, (long long)H,
              (long long)V);
   HK_REQUIRE(H % 8 == 0 && V % 8 == 0, "H and V must be multiples of 8 (16-byte rows)");
@@ -568,7 +628,7 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
                                                                              aligned_to(dweight, 16))),
              "hidden, weight and gradients must be 16-byte aligned");
   const int64_t C = flce_chunk(BT, chunk);
-  const FlceLayout lay = flce_layout(BT, H, V, C, 2, grad, 0, true);
+  const FlceLayout lay = flce_layout(BT, H, V, C, fl_esize(dtype), grad, 0, true);
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
@@ -622,22 +682,21 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
     }
     return HK_OK;
   };
-  if (dtype == HK_BF16) return run(Tag<__bf16>{});
-  return run(Tag<_Float16>{});
+  return fl_dispatch(dtype, run);
 }
 
 
 size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int dtype,
                                           int with_grad) {
-  if (BT < 0 || H <= 0 || Ht <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
-  return fljsd_layout(BT, H, Ht, V, flce_chunk(BT, chunk), 2, with_grad != 0).total;
+  if (BT < 0 || H <= 0 || Ht <= 0 || V <= 0 || !fl_dtype_ok(dtype)) return 0;
+  return fljsd_layout(BT, H, Ht, V, flce_chunk(BT, chunk), fl_esize(dtype), with_grad != 0).total;
 }
 
 int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
                         const void* t_input, const void* t_weight, const int64_t* labels, int64_t BT, int64_t H,
                         int64_t Ht, int64_t V, int64_t ignore_index, float beta, float temperature, int dtype,
                         int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
-  HK_REQUIRE(dtype == HK_BF16 || dtype == HK_F16, "fused linear JSD supports bf16 and fp16 (got %d)", dtype);
+  HK_REQUIRE(fl_dtype_ok(dtype), "fused linear JSD supports fp32, bf16 and fp16 (got %d)", dtype);
   HK_REQUIRE(BT >= 0 && H > 0 && Ht > 0 && V > 0, "invalid shape BT=%lld H=%lld Ht=%lld V=%lld", (long long)BT,
              (long long)H, (long long)Ht, (long long)V);
   HK_REQUIRE(H % 8 == 0 && Ht % 8 == 0 && V % 8 == 0, "H, Ht and V must be multiples of 8 (16-byte rows)");
@@ -652,7 +711,7 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
                  aligned_to(t_weight, 16) && (!grad || (aligned_to(dinput, 16) && aligned_to(dweight, 16))),
              "inputs, weights and gradients must be 16-byte aligned");
   const int64_t C = flce_chunk(BT, chunk);
-  const FljsdLayout lay = fljsd_layout(BT, H, Ht, V, C, 2, grad);
+  const FljsdLayout lay = fljsd_layout(BT, H, Ht, V, C, fl_esize(dtype), grad);
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
@@ -714,15 +773,15 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
     // the rows already carry 1/n (:190)
     return scaled_sum_rows_launch(loss_out, lrows, BT, 1.0f, st);
   };
-  if (dtype == HK_BF16) return run(Tag<__bf16>{});
-  return run(Tag<_Float16>{});
+  return fl_dispatch(dtype, run);
 }
 
 size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int dtype,
                                            int with_grad) {
-  if (B <= 0 || L < 0 || H <= 0 || V <= 0 || (dtype != HK_BF16 && dtype != HK_F16)) return 0;
+  if (B <= 0 || L < 0 || H <= 0 || V <= 0 || !fl_dtype_ok(dtype)) return 0;
   const int64_t BT = B * (L + 1);
-  return flce_layout(BT, H, V, flce_chunk(BT, chunk), 2, with_grad != 0, grpo_scratch_bytes(B, L)).total;
+  return flce_layout(BT, H, V, flce_chunk(BT, chunk), fl_esize(dtype), with_grad != 0, grpo_scratch_bytes(B, L))
+      .total;
 }
 
 int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float* lse_rows, float* loss_rows,
@@ -733,7 +792,7 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
                          int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t H, int64_t V,
                          float temperature, float beta, float eps_low, float eps_high, int dtype, int64_t chunk,
                          void* workspace, size_t workspace_bytes, hk_stream_t stream) {
-  HK_REQUIRE(dtype == HK_BF16 || dtype == HK_F16, "fused linear GRPO supports bf16 and fp16 (got %d)", dtype);
+  HK_REQUIRE(fl_dtype_ok(dtype), "fused linear GRPO supports fp32, bf16 and fp16 (got %d)", dtype);
   const GrpoInputs in{ids,    ids_sB, ids_sL, advantages, old_logp, old_sB,      old_sL, ref_logp,
                       ref_sB, ref_sL, mask,   mask_dtype, mask_sB,  mask_sL,     B,      L,
                       V,      temperature,    beta,       eps_low,  eps_high};
@@ -749,7 +808,7 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
              "hidden, weight and gradients must be 16-byte aligned");
   const int64_t BT = B * (L + 1);
   const int64_t C = flce_chunk(BT, chunk);
-  const FlceLayout lay = flce_layout(BT, H, V, C, 2, grad, grpo_scratch_bytes(B, L));
+  const FlceLayout lay = flce_layout(BT, H, V, C, fl_esize(dtype), grad, grpo_scratch_bytes(B, L));
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
@@ -783,8 +842,7 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
     return grpo_finalize_launch(in, scratch, loss_out, kl_out, clip_out, lse_rows, loss_rows, kl_rows, clip_rows,
                                 st);
   };
-  if (dtype == HK_BF16) return run(Tag<__bf16>{});
-  return run(Tag<_Float16>{});
+  return fl_dispatch(dtype, run);
 }
 
 }  // extern "C"

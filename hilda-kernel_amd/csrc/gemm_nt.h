@@ -1,5 +1,7 @@
-// bf16/fp16 GEMM on gfx950 MFMA: C[M,N] = sum_k A(m,k) * B(n,k), fp32
-// accumulation, result handed to an epilogue functor in 16-byte row chunks.
+// GEMM on gfx950 MFMA: C[M,N] = sum_k A(m,k) * B(n,k), fp32 accumulation,
+// result handed to an epilogue functor in 16-byte row chunks. bf16/fp16 inputs
+// run v_mfma_f32_32x32x16_{bf16,f16}; fp32 inputs (K-contiguous only) run the
+// same pipeline on v_mfma_f32_32x32x2_f32, see mma_frag.
 // Each operand is stored either K-contiguous (A[m][k], the "NT" layout) or
 // MN-contiguous (A[k][m]); the stage tiles keep that orientation in LDS and
 // the MN-contiguous ones are read with the transposing ds_read_b64_tr_b16, so
@@ -33,8 +35,9 @@
 // panels in that XCD's L2.
 //
 // gemm_nt_kernel takes any layout and K; gemm_kk_kernel is the same pipeline
-// specialised for two K-contiguous operands with K % 64 == 0, and launch()
-// picks it whenever the call qualifies.
+// specialised for two K-contiguous operands with K a multiple of the stage
+// depth (64 16-bit or 32 fp32 elements), and launch() picks it whenever the
+// call qualifies.
 #pragma once
 
 #include "hk_common.h"
@@ -96,22 +99,28 @@ __device__ __forceinline__ void apply_bound(Shape& g, int kq) {
   else g.M = min(g.M, v);
 }
 
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int GROUP_M_ = 16>
+// EPC: elements of the input type in a 16-byte chunk (8 for bf16/fp16, 4 for
+// fp32). Stage rows of BK elements are CPR = BK / EPC chunks; a sub-step
+// consumes two chunks of k per row (one per half-wave of the MFMA operand),
+// one 16-bit MFMA or MPF = 4 fp32 MFMAs per fragment pair.
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int GROUP_M_ = 16, int EPC_ = 8>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
-  static constexpr int GROUP_M = GROUP_M_;
+  static constexpr int GROUP_M = GROUP_M_, EPC = EPC_;
+  static constexpr int MPF = EPC == 8 ? 1 : 4;     // MFMA instructions per fragment pair
   static constexpr int NW = WGM * WGN, NT = NW * 64;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int CPR = BK / 8, RPI = 64 / CPR;  // chunks per row, rows per load instruction
+  static constexpr int CPR = BK / EPC, RPI = 64 / CPR;  // chunks per row, rows per load instruction
   static constexpr int IA = BM / RPI / NW, IB = BN / RPI / NW;  // load instructions per wave per stage
   static constexpr int NI = IA + IB;
-  static constexpr int NKS = BK / 16;              // MFMA sub-steps per stage
+  static constexpr int NKS = BK / (2 * EPC);       // MFMA sub-steps per stage
   static constexpr int NR = TM + TN;               // LDS reads per sub-step
   static constexpr int STAGE = (BM + BN) * BK;     // elements per stage
+  static_assert(EPC == 8 || EPC == 4, "16-bit or 32-bit elements");
   static_assert(IA * RPI * NW == BM && IB * RPI * NW == BN, "stage tile must split in 1 KiB loads");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32x32");
-  static_assert(CPR == 4 || CPR == 8, "BK must be 32 or 64");
+  static_assert(CPR == 4 || CPR == 8, "stage rows of 64 or 128 bytes");
   static_assert(STAGES >= 2 && (STAGES - 1) * NI <= 63, "outstanding loads must fit vmcnt");
   static_assert(TM * TN >= NR, "sub-step must hold enough MFMAs to cover its reads");
   static constexpr int Q = NW >= 8 ? 2 : 4;        // MFMAs of a stage's last sub-step issued before its barrier
@@ -127,14 +136,55 @@ struct Cfg {
 // 128x128, BK=32 with 4 or 5 stages and groups of 6, 8, 16 and 32.
 using DefaultCfg = Cfg<256, 256, 64, 2, 4, 2, 4>;
 
+// fp32 inputs: the same tiles, waves and stage bytes (BK = 32 fp32 is the
+// 128-byte stage row of BK = 64 bf16), so the LDS layout, swizzle and DMA are
+// unchanged; each fragment pair feeds four fp32 MFMAs.
+using F32Cfg = Cfg<256, 256, 32, 2, 4, 2, 4, 4>;
+
+template <typename T>
+using CfgFor = typename std::conditional<sizeof(T) == 4, F32Cfg, DefaultCfg>::type;
+
+// One MFMA step of a fragment pair: a and b are 16-byte operand fragments in
+// which lane l holds row l % 32 at the chunk's k offsets 8*(l/32) .. +7
+// (16-bit) or 4*(l/32) .. +3 (fp32). 16-bit: one 32x32x16 MFMA. fp32: element
+// q of every lane feeds 32x32x2 MFMA number q, which sums lane l's k
+// (= l/32 in the instruction) over the two half-waves, so the four MFMAs
+// together sum over the chunk pair's eight k (in another order than a plain
+// k loop; the same products and one fp32 accumulation).
 template <typename T>
 __device__ __forceinline__ f32x16_t mfma32(const u32x4& a, const u32x4& b, const f32x16_t& c) {
-  if constexpr (std::is_same<T, __bf16>::value)
+  if constexpr (std::is_same<T, __bf16>::value) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                    c, 0, 0, 0);
-  else
+  } else if constexpr (std::is_same<T, _Float16>::value) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
                                                   0, 0, 0);
+  } else {
+    static_assert(std::is_same<T, float>::value, "bf16, fp16 or fp32 inputs");
+    // (the whole vector is cast and then indexed: __builtin_bit_cast of a
+    // single vector element, a.y, reads element 0 with this compiler)
+    const f32x4_t af = __builtin_bit_cast(f32x4_t, a), bf = __builtin_bit_cast(f32x4_t, b);
+    f32x16_t r = c;
+    r = __builtin_amdgcn_mfma_f32_32x32x2f32(af[0], bf[0], r, 0, 0, 0);
+    r = __builtin_amdgcn_mfma_f32_32x32x2f32(af[1], bf[1], r, 0, 0, 0);
+    r = __builtin_amdgcn_mfma_f32_32x32x2f32(af[2], bf[2], r, 0, 0, 0);
+    r = __builtin_amdgcn_mfma_f32_32x32x2f32(af[3], bf[3], r, 0, 0, 0);
+    return r;
+  }
+}
+
+// acc[t / TN][t % TN] += fragment pairs t of [first, first + count): one
+// MFMA each for 16-bit inputs, four chained ones (the same accumulator) for
+// fp32; interleaving the fp32 parts across accumulators instead needed 256
+// VGPRs and spilled, the chained order 244 without spills.
+template <typename T, class C>
+__device__ __forceinline__ void mma_frags(f32x16_t (&acc)[C::TM][C::TN], const u32x4* fa, const u32x4* fb, int first,
+                                          int count) {
+#pragma unroll
+  for (int t = first; t < first + count; ++t) {
+    const int i = t / C::TN, j = t % C::TN;
+    acc[i][j] = mfma32<T>(fb[j], fa[i], acc[i][j]);
+  }
 }
 
 // two values rounded to the 16-bit type T, packed low-first into one word
@@ -147,16 +197,16 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // XOR applied to the 16-byte chunk index of a stage row, chosen (by measuring
 // ds_read_b128 rates over candidate patterns on gfx950) so that the rows read
 // together at one logical chunk fall in distinct banks.
-template <int BK>
+template <int CPR>
 __device__ __forceinline__ int swz_xor(int row) {
-  constexpr int CPR = BK / 8;
   if constexpr (CPR == 8) return (row ^ (row >> 3)) & 7;
   else return (row ^ (row >> 2)) & 3;
 }
 
-template <int BK>
+// element offset of chunk kc of stage row `row`
+template <class C>
 __device__ __forceinline__ int swz(int row, int kc) {
-  return row * BK + ((kc ^ swz_xor<BK>(row)) << 3);
+  return row * C::BK + (kc ^ swz_xor<C::CPR>(row)) * C::EPC;
 }
 
 template <int GROUP_M>
@@ -209,7 +259,10 @@ template <typename T, class C, int ROWS, bool MN>
 struct Operand {
   static constexpr int I = ROWS * C::BK * (int)sizeof(T) / 1024 / C::NW;  // 1 KiB loads per wave per stage
   static_assert(I * 1024 * C::NW == ROWS * C::BK * (int)sizeof(T), "stage tile must split in 1 KiB loads");
+  static_assert(C::EPC * (int)sizeof(T) == 16, "configuration made for another element size");
+  static_assert(!MN || sizeof(T) == 2, "MN-contiguous operands are 16-bit (ds_read_b64_tr_b16)");
   static_assert(!MN || ROWS / 8 >= 16, "MN-contiguous tiles need at least 16 chunks per k-row");
+  static constexpr int kLoadElems = 1024 / (int)sizeof(T);  // LDS elements one 1 KiB load fills
   uint32_t voff[I];
   int key[I];  // K-contiguous: first column of the chunk in the stage; MN: first row of the chunk
   const T* p;
@@ -226,9 +279,9 @@ struct Operand {
     for (int i = 0; i < I; ++i) {
       const int q = (wave * I + i) * 64 + lane;  // chunk index in the stage tile
       if constexpr (!MN) {
-        constexpr int CPR = C::BK / 8;
+        constexpr int CPR = C::CPR;
         const int r = q / CPR;
-        key[i] = ((q % CPR) ^ swz_xor<C::BK>(r)) << 3;
+        key[i] = ((q % CPR) ^ swz_xor<CPR>(r)) * C::EPC;
         voff[i] = (uint32_t)(r * ld + key[i]) * sizeof(T);
       } else {
         constexpr int CPR = ROWS / 8;
@@ -252,7 +305,7 @@ struct Operand {
           __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(p + (int64_t)r0 * ld), 0, nrec, kRsrcWord3);
 #pragma unroll
       for (int i = 0; i < I; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * 512, 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * kLoadElems, 16,
                                                  key[i] < lim ? voff[i] : kOobOffset, k0 * (int)sizeof(T), 0, 0);
     } else {
       // from the stage's first k-row to the matrix's last element
@@ -262,7 +315,7 @@ struct Operand {
           const_cast<T*>(p + (int64_t)k0 * ld + r0), 0, nrec, kRsrcWord3);
 #pragma unroll
       for (int i = 0; i < I; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * 512, 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, tile + (wave * I + i) * kLoadElems, 16,
                                                  key[i] < rows_valid ? voff[i] : kOobOffset, 0, 0, 0);
     }
 #endif
@@ -275,7 +328,7 @@ struct Operand {
       const int fr = lane & 31, fk = lane >> 5;
 #pragma unroll
       for (int t = 0; t < CNT; ++t)
-        out[t] = *reinterpret_cast<const u32x4*>(tile + swz<C::BK>(R + t * 32 + fr, ks * 2 + fk));
+        out[t] = *reinterpret_cast<const u32x4*>(tile + swz<C>(R + t * 32 + fr, ks * 2 + fk));
     } else {
 #if defined(__HIP_DEVICE_COMPILE__)
       typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -442,13 +495,7 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
     opa.template frag<C::TM>(la, ks, wm * C::WTM, lane, a);
     opb.template frag<C::TN>(la + C::BM * C::BK, ks, wn * C::WTN, lane, b);
   };
-  auto mma = [&](int buf, int first, int count) {
-#pragma unroll
-    for (int t = first; t < first + count; ++t) {
-      const int i = t / C::TN, j = t % C::TN;
-      acc[i][j] = mfma32<T>(fb[buf][j], fa[buf][i], acc[i][j]);
-    }
-  };
+  auto mma = [&](int buf, int first, int count) { mma_frags<T, C>(acc, fa[buf], fb[buf], first, count); };
   auto barrier = [&]() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -465,12 +512,13 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - C::NR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, C::MPF * C::TM * C::TN - C::NR, 0);
     }
   };
   constexpr int LB = (C::NKS - 1) & 1;  // register buffer of a stage's last sub-step
-  constexpr int Q = C::Q;               // MFMAs issued before the per-stage barrier
-  constexpr int R = C::TM * C::TN - Q;  // MFMAs after it
+  constexpr int Q = C::Q;               // fragment pairs issued before the per-stage barrier
+  constexpr int R = C::TM * C::TN - Q;  // fragment pairs after it
+  constexpr int RM = R * C::MPF;        // their MFMA instructions
 
   // prologue: every buffer gets a stage
 #pragma unroll
@@ -493,10 +541,10 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
     // after the barrier: the next stage's first operand reads, then its loads,
     // each slotted behind one of the R remaining MFMAs while they last
 #pragma unroll
-    for (int t = 0; t < C::NR + C::NI || t < R; ++t) {
+    for (int t = 0; t < C::NR + C::NI || t < RM; ++t) {
       if (t < C::NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);             // LDS read
       else if (t < C::NR + C::NI) __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
-      if (t < R) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                   // MFMA
+      if (t < RM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                  // MFMA
     }
   }
   inner((KT - 1) % C::STAGES);
@@ -524,7 +572,7 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 template <typename T, class C, class Epi>
 __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A, const T* __restrict__ B, Shape g,
                                                         Epi epi) {
-  static_assert(C::STAGES == 2 && C::BK == 64, "two stages of BK = 64");
+  static_assert(C::STAGES == 2 && C::CPR == 8, "two stages of 128-byte rows");
   constexpr int kStageBytes = C::STAGES * C::STAGE * (int)sizeof(T);
   constexpr int kEpiBytes = epilogue_lds_bytes<C, Epi>();
   constexpr int kLdsBytes = kStageBytes > kEpiBytes ? kStageBytes : kEpiBytes;
@@ -577,7 +625,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     for (int ks = 0; ks < C::NKS; ++ks)
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const int ch = ((2 * ks + fk) ^ sx0 ^ (4 * p)) << 3;
+        const int ch = ((2 * ks + fk) ^ sx0 ^ (4 * p)) * C::EPC;
         abase[ks][p] = (uint32_t)(((wm * C::WTM + fr) * C::BK + ch) * (int)sizeof(T));
         bbase[ks][p] = (uint32_t)(kBRegion + ((wn * C::WTN + fr) * C::BK + ch) * (int)sizeof(T));
         asm volatile("" : "+v"(abase[ks][p]));  // kept in registers, not recomputed per read
@@ -585,18 +633,20 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
       }
   }
   // DMA: lane offsets inside the panel (row r, chunk swizzled by r); the stage's
-  // first column goes in the scalar offset.
+  // first column goes in the scalar offset. A 1 KiB load fills kLoadElems
+  // elements of LDS.
   constexpr int IA = C::IA, IB = C::IB;
+  constexpr int kLoadElems = 1024 / (int)sizeof(T);
   uint32_t va[IA], vb[IB];
 #pragma unroll
   for (int i = 0; i < IA; ++i) {
     const int q = (wave * IA + i) * 64 + lane, r = q / 8;
-    va[i] = (uint32_t)(r * g.lda + (((q % 8) ^ swz_xor<C::BK>(r)) << 3)) * (uint32_t)sizeof(T);
+    va[i] = (uint32_t)(r * g.lda + ((q % 8) ^ swz_xor<8>(r)) * C::EPC) * (uint32_t)sizeof(T);
   }
 #pragma unroll
   for (int i = 0; i < IB; ++i) {
     const int q = (wave * IB + i) * 64 + lane, r = q / 8;
-    vb[i] = (uint32_t)(r * g.ldb + (((q % 8) ^ swz_xor<C::BK>(r)) << 3)) * (uint32_t)sizeof(T);
+    vb[i] = (uint32_t)(r * g.ldb + ((q % 8) ^ swz_xor<8>(r)) * C::EPC) * (uint32_t)sizeof(T);
   }
   const T* const pa = A + (int64_t)m0 * g.lda + kt0 * C::BK;
   const T* const pb = B + (int64_t)n0 * g.ldb + kt0 * C::BK;
@@ -618,12 +668,13 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pb), 0, live ? nrb : 0, kRsrcWord3);
 #pragma unroll
     for (int i = 0; i < IA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds + (st * kABytes) / (int)sizeof(T) + (wave * IA + i) * 512, 16,
-                                               va[i], k0b, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds + (st * kABytes) / (int)sizeof(T) + (wave * IA + i) * kLoadElems,
+                                               16, va[i], k0b, 0, 0);
 #pragma unroll
     for (int i = 0; i < IB; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, lds + (kBRegion + st * kBBytes) / (int)sizeof(T) + (wave * IB + i) * 512, 16, vb[i], k0b, 0, 0);
+          rb, lds + (kBRegion + st * kBBytes) / (int)sizeof(T) + (wave * IB + i) * kLoadElems, 16, vb[i], k0b, 0,
+          0);
 #endif
   };
 
@@ -642,13 +693,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
                                                (st * kBBytes + j * 32 * C::BK * (int)sizeof(T)));
     }
   };
-  auto mma = [&](int buf, int first, int count) {
-#pragma unroll
-    for (int t = first; t < first + count; ++t) {
-      const int i = t / C::TN, j = t % C::TN;
-      acc[i][j] = mfma32<T>(fb[buf][j], fa[buf][i], acc[i][j]);
-    }
-  };
+  auto mma = [&](int buf, int first, int count) { mma_frags<T, C>(acc, fa[buf], fb[buf], first, count); };
   auto barrier = [&]() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -662,14 +707,15 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     for (int ks = 0; ks < C::NKS - 1; ++ks) {
       frag(stage_c, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
       mma(ks & 1, 0, C::TM * C::TN);
-      __builtin_amdgcn_sched_group_barrier(0x008, kPre, 0);                 // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, C::NR, 0);                // LDS read
-      __builtin_amdgcn_sched_group_barrier(0x008, C::TM * C::TN - kPre, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x008, kPre, 0);                          // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, C::NR, 0);                         // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, C::MPF * C::TM * C::TN - kPre, 0);  // MFMA
     }
   };
   constexpr int LB = (C::NKS - 1) & 1;  // register buffer of a stage's last sub-step
-  constexpr int Q = C::Q;               // MFMAs issued before the per-stage barrier
+  constexpr int Q = C::Q;               // fragment pairs issued before the per-stage barrier
   constexpr int R = C::TM * C::TN - Q;
+  constexpr int RM = R * C::MPF;        // MFMA instructions after the barrier
   // stage kt in buffer CUR (stage kt+1 is landing in the other one)
   auto body = [&](auto cur_c, int kt) {
     using NX = std::integral_constant<int, decltype(cur_c)::value ^ 1>;
@@ -681,10 +727,10 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     issue(cur_c, kt + 2);
     mma(LB, Q, R);
 #pragma unroll
-    for (int t = 0; t < C::NR + C::NI || t < R; ++t) {
+    for (int t = 0; t < C::NR + C::NI || t < RM; ++t) {
       if (t < C::NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);             // LDS read
       else if (t < C::NR + C::NI) __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
-      if (t < R) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                   // MFMA
+      if (t < RM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                  // MFMA
     }
   };
 
@@ -714,9 +760,10 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
 // AMN / BMN: the operand is stored MN-contiguous (A[k][m], B[k][n]) instead of
 // K-contiguous (A[m][k], B[n][k]); lda / ldb are the leading dimensions of
 // whichever layout is used.
-template <typename T, class C = DefaultCfg, bool AMN = false, bool BMN = false, class Epi>
+template <typename T, class C = CfgFor<T>, bool AMN = false, bool BMN = false, class Epi>
 int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
            const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1) {
+  static_assert(sizeof(T) == 2 || (!AMN && !BMN), "fp32 operands must be K-contiguous");
   if (M == 0 || N == 0) return 0;
   if (K <= 0) {
     set_error("gemm: K (%d) must be positive", K);
@@ -752,7 +799,7 @@ int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb
   if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
   Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0, ksplit < 1 ? 1 : ksplit};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN) * g.ksplit;
-  if constexpr (!AMN && !BMN && C::STAGES == 2 && C::BK == 64) {
+  if constexpr (!AMN && !BMN && C::STAGES == 2 && C::CPR == 8) {
     if (K % C::BK == 0) {
       hipLaunchKernelGGL((gemm_kk_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);
       return check_launch("gemm_kk_kernel");

@@ -44,8 +44,8 @@ def fused_linear_cross_entropy_forward(hidden_states, weight, targets, ignore_in
     assert targets.dim() == 1 and targets.shape[0] == hidden_states.shape[0]
     if hidden_states.dtype != weight.dtype:
         raise TypeError(f"hidden_states ({hidden_states.dtype}) and weight ({weight.dtype}) dtypes differ")
-    if hidden_states.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"fused linear cross entropy runs on bf16/fp16 MFMA; got {hidden_states.dtype}")
+    if hidden_states.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"fused linear cross entropy takes fp32, bf16 or fp16; got {hidden_states.dtype}")
     dev = _lib.require_device(hidden_states, weight, targets, row_scale)
     hidden_states = hidden_states.contiguous()
     weight = weight.contiguous()

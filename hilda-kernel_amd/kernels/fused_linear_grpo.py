@@ -35,8 +35,8 @@ def fused_linear_grpo_forward(hidden, weight, completion_ids, advantages, old_lo
         f"expected hidden (B, L+1, H) and weight (V, H); got {tuple(hidden.shape)} and {tuple(weight.shape)}"
     if hidden.dtype != weight.dtype:
         raise TypeError(f"hidden ({hidden.dtype}) and weight ({weight.dtype}) dtypes differ")
-    if hidden.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"fused linear GRPO runs on bf16/fp16 MFMA; got {hidden.dtype}")
+    if hidden.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"fused linear GRPO takes fp32, bf16 or fp16; got {hidden.dtype}")
     if beta != 0.0 and ref_logp is None:
         raise ValueError("beta != 0 needs ref_logp")
     dev = _lib.require_device(hidden, weight, completion_ids, advantages, old_logp, ref_logp, completion_mask)

@@ -20,7 +20,7 @@ Differences from the reference, by design:
   * rows labelled ignore_index are compacted away on the device before the
     GEMMs, so they cost no FLOPs (the reference computes their logits);
   * the label count stays on the device (the reference reads it, :139);
-  * bf16/fp16 only: the contractions run on MFMA (fp32 raises TypeError).
+  * fp32, bf16 and fp16: the contractions run on fp32 or bf16/fp16 MFMA.
 """
 from __future__ import annotations
 
@@ -39,8 +39,8 @@ def fused_linear_jsd_forward(student_input, student_weight, teacher_input, teach
         f"expected student input (BT, H) and weight (V, H); got {tuple(si.shape)} and {tuple(sw.shape)}"
     assert ti.dim() == 2 and tw.dim() == 2 and ti.shape[1] == tw.shape[1] and ti.shape[0] == si.shape[0] \
         and tw.shape[0] == sw.shape[0], "expected teacher input (BT, Ht) and weight (V, Ht)"
-    if si.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"fused linear JSD runs on bf16/fp16 MFMA; got {si.dtype}")
+    if si.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"fused linear JSD takes fp32, bf16 or fp16; got {si.dtype}")
     if not (sw.dtype == ti.dtype == tw.dtype == si.dtype):
         raise TypeError("student and teacher inputs and weights must share one dtype")
     dev = _lib.require_device(si, sw, ti, tw, labels)

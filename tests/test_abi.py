@@ -83,8 +83,8 @@ def test_argument_validation_losses_without_gpu():
     _expect_einval(lib.hk_geglu_fwd(p, p, p, -1, 2, None), "element count")
     # FusedLinearCE: hidden [BT, H], weight [V, H]
     flce = [p, p, p, p, p, p, p, None]
-    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 0, 0, ws, 1 << 20, None),
-                   "bf16 and fp16")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 5, 0, ws, 1 << 20, None),
+                   "fp32, bf16 and fp16")
     _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 60, 128, -100, 1, 2, 0, ws, 1 << 20, None),
                    "multiples of 8")
     _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 5, 2, 0, ws, 1 << 20, None),
@@ -95,8 +95,8 @@ def test_argument_validation_losses_without_gpu():
                                                      1 << 20, None), "computed together")
     # FusedLinear-GRPO: hidden (B, L+1, H), weight [V, H]
     head = [p, p, p, p, p, p, p, p, p, p, p, p, 8, 1, p, None, 0, 0, None, 0, 0, None, 0, 0, 0, 2, 7]
-    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 0, 0, ws, 1 << 30, None),
-                   "bf16 and fp16")
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 3, 0, ws, 1 << 30, None),
+                   "fp32, bf16 and fp16")
     _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 100, 1.0, 0.0, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
                    "multiples of 8")
     _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.1, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
@@ -115,8 +115,11 @@ def test_argument_validation_losses_without_gpu():
 @needs_lib
 def test_fused_linear_workspace_queries():
     lib = _lib.load()
-    # bf16/fp16 only; a gradient call needs more (transposed operands, D^T) than a loss-only call
-    assert lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 0, 1) == 0
+    # fp32, bf16 and fp16 (fp32 operands take twice the bytes); an unknown dtype needs no workspace; a gradient
+    # call needs more (transposed operands, D^T) than a loss-only call
+    assert lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 5, 1) == 0
+    assert lib.hk_fused_linear_cross_entropy_workspace_size(256, 4096, 32000, 0, 0, 1) > \
+        lib.hk_fused_linear_cross_entropy_workspace_size(256, 4096, 32000, 0, 2, 1)
     fwd = lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 2, 0)
     bwd = lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 2, 1)
     assert 0 < fwd < bwd

@@ -41,7 +41,7 @@ def _oracle(h, w, t, reduction="mean", grads=None):
     return oracle.fwd_bwd(f, [h, w], grads, dtype=torch.float64)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("shape,chunk", [((96, 256, 1000), 4096), ((300, 128, 4096), 4096), ((200, 64, 520), 64),
                                          ((513, 256, 2048), 128), ((64, 4096, 32000), 4096)])
 @pytest.mark.parametrize("reduction", ["mean", "sum"])
@@ -61,7 +61,8 @@ def test_flce(dtype, shape, chunk, reduction):
         loss.backward()
     n_valid = int((t != -100).sum())
     s = n_valid if reduction == "mean" else 1
-    assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
+    lt = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
+    assert_close(loss, l_ref, name="loss", **lt)
     tt = tol(dtype)
     assert_close(hg.grad, dh_ref, name="dhidden", **tt)
     assert_close(wg.grad, dw_ref, name="dweight", **tt)
@@ -69,6 +70,27 @@ def test_flce(dtype, shape, chunk, reduction):
     assert_close(wg.grad.float() * s, dw_ref * s, name="dweight*n_valid", **tt)
     assert rel_fro(hg.grad, dh_ref) < 1e-2 and rel_fro(wg.grad, dw_ref) < 1e-2
     assert torch.count_nonzero(hg.grad[(t == -100).to(dev)]).item() == 0
+
+
+def test_flce_fp32_reference_check():
+    """benchmarks/bench_fused_linear_ce.py:45-49,71-90: the reference's fp32 checks at (256, 4096, 32000),
+    hidden ~ N(0,1), weight ~ N(0, 0.02), no ignored targets, mean; here against the fp64 oracle at the
+    north-star fp32 tolerance (rtol 1e-5, atol 1e-5), the gradients also multiplied back by n_valid."""
+    dtype = torch.float32
+    h, w, t = _case(256, 4096, 32000, dtype, 4096, ignore_frac=0.0)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, "mean")
+    dev = gpu()
+    hg = h.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    loss = hilda_fused_linear_cross_entropy(hg, wg, t.to(dev))
+    loss.backward()
+    tt = tol(dtype)
+    assert_close(loss, l_ref, name="loss", **tt)
+    assert_close(hg.grad, dh_ref, name="dhidden", **tt)
+    assert_close(wg.grad, dw_ref, name="dweight", **tt)
+    assert_close(hg.grad * 256, dh_ref * 256, name="dhidden*n_valid", **tt)
+    assert_close(wg.grad * 256, dw_ref * 256, name="dweight*n_valid", **tt)
+    assert rel_fro(hg.grad, dh_ref) < 1e-5 and rel_fro(wg.grad, dw_ref) < 1e-5
 
 
 def test_flce_reduction_none_and_upstream_grad():

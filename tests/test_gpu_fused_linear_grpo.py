@@ -67,7 +67,7 @@ CASES = [
 
 
 @pytest.mark.parametrize("case", CASES)
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fused_linear_grpo(case, dtype):
     B, L, H, V, mk, beta, with_old, T, el, eh, chunk = case
     h, w, ids, adv, old, ref, mask = _case(B, L, H, V, dtype, B * 100 + L + H, mk, beta, with_old)
@@ -83,7 +83,7 @@ def test_fused_linear_grpo(case, dtype):
     else:
         loss, kl, clip = hilda_fused_linear_grpo_loss(hg, wg, *args)
         loss.backward()
-    lt = dict(rtol=2e-3, atol=2e-3)
+    lt = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
     assert_close(loss, outs[0], name="loss", **lt)
     if beta != 0:
         assert_close(kl, outs[1], name="kl_mean", **lt)
@@ -162,7 +162,7 @@ def test_fused_linear_grpo_rejects():
     ids = torch.zeros(2, 4, dtype=torch.int64, device=dev)
     adv = torch.zeros(2, device=dev)
     with pytest.raises(TypeError):
-        hilda_fused_linear_grpo_loss(h.float(), w.float(), ids, adv)
+        hilda_fused_linear_grpo_loss(h.double(), w.double(), ids, adv)
     with pytest.raises(RuntimeError, match="multiples of 8"):
         hilda_fused_linear_grpo_loss(h, w[:99], ids, adv)
     with pytest.raises(ValueError):

@@ -172,7 +172,7 @@ def bench_c2_ops(c2, reps, flush):
     return out
 
 
-def bench_c1(K, dev, reps, flush):
+def bench_c1(K, dev, reps, flush, cpu=False):
     c = workloads.c1_rms_norm(device=dev)
     x = c["x"].requires_grad_(True)
     w = c["w"].requires_grad_(True)
@@ -182,8 +182,19 @@ def bench_c1(K, dev, reps, flush):
         y = K.hilda_rms_norm(x, w, c["eps"])
         return torch.autograd.grad([y], [x, w], [dy])
 
-    e = op_entry("C1", time_events(fn, reps, flush), bytes_rms_norm(*x.shape), "GB/s", HBM_PEAK_GBPS)
+    work = bytes_rms_norm(*x.shape)
+    e = op_entry("C1", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
     log(f"  rms_norm (C1 fp32): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    if cpu:
+        import oracle
+        xc, wc, dyc = (t.detach().cpu().requires_grad_(t is not dy) for t in (x, w, dy))
+
+        def step():
+            y = oracle.rms_norm_ref(xc, wc, c["eps"])
+            torch.autograd.grad([y], [xc, wc], [dyc])
+
+        e["cpu_baseline"] = cpu_entry(step, work, "GB/s", 1.0, "the full C1 input (x [4096,4096] fp32), the "
+                                      "PyTorch reference path fwd+bwd", False)
     return e
 
 
@@ -287,7 +298,7 @@ def bench_attn_res(K, dev, reps, flush, N=8, B=4, T=2048, D=4096):
     return e
 
 
-def bench_c3(K, dev, reps, flush):
+def bench_c3(K, dev, reps, flush, cpu=False):
     c = workloads.c3_cross_entropy(device=dev)
     logits = c["logits"].requires_grad_(True)
     t = c["targets"]
@@ -303,10 +314,22 @@ def bench_c3(K, dev, reps, flush):
     e = op_entry("C3", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
     e["n_valid"] = n_valid
     log(f"  cross_entropy (C3): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    if cpu:
+        import oracle
+        rows = 512
+        lc = logits[:rows].detach().cpu().requires_grad_(True)
+        tc = t[:rows].cpu()
+
+        def step():
+            loss = oracle.cross_entropy_ref(lc, tc)
+            torch.autograd.grad([loss], [lc])
+
+        e["cpu_baseline"] = cpu_entry(step, work, "GB/s", N / rows, f"the first {rows} of the 8192 C3 rows (bf16 "
+                                      "logits, F.cross_entropy fwd+bwd), time scaled by 8192/512", True)
     return e
 
 
-def bench_c4(K, dev, reps, flush):
+def bench_c4(K, dev, reps, flush, cpu=False):
     sls = K.fused_selective_log_softmax
     c = workloads.c4_grpo(lambda lg, ids: sls(lg, torch.cat([torch.zeros_like(ids[:, :1]), ids], 1)), device=dev)
     logits = c["logits"].requires_grad_(True)
@@ -323,10 +346,24 @@ def bench_c4(K, dev, reps, flush):
     e = op_entry("C4", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
     e["n_valid"] = n_valid
     log(f"  grpo_loss (C4): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
+    if cpu:
+        import oracle
+        lc = logits[:1].detach().cpu().requires_grad_(True)
+        ac = [a[:1].cpu() for a in args]
+
+        def step():
+            # benchmarks/bench_grpo.py:80,158: the reference path runs on logits.float()
+            loss, _, _ = oracle.grpo_loss_ref(lc.float(), *ac, c["temperature"], c["beta"], c["eps_low"],
+                                              c["eps_high"])
+            torch.autograd.grad([loss], [lc])
+
+        e["cpu_baseline"] = cpu_entry(step, work, "GB/s", B, f"sequence 0 of the 16 C4 sequences (logits "
+                                      f"[1,1024,151936] bf16, the reference path on logits.float()), time scaled "
+                                      f"by 16", True)
     return e
 
 
-def bench_c5(K, dev, reps, flush):
+def bench_c5(K, dev, reps, flush, cpu=False):
     c = workloads.c5_fused_linear_ce(device=dev)
     h = c["hidden"].requires_grad_(True)
     w = c["weight"].requires_grad_(True)
@@ -346,6 +383,20 @@ def bench_c5(K, dev, reps, flush):
     e["n_valid"] = n_valid
     log(f"  fused_linear_cross_entropy (C5): {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  ({e['frac']:.1%}); "
         f"dense-equivalent {e['dense_equivalent_tflops']} TFLOP/s")
+    if cpu:
+        import oracle
+        rows = 128
+        hc = h[:rows].detach().cpu().requires_grad_(True)
+        wc = w.detach().cpu().requires_grad_(True)
+        tc = t[:rows].cpu()
+
+        def step():
+            loss = oracle.linear_ce_ref(hc, wc, tc)
+            torch.autograd.grad([loss], [hc, wc])
+
+        e["cpu_baseline"] = cpu_entry(step, work, "TFLOP/s", BT / rows, f"the first {rows} of the 16384 C5 rows "
+                                      "(bf16 hidden @ weight.T [128256,4096], then F.cross_entropy, fwd+bwd), time "
+                                      "scaled by 16384/128", True, min_reps=1)
     return e
 
 
@@ -386,6 +437,37 @@ def bench_flgrpo(K, dev, reps, flush):
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (the reference's PyTorch path) on the host cores
 # ---------------------------------------------------------------------------
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_entry(step, work, unit, scale, sample, extrapolated, seconds=3.0, min_reps=2):
+    """A config's CPU baseline: `step` (the oracle, the reference's PyTorch path, on a slice of the config's own
+    inputs) on every host core, one warm-up, then repeated for `seconds` of CPU work (at least `min_reps`); the
+    median time times `scale` (the config over the slice) against the config's whole algorithmic work."""
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    step()
+    times = []
+    while len(times) < min_reps or sum(times) < seconds:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times) * scale
+    rate = work / t / (1e9 if unit == "GB/s" else 1e12)
+    log(f"    CPU: {rate:.3f} {unit} ({t:.3f} s for the config, {len(times)} reps)")
+    return {"value": round(rate, 4), "unit": unit, "cores": cores, "kind": "port", "sample": sample,
+            "extrapolated": extrapolated, "seconds_per_config": round(t, 4), "reps": len(times),
+            "cpu_model": cpu_model_name()}
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle (the reference's PyTorch path) on the full C2 step, fwd+bwd, on every host core: one warm-up
     step, then whole steps until `seconds` of CPU work (at least 3); throughput over all of them."""
@@ -418,15 +500,7 @@ def cpu_baseline(seconds=10.0):
         step()
         times.append(time.perf_counter() - t0)
     t = sum(times) / len(times)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cpu_model = cpu_model_name()
     return {"value": round(work / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"the full C2 step (FusedAddRMSNorm [8192,4096], RoPE q[4,2048,32,128] k[4,2048,8,128], "
                       f"SwiGLU [8192,14336]), bf16 PyTorch reference path fwd+bwd: {len(times)} steps in "
@@ -581,6 +655,19 @@ def reference_configs(dev, reps):
     print("\n".join(mm))
 
 
+C2_OPS = ("fused_add_rms_norm", "rope", "swiglu")
+
+
+def op_table():
+    """(name, (bench function, full reps)) of the per-op entries after the C2 ops; the large-vocabulary ops run
+    half the reps."""
+    return (("rms_norm", (bench_c1, True)), ("geglu", (bench_geglu, True)), ("attn_res", (bench_attn_res, True)),
+            ("cross_entropy", (bench_c3, False)), ("grpo_loss", (bench_c4, False)),
+            ("fused_linear_cross_entropy", (bench_c5, False)), ("kl_div", (bench_kl_div, False)),
+            ("jsd", (bench_jsd, False)), ("fused_linear_jsd", (bench_fljsd, False)),
+            ("fused_linear_grpo", (bench_flgrpo, False)))
+
+
 def load_traffic(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -607,6 +694,11 @@ def main(argv=None):
                          "traffic for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     ap.add_argument("--reference-configs", action="store_true",
                     help="instead of the step: every op on the reference benchmarks' own shapes, as a markdown table")
+    ap.add_argument("--only", default=None,
+                    help="comma list of op names: time only these (op-reps each, cache flushed between reps), with "
+                         "no C2 headline step, copy ceilings or CPU baseline, and print their entries as JSON; "
+                         "the command the per-config rocprofv3 summaries in profiles/ are taken from. copy_1g alone: "
+                         "three 1 GiB device copies (the counter calibration)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -624,6 +716,33 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.reference_configs:
         reference_configs(dev, max(3, args.op_reps // 2))
+        return 0
+    if args.only:
+        table = dict(op_table())
+        names = args.only.split(",")
+        if names == ["copy_1g"]:
+            # the counter calibration alone: three plain 1 GiB device-to-device copies
+            src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            return 0
+        unknown = set(names) - set(table) - set(C2_OPS)
+        if unknown:
+            raise SystemExit(f"unknown op(s) {sorted(unknown)}; known: {sorted(table)}")
+        flush = Flusher(dev)
+        c2 = C2Step(K, dev) if any(n in C2_OPS for n in names) else None
+        out = {}
+        for name in names:
+            if name in C2_OPS:
+                fn = {"fused_add_rms_norm": c2.fused_add, "rope": c2.rope, "swiglu": c2.swiglu}[name]
+                out[name] = op_entry("C2", time_events(fn, args.op_reps, flush), c2.bytes[name], "GB/s",
+                                     HBM_PEAK_GBPS)
+            else:
+                out[name] = table[name][0](K, dev, args.op_reps, flush)
+            torch.cuda.empty_cache()
+        print(json.dumps(out), flush=True)
         return 0
     log(f"device: {torch.cuda.get_device_name(dev)}")
     c2 = C2Step(K, dev)
@@ -705,23 +824,23 @@ def main(argv=None):
         flush = Flusher(dev)
         log("per-op fwd+bwd (median, cache flushed between reps):")
         ops.update(bench_c2_ops(c2, args.op_reps, flush))
-        # (name, bench, full reps): the large-vocabulary ops run half the reps
-        table = (("rms_norm", bench_c1, True), ("geglu", bench_geglu, True), ("attn_res", bench_attn_res, True),
-                 ("cross_entropy", bench_c3, False), ("grpo_loss", bench_c4, False),
-                 ("fused_linear_cross_entropy", bench_c5, False), ("kl_div", bench_kl_div, False),
-                 ("jsd", bench_jsd, False), ("fused_linear_jsd", bench_fljsd, False),
-                 ("fused_linear_grpo", bench_flgrpo, False))
-        wanted = [n for n, _, _ in table] if args.ops == "all" else \
+        table = op_table()
+        wanted = [n for n, _ in table] if args.ops == "all" else \
             [] if args.ops == "c2" else args.ops.split(",")
-        unknown = set(wanted) - {n for n, _, _ in table}
+        unknown = set(wanted) - {n for n, _ in table}
         if unknown:
-            raise SystemExit(f"unknown op(s) {sorted(unknown)}; known: {[n for n, _, _ in table]}")
+            raise SystemExit(f"unknown op(s) {sorted(unknown)}; known: {[n for n, _ in table]}")
         del c2
         torch.cuda.empty_cache()
         c2 = None
-        for name, fn, full in table:
+        for name, (fn, full) in table:
             if name in wanted:
-                ops[name] = fn(K, dev, args.op_reps if full else max(3, args.op_reps // 2), flush)
+                reps = args.op_reps if full else max(3, args.op_reps // 2)
+                if fn in (bench_c1, bench_c3, bench_c4, bench_c5):
+                    # the config's own CPU baseline (a slice of the same inputs, scaled) unless --no-cpu
+                    ops[name] = fn(K, dev, reps, flush, cpu=not args.no_cpu)
+                else:
+                    ops[name] = fn(K, dev, reps, flush)
                 torch.cuda.empty_cache()
         log("device copy of the same bytes (practical HBM ceiling per op):")
         for name, e in ops.items():

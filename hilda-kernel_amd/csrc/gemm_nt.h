@@ -230,8 +230,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// word 3 of a raw buffer descriptor on gfx9-family parts (32-bit data format, no swizzle)
-constexpr int kRsrcWord3 = 0x00020000;
 // A buffer offset past the end of any buffer this kernel builds (the launcher
 // keeps them below it) that cannot wrap when the scalar offset is added.
 constexpr uint32_t kOobOffset = 0x7ff00000u;

@@ -181,6 +181,18 @@ __device__ __forceinline__ Pack<T, VEC> splat_pack(float value) {
   return pack<T, VEC>(x);
 }
 
+// A uniform load issued on the scalar unit (s_load, counted by lgkmcnt): the
+// pointer is read as constant memory, so use it only on data that the kernel
+// never writes. A vector load of the same value would be counted by vmcnt,
+// and waiting for it would also wait for every older vector load or store.
+template <typename T>
+__device__ __forceinline__ T scalar_load(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
+// word 3 of a raw buffer descriptor on gfx9-family parts (32-bit data format, no swizzle)
+constexpr int kRsrcWord3 = 0x00020000;
+
 // Keep the optimiser from reusing values derived from the pack across this
 // point (it re-derives them from the raw words instead of keeping copies live).
 template <typename T, int VEC>

@@ -15,10 +15,19 @@ int count_valid_launch(int* n_valid, const int64_t* targets, int64_t rows, int64
 // when scale_by_n_valid, else 1; ignored rows give 0 and a zero row. dlogits may alias logits.
 // Without dlogits: loss_rows = lse - x_t (0 if ignored), no scaling.
 // rows_lim (nullable): a device-side bound, only rows < *rows_lim - rows_off are processed.
+// rowmap/n_live (nullable, with dlogits only; not with rows_lim): the plan of
+// ce_plan_launch, whose live rows the grid deals out evenly.
 int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const int64_t* targets, int64_t rows,
                    int64_t V, int64_t ld_in, int64_t ld_out, int64_t ignore_index, int has_ignore, const int* n_valid,
                    int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st,
-                   const int* rows_lim = nullptr, int64_t rows_off = 0);
+                   const int* rows_lim = nullptr, int64_t rows_off = 0, const int* rowmap = nullptr,
+                   const int* n_live = nullptr);
+
+// The CrossEntropy plan (one block): *n_valid = rows whose target is not
+// ignored; rowmap[0 .. *n_live) = rows with a gradient (target not ignored and
+// in [0, V)), in order. rows < 2^31.
+int ce_plan_launch(int* n_valid, int* rowmap, int* n_live, const int64_t* targets, int64_t rows, int64_t V,
+                   int64_t ignore_index, int has_ignore, hipStream_t st);
 
 // Stable compaction of the rows whose target is not ignore_index: rowmap[0 .. n)
 // the live rows in order, inv[r] their place (-1 for ignored rows), *n_live = n.

@@ -34,6 +34,10 @@ namespace {
 // ---------------------------------------------------------------------------
 // register-resident row helpers
 // ---------------------------------------------------------------------------
+// s_waitcnt immediate for lgkmcnt(0) alone on gfx9-family parts (vmcnt 63 and
+// expcnt 7 leave those counters unwaited)
+constexpr int kWaitLgkm0 = 0xC07F;
+
 // max(a, b, c) in one instruction (fmaxf would add a canonicalising max per operand)
 __device__ __forceinline__ float max3(float a, float b, float c) {
   float r;
@@ -41,8 +45,9 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   return r;
 }
 
-template <typename T, int VEC, int NCH, int BLOCK>
+template <typename T, int VEC, int NCH, int BLOCK, int NFULL = 0>
 struct RowRegs {
+  static_assert(NFULL <= NCH, "full vectors");
   Pack<T, VEC> v[NCH];
 
   // Addressing: vector j of lane t covers columns [j*BLOCK*VEC + t*VEC, +VEC).
@@ -51,6 +56,11 @@ struct RowRegs {
   // only on the uniform remainder n - j*BLOCK*VEC, so those cases are scalar
   // branches; only a partial vector needs a per-lane test. Column indices are
   // 32-bit: the host rejects rows of 2^31 or more elements.
+  // Vectors j < NFULL are full in every row that the caller hands over (it
+  // guarantees n >= NFULL * kSpan); only the LDS stage relies on it. The
+  // other tests stay scalar branches even where they always pass: each
+  // vector's work then stays a block of its own, which keeps the compiler
+  // from overlapping the vectors' temporaries (and spilling).
   static constexpr int kSpan = BLOCK * VEC;
   __device__ __forceinline__ static int lane_col() { return (int)threadIdx.x * VEC; }
   // element offset of vector j for a lane at column tc, as an unsigned 32-bit
@@ -58,22 +68,59 @@ struct RowRegs {
   // (the global_load saddr form) rather than one 64-bit base per vector.
   __device__ __forceinline__ static uint32_t off(int j, int tc) { return (uint32_t)(j * kSpan) + (uint32_t)tc; }
 
-  // Elements past the row end hold -inf: they add nothing to the max or the
-  // sum, so the max/sum phases run without lane masks.
+  // The lanes of a partial vector past the row end load the row's first
+  // elements (an in-bounds address) and keep them: the reduction reads them as
+  // -inf (mask_tail) and the stores skip them. Masking at load time instead
+  // would make the wave wait for that load, and so for every store and load
+  // issued before it, at the end of each refill.
   __device__ __forceinline__ void load(const T* __restrict__ row, int n) {
     const int tc = lane_col();
     const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int lim = n - j * kSpan;  // uniform
-      if (lim >= kSpan) {
+      if (j < NFULL || lim >= kSpan) {
         v[j] = load_pack<T, VEC>(row + off(j, tc));
       } else if (lim > 0) {
-        const Pack<T, VEC> x = load_pack<T, VEC>(row + off(j, tc < lim ? tc : 0));  // in-bounds address
-        v[j] = tc < lim ? x : ninf;
+        v[j] = load_pack<T, VEC>(row + off(j, tc < lim ? tc : 0));  // in-bounds address
       } else {
         v[j] = ninf;  // defined on every path, so no value flows in from the previous row
       }
+    }
+  }
+
+  // load() for a pipeline that refills vectors 0..NPF-1 from the LDS stage:
+  // the first row takes the same path (stage, the other vectors from global,
+  // then the staged ones from LDS), so at every use those registers come from
+  // an LDS read and the waits for the global loads can count down vector by
+  // vector instead of waiting for all of them at the first vector.
+  template <int NPF>
+  __device__ __forceinline__ void load_staged(const T* __restrict__ row, int n, T* lds) {
+    stage<NPF>(lds, row, n);
+    const int tc = lane_col();
+    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
+#pragma unroll
+    for (int j = NPF; j < NCH; ++j) {
+      const int lim = n - j * kSpan;  // uniform
+      if (j < NFULL || lim >= kSpan) {
+        v[j] = load_pack<T, VEC>(row + off(j, tc));
+      } else if (lim > 0) {
+        v[j] = load_pack<T, VEC>(row + off(j, tc < lim ? tc : 0));  // in-bounds address
+      } else {
+        v[j] = ninf;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NPF; ++j) v[j] = load_pack<T, VEC>(lds + (j * BLOCK + (int)threadIdx.x) * VEC);
+  }
+
+  // The unpacked floats of vector j with the lanes past the row end at -inf.
+  __device__ __forceinline__ static void mask_tail(int j, int n, float (&x)[VEC]) {
+    const int lim = n - j * kSpan;  // uniform
+    if (lim < kSpan) {
+      const bool in_row = lane_col() < lim;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = in_row ? x[e] : -INFINITY;
     }
   }
 
@@ -90,23 +137,31 @@ struct RowRegs {
   // when p_t is close to 1. The target's vector is a uniform test, and only
   // that vector's unpacked floats are masked (rewriting the registers would
   // make the compiler carry every vector through phi copies).
-  __device__ __forceinline__ void reduce_lane(int n, float c, int target, float* m_out, float* s_out) {
+  // *xt_out (when given) receives the target's own x in the lane that holds
+  // it, the one lane of the block for which owns_target() is true.
+  __device__ __forceinline__ void reduce_lane(int n, float c, int target, float* m_out, float* s_out,
+                                              float* xt_out = nullptr) {
     const int jt = target >= 0 ? target / kSpan : -1;  // uniform
     const int rel = target - jt * kSpan - lane_col();  // in [0, VEC) in the owning lane only
-    float m = -INFINITY;
+    float m = -INFINITY, xt = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       if (j * kSpan < n) {
         float x[VEC];
         unpack(v[j], x);
+        mask_tail(j, n, x);
         if (j == jt) {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) x[e] = e == rel ? -INFINITY : x[e];
+          for (int e = 0; e < VEC; ++e) {
+            xt = e == rel ? x[e] : xt;
+            x[e] = e == rel ? -INFINITY : x[e];
+          }
         }
 #pragma unroll
         for (int e = 0; e + 1 < VEC; e += 2) m = max3(m, x[e], x[e + 1]);
         if constexpr (VEC & 1) m = fmaxf(m, x[VEC - 1]);
       }
+      __builtin_amdgcn_sched_barrier(0);  // one vector's floats live at a time
     }
     m *= c;
     opaque();  // unpack again below rather than keep all the floats of the max pass live
@@ -117,6 +172,7 @@ struct RowRegs {
       if (j * kSpan < n) {
         float x[VEC];
         unpack(v[j], x);
+        mask_tail(j, n, x);
         if (j == jt) {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) x[e] = e == rel ? -INFINITY : x[e];
@@ -128,6 +184,12 @@ struct RowRegs {
     }
     *m_out = m;
     *s_out = s;
+    if (xt_out) *xt_out = xt;
+  }
+
+  // Whether this lane holds column `target` (of a row of n > target columns).
+  __device__ __forceinline__ static bool owns_target(int target) {
+    return target >= 0 && (target % kSpan) / VEC == (int)threadIdx.x;
   }
 
   // Gradient of the row, p_j * g = 2^(x_j*c - lse2) * g computed in fp32 and
@@ -137,28 +199,52 @@ struct RowRegs {
   // stores and the next row's loads are in flight together. Recomputing the
   // exponential here instead of keeping 2^(x*c - m) from the sum pass measured
   // as fast (the sum pass, which runs while HBM idles, writes no registers).
+  // With NPF > 0, vectors 0..NPF-1 of `next` come from the LDS stage that
+  // stage<NPF>() filled (the caller issued it for the same row).
+  template <int NPF = 0>
   __device__ __forceinline__ void store_prob_grad_then_load(T* out, int n, float c, float lse2, float g,
-                                                            const T* next) {
+                                                            const T* next, const T* lds = nullptr) {
     const int tc = lane_col();
-    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int lim = n - j * kSpan;  // uniform
-      if (lim > 0) {
+      if (j < NFULL || lim > 0) {
         float x[VEC];
         unpack(v[j], x);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) x[e] = exp2_fast(fmaf(x[e], c, -lse2)) * g;
-        if (lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
-        if (lim >= kSpan) {
-          v[j] = load_pack<T, VEC>(next + off(j, tc));
+        if (j < NFULL || lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
+        if (j < NPF) {
+          v[j] = load_pack<T, VEC>(lds + (j * BLOCK + (int)threadIdx.x) * VEC);
         } else {
-          const Pack<T, VEC> y = load_pack<T, VEC>(next + off(j, tc < lim ? tc : 0));
-          v[j] = tc < lim ? y : ninf;
+          v[j] = load_pack<T, VEC>(next + off(j, lim >= kSpan || tc < lim ? tc : 0));  // see load()
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
+
+  // LDS stage of a row's leading vectors: each full vector j < NPF of `row`
+  // copied into `lds` by LDS DMA (buffer_load_dwordx4 ... lds), which moves
+  // the data without holding VGPRs, so the copy can be in flight while the
+  // registers still hold (and reduce) the current row. Wave w's 64 lanes land
+  // in lane order in the 1 KiB at lds + (j*BLOCK + 64w)*VEC, so each lane
+  // reads back exactly the 16 bytes it would have loaded. The caller makes
+  // sure no earlier LDS read of the stage is still pending.
+  template <int NPF>
+  __device__ __forceinline__ static void stage(T* lds, const T* row, int n) {
+    static_assert(sizeof(T) * VEC == 16, "the stage moves 16 bytes a lane");
+    static_assert(NPF <= NFULL, "only vectors that are full in every row are staged");
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), 0, n * (int)sizeof(T), kRsrcWord3);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);  // the LDS base goes in M0
+    const uint32_t lane_off = (uint32_t)threadIdx.x * 16u;
+#pragma unroll
+    for (int j = 0; j < NPF; ++j)  // full vectors: every lane in bounds
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds + (j * BLOCK + wave * kWave) * VEC, 16, lane_off,
+                                               j * kSpan * (int)sizeof(T), 0, 0);
+#endif
   }
 };
 
@@ -189,28 +275,42 @@ __device__ __forceinline__ void lse2_merge(float& m, float& s, float m2, float s
 }
 
 // Block-wide (max, sum) of per-lane (m, s) pairs, one LDS exchange: *M the
-// block max, *S the sum scaled to it. `red` holds 2*NW floats per parity;
-// alternating `parity` between consecutive calls lets the exchange go without
-// a trailing barrier.
+// block max, *S the sum scaled to it. `red` holds kRedStride floats per
+// parity; alternating `parity` between consecutive calls lets the exchange go
+// without a trailing barrier. With X, the same exchange also broadcasts one
+// lane's value: the lane with `own` set (exactly one in the block) passes x
+// and every lane receives it in *X, as a uniform (scalar) value.
 template <int NW>
-__device__ __forceinline__ void block_lse2_ms(float m, float s, float* red, int parity, float* M, float* S) {
+struct BlockRed {
+  static constexpr int kStride = 2 * NW + 4;  // m[NW], s[NW], x, padding to 16 bytes
+  static constexpr int kFloats = 2 * kStride;
+};
+
+template <int NW>
+__device__ __forceinline__ void block_lse2_ms(float m, float s, float* red, int parity, float* M, float* S,
+                                              float x = 0.f, bool own = false, float* X = nullptr) {
+  static_assert(NW > 1, "the exchange goes through LDS");
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) lse2_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
-  if constexpr (NW > 1) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    float* r = red + parity * 2 * NW;
-    if (lane == 0) {
-      r[wave] = m;
-      r[NW + wave] = s;
-    }
-    __syncthreads();
-    m = r[0];
-    s = r[NW];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) lse2_merge(m, s, r[i], r[NW + i]);
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  float* r = red + parity * BlockRed<NW>::kStride;
+  if (lane == 0) {
+    r[wave] = m;
+    r[NW + wave] = s;
   }
+  if (X && own) r[2 * NW] = x;
+  // A barrier for LDS traffic only: each wave's LDS writes have completed
+  // before it arrives. __syncthreads() would also wait for every global load
+  // the wave has in flight, including an LDS stage of the next row. (One asm
+  // statement, so the compiler moves no memory access across the barrier.)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  m = r[0];
+  s = r[NW];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) lse2_merge(m, s, r[i], r[NW + i]);
   *M = m;
   *S = s;
+  if (X) *X = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, r[2 * NW])));
 }
 
 // The row's log2-sum-exp from the (max, sum) of every column but the target,
@@ -332,6 +432,32 @@ __device__ __forceinline__ void lse_rows_resident(int n, float c, int64_t rows, 
   }
 }
 
+// The register-resident forms (block, vectors per lane), smallest first; a row
+// of nv vectors takes the first form with block * nch >= nv (choose_row_cfg).
+struct RowForm {
+  int block, nch;
+};
+constexpr RowForm kRowForms[] = {{256, 1},   {256, 2},   {256, 4},    {256, 8},    {256, 12},   {256, 16},
+                                 {512, 12},  {512, 16},  {1024, 12},  {1024, 16},  {1024, 20},  {1024, 24}};
+
+// Vectors per lane that are full in every row a form serves: such a row is
+// longer than the previous form's capacity.
+constexpr int full_vectors(int nch, int block) {
+  int prev = 0;
+  for (const RowForm& f : kRowForms) {
+    if (f.block == block && f.nch == nch) return prev / block;
+    prev = f.block * f.nch;
+  }
+  return 0;
+}
+
+// LDS stage depth of a register-resident gradient form (RowRegs::stage): the
+// 1024-lane forms, one block a CU whose waves all reduce at once, stage up to
+// 9 of their full 16-byte vectors (144 KiB of the CU's 160 KiB of LDS).
+constexpr int stage_depth(int nch, int block) {
+  return block == 1024 ? (full_vectors(nch, block) < 9 ? full_vectors(nch, block) : 9) : 0;
+}
+
 // ---------------------------------------------------------------------------
 // CrossEntropy
 // ---------------------------------------------------------------------------
@@ -346,6 +472,10 @@ struct CeArgs {
   int scale_by_n_valid;
   const int* rows_lim;  // optional device-side bound: rows cut to *rows_lim - rows_off
   int64_t rows_off;
+  // optional plan (ce_plan_kernel): the rows that get a gradient are
+  // rowmap[0 .. *n_live), dealt out to the blocks in turn
+  const int* rowmap;
+  const int* n_live;
 };
 
 // Applies CeArgs::rows_lim (a uniform scalar load) to the kernel's copy of the arguments.
@@ -362,15 +492,18 @@ __device__ __forceinline__ float ce_scale(const CeArgs& a) {
 // never read.
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T* logits, CeArgs a) {
+  constexpr int NPF = RESIDENT ? stage_depth(NCH, BLOCK) : 0;
   // dlogits may alias logits (in-place use): every element is read before the
   // same thread overwrites it, and a row's stores are issued before the next
   // row's loads of the same vector, so the pointers are not declared __restrict__.
-  __shared__ float red[4 * (BLOCK / kWave)];
+  __shared__ float red[BlockRed<BLOCK / kWave>::kFloats];
+  __shared__ __attribute__((aligned(1024))) T pf[NPF > 0 ? NPF * BLOCK * VEC : 1];
   ce_bound(a);
   const float scale = ce_scale(a);
   const int64_t G = gridDim.x;
   auto is_live = [&](int64_t t) { return !(a.has_ignore && t == a.ignore_index) && t >= 0 && t < a.V; };
   if constexpr (RESIDENT) {
+    using Regs = RowRegs<T, VEC, NCH, BLOCK, full_vectors(NCH, BLOCK)>;
     const int n = row_len(a.V);
     // dead rows (ignored or out of range) first: a zero (NaN) row, never read
     for (int64_t row = blockIdx.x; row < a.rows; row += G) {
@@ -381,41 +514,67 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
         if (threadIdx.x == 0) a.loss_rows[row] = ignored ? 0.f : NAN;
       }
     }
-    // then the live rows, each one's gradient stores overlapped with the next one's loads
-    auto next_live = [&](int64_t from) {
-      int64_t q = from;
-      while (q < a.rows && !is_live(a.targets[q])) q += G;
-      return q;
+    // Then the live rows. Row r's gradient stores go out with the loads of the
+    // next live row r' (register refill), and while r is reduced the leading
+    // NPF vectors of r' are already on their way into LDS, so HBM has work
+    // during the reduction and the block exchange too. The per-row scalars
+    // (targets, row scale) are scalar loads, so waiting for them never waits
+    // for the staged copy; the search for the row after r' runs at the end of
+    // the iteration, while r's stores and r''s loads are in flight. The target
+    // logit comes out of the registers, broadcast by the block exchange.
+    // The block's live rows: with a plan, rowmap[q] for q = blockIdx.x,
+    // + G, ... (every such row is live, and the blocks' counts differ by one
+    // at most); without one, rows q = blockIdx.x, + G, ... that are live.
+    struct LiveRow {
+      int64_t q, row, t;  // q >= nq: none
     };
-    int64_t row = next_live(blockIdx.x);
-    if (row >= a.rows) return;
-    RowRegs<T, VEC, NCH, BLOCK> r;
-    r.load(logits + row * a.ld_in, n);
+    const int64_t nq = a.rowmap ? (int64_t)scalar_load(a.n_live) : a.rows;
+    auto next_live = [&](int64_t from) {
+      LiveRow x{from, 0, 0};
+      for (; x.q < nq; x.q += G) {
+        x.row = a.rowmap ? (int64_t)scalar_load(a.rowmap + x.q) : x.q;
+        x.t = scalar_load(a.targets + x.row);
+        if (is_live(x.t)) break;
+      }
+      return x;
+    };
+    LiveRow cur = next_live(blockIdx.x);
+    if (cur.q >= nq) return;
+    Regs r;
+    r.template load_staged<NPF>(logits + cur.row * a.ld_in, n, pf);
+    LiveRow next = next_live(cur.q + G);
     int parity = 0;
     for (;;) {
-      const int64_t t = a.targets[row];
+      const int n = row_len(a.V);  // per iteration (see row_len)
+      const int64_t row = cur.row;
+      const int t = (int)cur.t;
       const T* in = logits + row * a.ld_in;
-      const int64_t next = next_live(row + G);
-      const float xt = to_f32<T>(in[t]);
-      const float gscale = a.row_scale ? scale * a.row_scale[row] : scale;
-      float m, s, M, R, rest;
-      r.reduce_lane(n, kLog2e, (int)t, &m, &s);
-      block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R);
-      const float lse2 = target_merge(M, R, xt * kLog2e, true, &rest);
+      // The refill and the stage are unconditional (the last row re-reads
+      // itself, from L2, and the data is not used), so the registers carry one
+      // definition around the loop and every path has the same loads in flight.
+      const T* src = next.q < nq ? logits + next.row * a.ld_in : in;
+      if constexpr (NPF > 0) {
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the previous row's reads of the stage have completed
+        Regs::template stage<NPF>(pf, src, n);
+      }
+      const float gscale = a.row_scale ? scale * scalar_load(a.row_scale + row) : scale;
+      float m, s, xt, M, R, X, rest;
+      r.reduce_lane(n, kLog2e, t, &m, &s, &xt);
+      block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R, xt, Regs::owns_target(t), &X);
+      const float lse2 = target_merge(M, R, X * kLog2e, true, &rest);
       parity ^= 1;
       r.opaque();
-      if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - xt) * scale;
-      // the refill is unconditional (the last row re-reads itself, from L2) so the
-      // registers carry one definition around the loop
-      const T* src = next < a.rows ? logits + next * a.ld_in : in;
       T* out = dlogits + row * a.ld_out;
-      r.store_prob_grad_then_load(out, n, kLog2e, lse2, gscale, src);
+      r.template store_prob_grad_then_load<NPF>(out, n, kLog2e, lse2, gscale, src, pf);
       // the target element: (p_t - 1) * g = -(1 - p_t) * g, stored after (and
       // over) the vector store of the same thread
-      if ((int)threadIdx.x == (int)(t % RowRegs<T, VEC, NCH, BLOCK>::kSpan) / VEC)
-        out[t] = from_f32<T>(-rest * gscale);
-      if (next >= a.rows) break;
-      row = next;
+      if (Regs::owns_target(t)) out[t] = from_f32<T>(-rest * gscale);
+      // (after the row's stores: a store ahead of them would hold up the
+      // first LDS refill, which waits for the stage's loads in issue order)
+      if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - X) * scale;
+      if (next.q >= nq) break;
+      cur = next;
+      next = next_live(cur.q + G);
     }
   } else {
     __shared__ float red1[BLOCK / kWave];
@@ -449,7 +608,7 @@ struct TargetLogit {
 
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void ce_fwd_kernel(const T* __restrict__ logits, CeArgs a) {
-  __shared__ float red[4 * (BLOCK / kWave)];
+  __shared__ float red[BlockRed<BLOCK / kWave>::kFloats];
   ce_bound(a);
   auto target = [&](int64_t row) {
     const int64_t t = a.targets[row];
@@ -497,6 +656,47 @@ __global__ __launch_bounds__(1024) void count_valid_kernel(int* __restrict__ n_v
       for (int64_t i = 0; i < rows; ++i) n += (!has_ignore || t[i] != ignore_index);
       *n_valid = (int)(n > 0x7fffffff ? 0x7fffffff : n);
     }
+  }
+}
+
+// The CrossEntropy launch plan, one block: *n_valid = the rows whose target is
+// not the ignore index (the divisor of 'mean') and rowmap[0 .. *n_live) the rows
+// that get a gradient (target not ignored and inside [0, V)), in order, so the
+// persistent grid can deal them out evenly. Per 1024 rows, a wave ballot and an
+// exclusive scan of the 16 wave counts; rows < 2^31 (the launcher checks).
+__global__ __launch_bounds__(1024) void ce_plan_kernel(int* __restrict__ n_valid, int* __restrict__ rowmap,
+                                                       int* __restrict__ n_live, const int64_t* __restrict__ t,
+                                                       int64_t rows, int64_t V, int64_t ignore_index,
+                                                       int has_ignore) {
+  __shared__ int wcount[2][16];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  int live_base = 0, valid_base = 0;  // counts before this 1024-row step (the same in every lane)
+  for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
+    const int64_t r = r0 + threadIdx.x;
+    const int64_t tr = r < rows ? t[r] : ignore_index;
+    const bool valid = r < rows && (!has_ignore || tr != ignore_index);
+    const bool live = valid && tr >= 0 && tr < V;
+    const uint64_t bal = __ballot(live);
+    const uint64_t bv = __ballot(valid);
+    if (lane == 0) {
+      wcount[0][wave] = __popcll(bal);
+      wcount[1][wave] = __popcll(bv);
+    }
+    __syncthreads();
+    int before = live_base, total = live_base, vtotal = valid_base;
+    for (int w = 0; w < 16; ++w) {
+      before += w < wave ? wcount[0][w] : 0;
+      total += wcount[0][w];
+      vtotal += wcount[1][w];
+    }
+    if (live) rowmap[before + __popcll(bal & ((1ull << lane) - 1ull))] = (int)r;
+    live_base = total;
+    valid_base = vtotal;
+    __syncthreads();  // wcount is rewritten by the next step
+  }
+  if (threadIdx.x == 0) {
+    *n_valid = valid_base;
+    *n_live = live_base;
   }
 }
 
@@ -582,7 +782,7 @@ struct GrpoArgs {
 // tokens get 0 and their rows are not read.
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void selective_log_softmax_kernel(const T* __restrict__ logits, GrpoArgs a) {
-  __shared__ float red[4 * (BLOCK / kWave)];
+  __shared__ float red[BlockRed<BLOCK / kWave>::kFloats];
   const int64_t rows = a.B * a.L;
   const float c = kLog2e * a.inv_T;
   auto row_ptr = [&](int64_t r) {
@@ -634,6 +834,14 @@ struct alignas(16) GrpoTok {
   float gs;     // m / (max(len_b, 1) * B) / T: dloss / T at unit upstream gradient
   float pad0, pad1;
 };
+// A token record as one scalar load (s_load_dwordx8): a field-by-field copy
+// may be split into loads that the scalar unit has no form for, and those go
+// to the vector unit.
+__device__ __forceinline__ GrpoTok load_tok(const GrpoTok* p) {
+  typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+  static_assert(sizeof(GrpoTok) == sizeof(u32x8), "one 32-byte record");
+  return __builtin_bit_cast(GrpoTok, scalar_load(reinterpret_cast<const u32x8*>(p)));
+}
 struct alignas(16) GrpoOut {
   float lse, loss, kl, clip;
 };
@@ -682,11 +890,13 @@ __device__ __forceinline__ GrpoOut grpo_terms(const GrpoHot& a, const GrpoTok& t
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT, bool GRAD>
 __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits, GrpoHot a) {
   // dlogits may alias logits (FusedLinear-GRPO writes the gradient over the
-  // chunk's logits): the id logit is read before the row's reduction barriers,
-  // every other element is read by the thread that later overwrites it, and a
-  // row's stores are issued before the next row's loads of the same vector, so
-  // the pointers are not declared __restrict__.
-  __shared__ float red[4 * (BLOCK / kWave)];
+  // chunk's logits): every element is read by the thread that later
+  // overwrites it (the gradient path takes the id logit from the registers,
+  // the forward-only paths read it before the row's reduction barriers), a
+  // row's stores are issued before the next row's loads of the same vector,
+  // and a row is staged into LDS only before any of its stores, so the
+  // pointers are not declared __restrict__.
+  __shared__ float red[BlockRed<BLOCK / kWave>::kFloats];
   const int64_t rows =
       a.nlim ? min(a.nrows, max((int64_t)0, (int64_t)*a.nlim - a.row0)) : a.nrows;  // row below: local to the launch
   const int64_t G = gridDim.x;
@@ -713,51 +923,71 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
     }
   }
   if constexpr (RESIDENT && GRAD) {
-    // live rows, each one's gradient stores overlapped with the next one's loads
-    const int n = row_len(a.V);
+    // Live rows, pipelined as in the CE kernel: the register refill rides
+    // with the gradient stores, the next row's leading vectors are staged into
+    // LDS during the reduction, the per-row records are scalar loads (the
+    // search for the row after next runs at the end of the iteration) and the
+    // id logit comes out of the registers through the block exchange.
+    using Regs = RowRegs<T, VEC, NCH, BLOCK, full_vectors(NCH, BLOCK)>;
+    constexpr int NPF = stage_depth(NCH, BLOCK);
+    __shared__ __attribute__((aligned(1024))) T pf[NPF > 0 ? NPF * BLOCK * VEC : 1];
+    // (the token's id rides along; the rest of its record is loaded again
+    // when the row starts, in time for the loss terms after the exchange)
+    struct LiveRow {
+      int64_t row, tok_i;  // row >= rows: none
+      int id;
+    };
     auto next_live = [&](int64_t from) {
-      int64_t q = from;
-      GrpoTok t{};
-      while (q < rows && !live(q, &t)) q += G;
+      LiveRow q{from, 0, -1};
+      for (; q.row < rows; q.row += G) {
+        const int64_t g = a.rowmap ? scalar_load(a.rowmap + a.row0 + q.row) : a.row0 + q.row;
+        const int64_t b = g / (a.L + 1), l = g - b * (a.L + 1);
+        if (l == a.L) continue;
+        q.tok_i = b * a.L + l;
+        const GrpoTok tk = load_tok(a.tok + q.tok_i);
+        q.id = tk.id;
+        if (tk.m != 0.f) break;
+      }
       return q;
     };
-    int64_t row = next_live(blockIdx.x);
-    if (row >= rows) return;
-    RowRegs<T, VEC, NCH, BLOCK> r;
-    r.load(logits + row * a.V, n);
+    LiveRow cur = next_live(blockIdx.x);
+    if (cur.row >= rows) return;
+    Regs r;
+    r.template load_staged<NPF>(logits + cur.row * a.V, row_len(a.V), pf);
+    LiveRow next = next_live(cur.row + G);
     int parity = 0;
     for (;;) {
+      const int n = row_len(a.V);  // per iteration (see row_len)
+      const int64_t row = cur.row;
+      const int id = cur.id;
       const T* in = logits + row * a.V;
-      // the token record is uniform: keep it in scalar registers, off the row's VGPR budget
-      GrpoTok tk = a.tok[token(row)];
-      tk.id = __builtin_amdgcn_readfirstlane(tk.id);
-      tk.old = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.old)));
-      tk.ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.ref)));
-      tk.adv = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.adv)));
-      tk.gs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tk.gs)));
-      const int64_t next = next_live(row + G);
-      const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
-      float m, s, M, R, rest;
-      r.reduce_lane(n, c, tk.id, &m, &s);
-      block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R);
-      const float lse2 = target_merge(M, R, xid * c, tk.id >= 0, &rest);
+      const T* src = next.row < rows ? logits + next.row * a.V : in;  // unconditional (see the CE kernel)
+      if constexpr (NPF > 0) {
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the previous row's reads of the stage have completed
+        Regs::template stage<NPF>(pf, src, n);
+      }
+      const GrpoTok tk = load_tok(a.tok + cur.tok_i);
+      float m, s, xt, M, R, X, rest;
+      r.reduce_lane(n, c, id, &m, &s, &xt);
+      block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R, xt, Regs::owns_target(id), &X);
+      const float xid = id >= 0 ? X : 0.f;
+      const float lse2 = target_merge(M, R, xid * c, id >= 0, &rest);
       parity ^= 1;
       r.opaque();
       const float lse = lse2 * kLn2;
-      const float logp = tk.id >= 0 ? xid * a.inv_T - lse : NAN;
+      const float logp = id >= 0 ? xid * a.inv_T - lse : NAN;
       float dlogp;
       const GrpoOut res = grpo_terms(a, tk, lse, logp, &dlogp);
-      if (threadIdx.x == 0) a.out[token(row)] = res;
       // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
       const float g = -dlogp * tk.gs;
       T* out = dlogits + row * a.V;
-      const T* src = next < rows ? logits + next * a.V : in;  // unconditional refill (see the CE kernel)
-      r.store_prob_grad_then_load(out, n, c, lse2, g, src);
+      r.template store_prob_grad_then_load<NPF>(out, n, c, lse2, g, src, pf);
       // the id element: (p_id - 1) * g = -(1 - p_id) * g (see reduce_lane)
-      if (tk.id >= 0 && (int)threadIdx.x == (tk.id % RowRegs<T, VEC, NCH, BLOCK>::kSpan) / VEC)
-        out[tk.id] = from_f32<T>(-rest * g);
-      if (next >= rows) break;
-      row = next;
+      if (Regs::owns_target(id)) out[id] = from_f32<T>(-rest * g);
+      if (threadIdx.x == 0) a.out[cur.tok_i] = res;  // after the row's stores (see the CE kernel)
+      if (next.row >= rows) break;
+      cur = next;
+      next = next_live(cur.row + G);
     }
   } else if constexpr (RESIDENT && BLOCK < 1024) {
     // forward only: the same (max, sum) arithmetic as the gradient path, so
@@ -995,11 +1225,8 @@ RowCfg choose_row_cfg(int64_t V, int esize, bool vec_ok) {
   RowCfg c{1024, 0, vec_ok ? 16 / esize : 1};
   if (!vec_ok) return c;
   const int64_t nv = V / c.vec;
-  static const RowCfg table[] = {{256, 1, 0},  {256, 2, 0},   {256, 4, 0},   {256, 8, 0},   {256, 12, 0},
-                                 {256, 16, 0}, {512, 12, 0},  {512, 16, 0},  {1024, 12, 0}, {1024, 16, 0},
-                                 {1024, 20, 0}, {1024, 24, 0}};
-  for (const RowCfg& t : table)
-    if (nv <= (int64_t)t.block * t.nch) return RowCfg{t.block, t.nch, c.vec};
+  for (const RowForm& f : kRowForms)
+    if (nv <= (int64_t)f.block * f.nch) return RowCfg{f.block, f.nch, c.vec};
   return c;
 }
 
@@ -1031,6 +1258,15 @@ int dispatch_cfg(const RowCfg& c, F&& f) {
   }
   set_error("internal: bad row config (%d, %d)", c.block, c.nch);
   return HK_EINVAL;
+}
+
+// The kernels take the leading full_vectors() vectors of a register-resident
+// form as full without testing them; choose_row_cfg's order guarantees it.
+bool form_fits(int64_t V, const RowCfg& c) {
+  const int64_t need = (int64_t)full_vectors(c.nch, c.block) * c.block * c.vec;
+  if (V >= need && V <= (int64_t)c.nch * c.block * c.vec) return true;
+  set_error("internal: a row of %lld elements given to the (%d x %d) form", (long long)V, c.block, c.nch);
+  return false;
 }
 
 // A persistent grid: `rounds` times the blocks the CUs hold at once for this
@@ -1178,6 +1414,13 @@ int grpo_compact_launch(int* rowmap, int* inv, int* n_live, const GrpoInputs& in
   return check_launch("compact_rows_kernel");
 }
 
+int ce_plan_launch(int* n_valid, int* rowmap, int* n_live, const int64_t* targets, int64_t rows, int64_t V,
+                   int64_t ignore_index, int has_ignore, hipStream_t st) {
+  hipLaunchKernelGGL(ce_plan_kernel, dim3(1), dim3(1024), 0, st, n_valid, rowmap, n_live, targets, rows, V,
+                     ignore_index, has_ignore);
+  return check_launch("ce_plan_kernel");
+}
+
 int count_valid_launch(int* n_valid, const int64_t* targets, int64_t rows, int64_t ignore_index, int has_ignore,
                        hipStream_t st) {
   hipLaunchKernelGGL(count_valid_kernel, dim3(1), dim3(1024), 0, st, n_valid, targets, rows, ignore_index,
@@ -1228,12 +1471,14 @@ int ce_lse_launch(const void* logits, const CeArgs& a, int dtype, hipStream_t st
 int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const int64_t* targets, int64_t rows,
                    int64_t V, int64_t ld_in, int64_t ld_out, int64_t ignore_index, int has_ignore, const int* n_valid,
                    int scale_by_n_valid, const float* row_scale, int dtype, hipStream_t st, const int* rows_lim,
-                   int64_t rows_off) {
+                   int64_t rows_off, const int* rowmap, const int* n_live) {
   if (rows == 0) return HK_OK;
   const int es = esize(dtype);
   CeArgs a{};
   a.rows_lim = rows_lim;
   a.rows_off = rows_off;
+  a.rowmap = rowmap;
+  a.n_live = n_live;
   a.targets = targets;
   a.loss_rows = loss_rows;
   a.n_valid = n_valid;
@@ -1263,8 +1508,12 @@ int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const in
         return check_launch("ce_fwd_grad_kernel");
       };
       if (cfg.vec == 1) return run(ce_fwd_grad_kernel<T, 1, 1, 1024, false>, 1024);
-      if constexpr (NCH == 0) return run(ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>, BLOCK);
-      else return run(ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>, BLOCK);
+      if constexpr (NCH == 0) {
+        return run(ce_fwd_grad_kernel<T, 16 / sizeof(T), 1, BLOCK, false>, BLOCK);
+      } else {
+        if (!form_fits(V, cfg)) return HK_EINVAL;
+        return run(ce_fwd_grad_kernel<T, 16 / sizeof(T), NCH, BLOCK, true>, BLOCK);
+      }
     });
   });
 }
@@ -1275,9 +1524,14 @@ using namespace hk;
 
 extern "C" {
 
+// [0, 256): the valid-row and live-row counts; then, when the workspace
+// holds it, the launch plan's row list (4 bytes a row).
+namespace {
+size_t ce_plan_bytes(int64_t rows) { return rows < (1LL << 31) ? ((size_t)rows * 4 + 255) / 256 * 256 : 0; }
+}  // namespace
+
 size_t hk_cross_entropy_workspace_size(int64_t rows) {
-  (void)rows;
-  return 256;
+  return 256 + ce_plan_bytes(rows > 0 ? rows : 0);
 }
 
 int hk_cross_entropy_fwd_grad(void* dlogits, float* loss_rows, float* loss_out, const void* logits,
@@ -1296,10 +1550,19 @@ int hk_cross_entropy_fwd_grad(void* dlogits, float* loss_rows, float* loss_out, 
   // ignore_index == -1 is the reference's "ignore nothing" sentinel (cross_entropy.py:197-198,219-225)
   const int has_ignore = ignore_index != -1;
   if (rows > 0) {
-    int rc = count_valid_launch(n_valid, targets, rows, ignore_index, has_ignore, st);
+    // with room for the plan, the live rows are dealt out evenly over the
+    // grid (a 256-byte workspace, the older minimum, still works: rows are
+    // then strided over the grid whether they are live or not)
+    const size_t plan = ce_plan_bytes(rows);
+    const bool planned = plan > 0 && workspace_bytes >= 256 + plan;
+    int* n_live = n_valid + 1;
+    int* rowmap = planned ? (int*)((char*)workspace + 256) : nullptr;
+    int rc = planned ? ce_plan_launch(n_valid, rowmap, n_live, targets, rows, V, ignore_index, has_ignore, st)
+                     : count_valid_launch(n_valid, targets, rows, ignore_index, has_ignore, st);
     if (rc) return rc;
     rc = ce_rows_launch(dlogits, loss_rows, logits, targets, rows, V, ld_logits, ld_dlogits, ignore_index, has_ignore,
-                        n_valid, reduction == HK_REDUCTION_MEAN, nullptr, dtype, st);
+                        n_valid, reduction == HK_REDUCTION_MEAN, nullptr, dtype, st, nullptr, 0, rowmap,
+                        planned ? n_live : nullptr);
     if (rc) return rc;
   }
   // the rows are already scaled by 1/max(n_valid, 1) for 'mean'

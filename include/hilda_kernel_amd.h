@@ -261,7 +261,10 @@ int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, con
 /* ----------------------------------------------------------------------- */
 /* CrossEntropy                                                            */
 /* ----------------------------------------------------------------------- */
-/* Bytes of device workspace the CrossEntropy entry points need (n_valid). */
+/* Bytes of device workspace the CrossEntropy entry points use: 256 (n_valid)
+ * plus 4 per row for the launch plan of hk_cross_entropy_fwd_grad, which deals
+ * the rows that get a gradient out evenly over the GPU. A workspace of 256
+ * bytes or more but less than this is accepted and runs without the plan. */
 size_t hk_cross_entropy_workspace_size(int64_t rows);
 
 /* Replaces cross_entropy_forward's training path (cross_entropy.py:206-236:

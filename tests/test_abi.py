@@ -131,6 +131,17 @@ def test_fused_linear_workspace_queries():
 
 
 @needs_lib
+def test_cross_entropy_workspace_query():
+    lib = _lib.load()
+    # 256 bytes of counters, then the launch plan's row list (4 bytes a row, whole 256-byte blocks)
+    assert lib.hk_cross_entropy_workspace_size(0) == 256
+    assert lib.hk_cross_entropy_workspace_size(1) == 512
+    assert lib.hk_cross_entropy_workspace_size(64) == 512
+    assert lib.hk_cross_entropy_workspace_size(65) == 768
+    assert lib.hk_cross_entropy_workspace_size(8192) == 256 + 8192 * 4
+
+
+@needs_lib
 def test_workspace_query_is_pure():
     lib = _lib.load()
     # atomic path: one [cols] fp64 row; partial path (bf16 -> fp32 accumulators): one row per row group

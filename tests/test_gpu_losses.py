@@ -217,6 +217,50 @@ def test_cross_entropy_c3_config():
     assert rel_fro(grad[sl].float() * n_valid, d_ref) < 1e-2
 
 
+def _ce_raw(logits, t, ignore_index, reduction, ws_bytes):
+    """hk_cross_entropy_fwd_grad through the C ABI with a workspace of ws_bytes."""
+    from kernels import _lib
+    n, V = logits.shape
+    d = torch.empty_like(logits)
+    rows = torch.empty(n, dtype=torch.float32, device=logits.device)
+    loss = torch.empty((), dtype=torch.float32, device=logits.device)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=logits.device)
+    _lib.call("hk_cross_entropy_fwd_grad", d.data_ptr(), rows.data_ptr(), loss.data_ptr(), logits.data_ptr(),
+              t.data_ptr(), n, V, V, V, int(ignore_index), _lib.REDUCTION[reduction], _lib.dtype_code(logits),
+              ws.data_ptr(), ws_bytes, _lib.stream_of(logits.device))
+    return d, rows, loss, int(ws[:4].view(torch.int32)[0])
+
+
+# row counts around the grid sizes (256 and 1024 blocks) and a handful of rows
+@pytest.mark.parametrize("V,N", [(128256, 300), (128256, 7), (151936, 260), (32000, 1100), (4096, 3000)])
+@pytest.mark.parametrize("ignore_index", [-100, -1])
+def test_cross_entropy_plan_matches_strided(V, N, ignore_index):
+    """With the full workspace the live rows are dealt out by the launch plan;
+    with 256 bytes they are strided over the grid. Both must agree bit for bit,
+    with ignored rows, targets out of range (NaN rows) and ignore_index -1."""
+    from kernels import _lib
+    dev = gpu()
+    logits, t = _ce_case(N, V, torch.bfloat16, 0.3, V + N)
+    t[1::11] = V + 5  # out of range: a NaN row, never live
+    t[2::13] = -7
+    if ignore_index == -1:
+        t[t == -100] = 3
+    logits, t = logits.to(dev), t.to(dev)
+    full = _lib.load().hk_cross_entropy_workspace_size(N)
+    assert full >= 256 + 4 * N
+    d1, r1, l1, nv1 = _ce_raw(logits, t, ignore_index, "mean", full)
+    d0, r0, l0, nv0 = _ce_raw(logits, t, ignore_index, "mean", 256)
+    valid = (t != ignore_index) if ignore_index != -1 else torch.ones_like(t, dtype=torch.bool)
+    assert nv1 == nv0 == int(valid.sum())
+    assert torch.equal(d1.view(torch.int16), d0.view(torch.int16))
+    assert torch.equal(r1.view(torch.int32), r0.view(torch.int32))
+    live = valid & (t >= 0) & (t < V)
+    assert torch.isnan(d1[valid & ~live].float()).all()
+    (_,), (d_ref,) = oracle.fwd_bwd(lambda z: oracle.cross_entropy_ref(z, t[live].cpu(), -100, "sum"),
+                                    [logits[live].cpu()], dtype=torch.float64)
+    assert_close(d1[live].float() * nv1, d_ref, name="planned dlogits * n_valid", **tol(torch.bfloat16))
+
+
 # --------------------------------------------------------------------------
 # selective log-softmax and GRPO
 # --------------------------------------------------------------------------

@@ -313,6 +313,7 @@ def bench_c3(K, dev, reps, flush, cpu=False):
     work = 2 * V * n_valid + 2 * V * N + 12 * N
     e = op_entry("C3", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
     e["n_valid"] = n_valid
+    e["row_bytes"] = V * logits.element_size()
     log(f"  cross_entropy (C3): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
     if cpu:
         import oracle
@@ -344,6 +345,7 @@ def bench_c4(K, dev, reps, flush, cpu=False):
 
     work = 2 * V * n_valid + 2 * V * B * (L + 1) + 36 * B * L
     e = op_entry("C4", time_events(fn, reps, flush), work, "GB/s", HBM_PEAK_GBPS)
+    e["row_bytes"] = V * logits.element_size()
     e["n_valid"] = n_valid
     log(f"  grpo_loss (C4): {e['ms']:.4f} ms  {e['value']:.0f} GB/s  ({e['frac']:.1%})")
     if cpu:
@@ -508,19 +510,52 @@ def cpu_baseline(seconds=10.0):
             "seconds_per_step": round(t, 4), "cpu_model": cpu_model}
 
 
-def copy_ceiling(work, dev, reps, flush):
-    """A device-to-device copy moving the same bytes (work/2 read, work/2 written), timed like the ops.
+def copy_ceiling(work, dev, reps, flush, row_bytes=None):
+    """A device copy moving the same bytes (work/2 read, work/2 written), timed like the ops: the practical
+    ceiling for an HBM-bound op (at a few GB it sits well below the 8 TB/s peak: read/write turnaround,
+    refresh, open pages).
 
-    What a plain streaming copy reaches at that size is the practical ceiling for an HBM-bound op:
-    at a few GB per op it sits well below the 8 TB/s peak (read/write turnaround, refresh).
+    The copy is the library's hand-written streaming kernel (hk_stream_copy): by default the flat order, the
+    whole GPU sweeping one contiguous front (the fastest order measured, faster than hipMemcpy); with
+    row_bytes, one row of that size per CU at a time in the order of the register-resident row kernels.
+    Returns GB/s.
     """
-    n = (work // 2 + 4095) // 4096 * 4096
+    from kernels import _lib
+    if row_bytes:
+        rows = max(1, (work // 2) // row_bytes)
+        n = rows * row_bytes
+        mode = _lib.COPY_ROWS
+    else:
+        n = (work // 2 + 4095) // 4096 * 4096
+        rows, mode = 1, _lib.COPY_FLAT
     src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    ms = statistics.median(time_events(lambda: dst.copy_(src), reps, flush))
+    st = _lib.stream_of(dev)
+
+    def fn():
+        _lib.call("hk_stream_copy", dst.data_ptr(), src.data_ptr(), rows, n // rows, mode, st)
+
+    fn()
+    torch.cuda.synchronize()
+    if not torch.equal(dst, src):
+        raise RuntimeError("hk_stream_copy produced a wrong copy")
+    ms = statistics.median(time_events(fn, reps, flush))
     del src, dst
     torch.cuda.empty_cache()
     return 2 * n / (ms * 1e-3) / 1e9
+
+
+def attach_copy(e, dev, reps, flush):
+    """e["copy_same_bytes"] (flat copy) and, for the row kernels' entries (e["row_bytes"]),
+    e["copy_rows_same_bytes"]: the op against copies of its own bytes."""
+    cc = copy_ceiling(e["work"], dev, reps, flush)
+    e["copy_same_bytes"] = {"value": round(cc, 1), "unit": "GB/s", "op_over_copy": round(e["value"] / cc, 3),
+                            "kernel": "hk_stream_copy flat"}
+    if e.get("row_bytes"):
+        cr = copy_ceiling(e["work"], dev, reps, flush, e["row_bytes"])
+        e["copy_rows_same_bytes"] = {"value": round(cr, 1), "unit": "GB/s", "op_over_copy": round(e["value"] / cr, 3),
+                                     "kernel": "hk_stream_copy rows of %d bytes" % e["row_bytes"]}
+    return e
 
 
 # ---------------------------------------------------------------------------
@@ -694,6 +729,9 @@ def main(argv=None):
                          "traffic for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     ap.add_argument("--reference-configs", action="store_true",
                     help="instead of the step: every op on the reference benchmarks' own shapes, as a markdown table")
+    ap.add_argument("--only-copy", action="store_true",
+                    help="with --only: after each op, a device copy of the same bytes timed the same way (its "
+                         "copyBuffer launches sit beside the op's kernels in a rocprofv3 trace)")
     ap.add_argument("--only", default=None,
                     help="comma list of op names: time only these (op-reps each, cache flushed between reps), with "
                          "no C2 headline step, copy ceilings or CPU baseline, and print their entries as JSON; "
@@ -742,6 +780,8 @@ def main(argv=None):
             else:
                 out[name] = table[name][0](K, dev, args.op_reps, flush)
             torch.cuda.empty_cache()
+            if args.only_copy and out[name].get("unit") == "GB/s":
+                attach_copy(out[name], dev, args.op_reps, flush)
         print(json.dumps(out), flush=True)
         return 0
     log(f"device: {torch.cuda.get_device_name(dev)}")
@@ -846,9 +886,13 @@ def main(argv=None):
         for name, e in ops.items():
             if e["unit"] != "GB/s":
                 continue
-            cc = copy_ceiling(e["work"], dev, max(3, args.op_reps // 2), flush)
-            e["copy_same_bytes"] = {"value": round(cc, 1), "unit": "GB/s", "op_over_copy": round(e["value"] / cc, 3)}
-            log(f"  {name}: copy {cc:.0f} GB/s, op at {e['value'] / cc:.1%} of it")
+            attach_copy(e, dev, max(3, args.op_reps // 2), flush)
+            cc = e["copy_same_bytes"]["value"]
+            extra = ""
+            if "copy_rows_same_bytes" in e:
+                cr = e["copy_rows_same_bytes"]["value"]
+                extra = f"; row-order copy {cr:.0f} GB/s, op at {e['value'] / cr:.1%} of it"
+            log(f"  {name}: copy {cc:.0f} GB/s, op at {e['value'] / cc:.1%} of it{extra}")
         del flush
 
     del c2

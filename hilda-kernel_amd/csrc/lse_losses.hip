@@ -34,10 +34,6 @@ namespace {
 // ---------------------------------------------------------------------------
 // register-resident row helpers
 // ---------------------------------------------------------------------------
-// s_waitcnt immediate for lgkmcnt(0) alone on gfx9-family parts (vmcnt 63 and
-// expcnt 7 leave those counters unwaited)
-constexpr int kWaitLgkm0 = 0xC07F;
-
 // max(a, b, c) in one instruction (fmaxf would add a canonicalising max per operand)
 __device__ __forceinline__ float max3(float a, float b, float c) {
   float r;
@@ -57,8 +53,10 @@ struct RowRegs {
   // branches; only a partial vector needs a per-lane test. Column indices are
   // 32-bit: the host rejects rows of 2^31 or more elements.
   // Vectors j < NFULL are full in every row that the caller hands over (it
-  // guarantees n >= NFULL * kSpan); only the LDS stage relies on it. The
-  // other tests stay scalar branches even where they always pass: each
+  // guarantees n >= NFULL * kSpan): their loads and stores need no test, so
+  // the compiler can count the loads in flight and wait for each vector's
+  // load in turn rather than for all of them at the first vector. The
+  // reduction's tests stay scalar branches even where they always pass: each
   // vector's work then stays a block of its own, which keeps the compiler
   // from overlapping the vectors' temporaries (and spilling).
   static constexpr int kSpan = BLOCK * VEC;
@@ -87,31 +85,6 @@ struct RowRegs {
         v[j] = ninf;  // defined on every path, so no value flows in from the previous row
       }
     }
-  }
-
-  // load() for a pipeline that refills vectors 0..NPF-1 from the LDS stage:
-  // the first row takes the same path (stage, the other vectors from global,
-  // then the staged ones from LDS), so at every use those registers come from
-  // an LDS read and the waits for the global loads can count down vector by
-  // vector instead of waiting for all of them at the first vector.
-  template <int NPF>
-  __device__ __forceinline__ void load_staged(const T* __restrict__ row, int n, T* lds) {
-    stage<NPF>(lds, row, n);
-    const int tc = lane_col();
-    const Pack<T, VEC> ninf = splat_pack<T, VEC>(-INFINITY);
-#pragma unroll
-    for (int j = NPF; j < NCH; ++j) {
-      const int lim = n - j * kSpan;  // uniform
-      if (j < NFULL || lim >= kSpan) {
-        v[j] = load_pack<T, VEC>(row + off(j, tc));
-      } else if (lim > 0) {
-        v[j] = load_pack<T, VEC>(row + off(j, tc < lim ? tc : 0));  // in-bounds address
-      } else {
-        v[j] = ninf;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NPF; ++j) v[j] = load_pack<T, VEC>(lds + (j * BLOCK + (int)threadIdx.x) * VEC);
   }
 
   // The unpacked floats of vector j with the lanes past the row end at -inf.
@@ -195,15 +168,16 @@ struct RowRegs {
   // Gradient of the row, p_j * g = 2^(x_j*c - lse2) * g computed in fp32 and
   // rounded once to T (the arithmetic of kernels/cross_entropy.py:159-166),
   // without the one-hot term (the caller patches the target element); then the
-  // row at `next` loaded into the same registers vector by vector, so the row's
-  // stores and the next row's loads are in flight together. Recomputing the
-  // exponential here instead of keeping 2^(x*c - m) from the sum pass measured
-  // as fast (the sum pass, which runs while HBM idles, writes no registers).
-  // With NPF > 0, vectors 0..NPF-1 of `next` come from the LDS stage that
-  // stage<NPF>() filled (the caller issued it for the same row).
-  template <int NPF = 0>
+  // row at `next` loaded into the same registers, so the row's stores and the
+  // next row's loads are in flight together. Recomputing the exponential here
+  // instead of keeping 2^(x*c - m) from the sum pass measured as fast. The
+  // loads follow all of the row's stores: issuing each beside its vector's
+  // store measured 3% slower on CrossEntropy [8192, 128256] and 2% on GRPO
+  // (HBM serves a run of writes, then a run of reads, better than the two
+  // interleaved). With this order, staging the next row's first half into LDS
+  // by DMA during the reduction (a second row in flight) measured no faster.
   __device__ __forceinline__ void store_prob_grad_then_load(T* out, int n, float c, float lse2, float g,
-                                                            const T* next, const T* lds = nullptr) {
+                                                            const T* next) {
     const int tc = lane_col();
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -214,37 +188,14 @@ struct RowRegs {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) x[e] = exp2_fast(fmaf(x[e], c, -lse2)) * g;
         if (j < NFULL || lim >= kSpan || tc < lim) store_pack_nt<T, VEC>(out + off(j, tc), pack<T, VEC>(x));
-        if (j < NPF) {
-          v[j] = load_pack<T, VEC>(lds + (j * BLOCK + (int)threadIdx.x) * VEC);
-        } else {
-          v[j] = load_pack<T, VEC>(next + off(j, lim >= kSpan || tc < lim ? tc : 0));  // see load()
-        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-  }
-
-  // LDS stage of a row's leading vectors: each full vector j < NPF of `row`
-  // copied into `lds` by LDS DMA (buffer_load_dwordx4 ... lds), which moves
-  // the data without holding VGPRs, so the copy can be in flight while the
-  // registers still hold (and reduce) the current row. Wave w's 64 lanes land
-  // in lane order in the 1 KiB at lds + (j*BLOCK + 64w)*VEC, so each lane
-  // reads back exactly the 16 bytes it would have loaded. The caller makes
-  // sure no earlier LDS read of the stage is still pending.
-  template <int NPF>
-  __device__ __forceinline__ static void stage(T* lds, const T* row, int n) {
-    static_assert(sizeof(T) * VEC == 16, "the stage moves 16 bytes a lane");
-    static_assert(NPF <= NFULL, "only vectors that are full in every row are staged");
-#if defined(__HIP_DEVICE_COMPILE__)
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), 0, n * (int)sizeof(T), kRsrcWord3);
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);  // the LDS base goes in M0
-    const uint32_t lane_off = (uint32_t)threadIdx.x * 16u;
 #pragma unroll
-    for (int j = 0; j < NPF; ++j)  // full vectors: every lane in bounds
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds + (j * BLOCK + wave * kWave) * VEC, 16, lane_off,
-                                               j * kSpan * (int)sizeof(T), 0, 0);
-#endif
+    for (int j = 0; j < NCH; ++j) {
+      const int lim = n - j * kSpan;  // uniform
+      if (j < NFULL || lim > 0) v[j] = load_pack<T, VEC>(next + off(j, lim >= kSpan || tc < lim ? tc : 0));  // see load()
+    }
   }
 };
 
@@ -301,8 +252,9 @@ __device__ __forceinline__ void block_lse2_ms(float m, float s, float* red, int 
   if (X && own) r[2 * NW] = x;
   // A barrier for LDS traffic only: each wave's LDS writes have completed
   // before it arrives. __syncthreads() would also wait for every global load
-  // the wave has in flight, including an LDS stage of the next row. (One asm
-  // statement, so the compiler moves no memory access across the barrier.)
+  // the wave has in flight, such as the next row's refill in the forward-only
+  // loop. (One asm statement, so the compiler moves no memory access across
+  // the barrier.)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   m = r[0];
   s = r[NW];
@@ -451,12 +403,6 @@ constexpr int full_vectors(int nch, int block) {
   return 0;
 }
 
-// LDS stage depth of a register-resident gradient form (RowRegs::stage): the
-// 1024-lane forms, one block a CU whose waves all reduce at once, stage up to
-// 9 of their full 16-byte vectors (144 KiB of the CU's 160 KiB of LDS).
-constexpr int stage_depth(int nch, int block) {
-  return block == 1024 ? (full_vectors(nch, block) < 9 ? full_vectors(nch, block) : 9) : 0;
-}
 
 // ---------------------------------------------------------------------------
 // CrossEntropy
@@ -492,12 +438,10 @@ __device__ __forceinline__ float ce_scale(const CeArgs& a) {
 // never read.
 template <typename T, int VEC, int NCH, int BLOCK, bool RESIDENT>
 __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T* logits, CeArgs a) {
-  constexpr int NPF = RESIDENT ? stage_depth(NCH, BLOCK) : 0;
   // dlogits may alias logits (in-place use): every element is read before the
   // same thread overwrites it, and a row's stores are issued before the next
   // row's loads of the same vector, so the pointers are not declared __restrict__.
   __shared__ float red[BlockRed<BLOCK / kWave>::kFloats];
-  __shared__ __attribute__((aligned(1024))) T pf[NPF > 0 ? NPF * BLOCK * VEC : 1];
   ce_bound(a);
   const float scale = ce_scale(a);
   const int64_t G = gridDim.x;
@@ -515,12 +459,10 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
       }
     }
     // Then the live rows. Row r's gradient stores go out with the loads of the
-    // next live row r' (register refill), and while r is reduced the leading
-    // NPF vectors of r' are already on their way into LDS, so HBM has work
-    // during the reduction and the block exchange too. The per-row scalars
-    // (targets, row scale) are scalar loads, so waiting for them never waits
-    // for the staged copy; the search for the row after r' runs at the end of
-    // the iteration, while r's stores and r''s loads are in flight. The target
+    // next live row r' (register refill). The per-row scalars (targets, row
+    // scale) are scalar loads, so waiting for them never waits for the vector
+    // loads in flight; the search for the row after r' runs at the end of the
+    // iteration, while r's stores and r''s loads are in flight. The target
     // logit comes out of the registers, broadcast by the block exchange.
     // The block's live rows: with a plan, rowmap[q] for q = blockIdx.x,
     // + G, ... (every such row is live, and the blocks' counts differ by one
@@ -541,7 +483,7 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
     LiveRow cur = next_live(blockIdx.x);
     if (cur.q >= nq) return;
     Regs r;
-    r.template load_staged<NPF>(logits + cur.row * a.ld_in, n, pf);
+    r.load(logits + cur.row * a.ld_in, n);
     LiveRow next = next_live(cur.q + G);
     int parity = 0;
     for (;;) {
@@ -549,14 +491,10 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
       const int64_t row = cur.row;
       const int t = (int)cur.t;
       const T* in = logits + row * a.ld_in;
-      // The refill and the stage are unconditional (the last row re-reads
-      // itself, from L2, and the data is not used), so the registers carry one
-      // definition around the loop and every path has the same loads in flight.
+      // The refill is unconditional (the last row re-reads itself, from L2,
+      // and the data is not used), so the registers carry one definition
+      // around the loop and every path has the same loads in flight.
       const T* src = next.q < nq ? logits + next.row * a.ld_in : in;
-      if constexpr (NPF > 0) {
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the previous row's reads of the stage have completed
-        Regs::template stage<NPF>(pf, src, n);
-      }
       const float gscale = a.row_scale ? scale * scalar_load(a.row_scale + row) : scale;
       float m, s, xt, M, R, X, rest;
       r.reduce_lane(n, kLog2e, t, &m, &s, &xt);
@@ -565,12 +503,10 @@ __global__ __launch_bounds__(BLOCK) void ce_fwd_grad_kernel(T* dlogits, const T*
       parity ^= 1;
       r.opaque();
       T* out = dlogits + row * a.ld_out;
-      r.template store_prob_grad_then_load<NPF>(out, n, kLog2e, lse2, gscale, src, pf);
+      r.store_prob_grad_then_load(out, n, kLog2e, lse2, gscale, src);
       // the target element: (p_t - 1) * g = -(1 - p_t) * g, stored after (and
       // over) the vector store of the same thread
       if (Regs::owns_target(t)) out[t] = from_f32<T>(-rest * gscale);
-      // (after the row's stores: a store ahead of them would hold up the
-      // first LDS refill, which waits for the stage's loads in issue order)
       if (threadIdx.x == 0) a.loss_rows[row] = (lse2 * kLn2 - X) * scale;
       if (next.q >= nq) break;
       cur = next;
@@ -892,10 +828,9 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
   // dlogits may alias logits (FusedLinear-GRPO writes the gradient over the
   // chunk's logits): every element is read by the thread that later
   // overwrites it (the gradient path takes the id logit from the registers,
-  // the forward-only paths read it before the row's reduction barriers), a
+  // the forward-only paths read it before the row's reduction barriers) and a
   // row's stores are issued before the next row's loads of the same vector,
-  // and a row is staged into LDS only before any of its stores, so the
-  // pointers are not declared __restrict__.
+  // so the pointers are not declared __restrict__.
   __shared__ float red[BlockRed<BLOCK / kWave>::kFloats];
   const int64_t rows =
       a.nlim ? min(a.nrows, max((int64_t)0, (int64_t)*a.nlim - a.row0)) : a.nrows;  // row below: local to the launch
@@ -924,13 +859,10 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
   }
   if constexpr (RESIDENT && GRAD) {
     // Live rows, pipelined as in the CE kernel: the register refill rides
-    // with the gradient stores, the next row's leading vectors are staged into
-    // LDS during the reduction, the per-row records are scalar loads (the
+    // with the gradient stores, the per-row records are scalar loads (the
     // search for the row after next runs at the end of the iteration) and the
     // id logit comes out of the registers through the block exchange.
     using Regs = RowRegs<T, VEC, NCH, BLOCK, full_vectors(NCH, BLOCK)>;
-    constexpr int NPF = stage_depth(NCH, BLOCK);
-    __shared__ __attribute__((aligned(1024))) T pf[NPF > 0 ? NPF * BLOCK * VEC : 1];
     // (the token's id rides along; the rest of its record is loaded again
     // when the row starts, in time for the loss terms after the exchange)
     struct LiveRow {
@@ -953,7 +885,7 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
     LiveRow cur = next_live(blockIdx.x);
     if (cur.row >= rows) return;
     Regs r;
-    r.template load_staged<NPF>(logits + cur.row * a.V, row_len(a.V), pf);
+    r.load(logits + cur.row * a.V, row_len(a.V));
     LiveRow next = next_live(cur.row + G);
     int parity = 0;
     for (;;) {
@@ -962,10 +894,6 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
       const int id = cur.id;
       const T* in = logits + row * a.V;
       const T* src = next.row < rows ? logits + next.row * a.V : in;  // unconditional (see the CE kernel)
-      if constexpr (NPF > 0) {
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the previous row's reads of the stage have completed
-        Regs::template stage<NPF>(pf, src, n);
-      }
       const GrpoTok tk = load_tok(a.tok + cur.tok_i);
       float m, s, xt, M, R, X, rest;
       r.reduce_lane(n, c, id, &m, &s, &xt);
@@ -981,10 +909,10 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
       // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
       const float g = -dlogp * tk.gs;
       T* out = dlogits + row * a.V;
-      r.template store_prob_grad_then_load<NPF>(out, n, c, lse2, g, src, pf);
+      r.store_prob_grad_then_load(out, n, c, lse2, g, src);
       // the id element: (p_id - 1) * g = -(1 - p_id) * g (see reduce_lane)
       if (Regs::owns_target(id)) out[id] = from_f32<T>(-rest * g);
-      if (threadIdx.x == 0) a.out[cur.tok_i] = res;  // after the row's stores (see the CE kernel)
+      if (threadIdx.x == 0) a.out[cur.tok_i] = res;
       if (next.row >= rows) break;
       cur = next;
       next = next_live(cur.row + G);
@@ -1274,8 +1202,10 @@ bool form_fits(int64_t V, const RowCfg& c) {
 // rounds, the second round's blocks start as the first round's finish, which
 // evens out rows of uneven cost: GRPO's prefix-masked positions, strided over
 // the grid, give some blocks a third more live rows than others (C4 1.70 ms
-// with one round, 1.65 with two). Rows of even cost keep one round, where each
-// block's next-row prefetch covers more rows (CE 2048 x 32000: 64 against 70 us).
+// with one round, 1.65 with two), and CrossEntropy's 1024-lane form gains 1%
+// ([8192, 128256]: 744 against 750 us). The smaller CrossEntropy forms keep
+// one round, where each block's next-row prefetch covers more rows (2048 x
+// 32000: 64 against 70 us).
 int64_t resident_grid(const void* kernel, int64_t rows, int block, int rounds = 1) {
   const int dev = current_device();
   const int cu = dev >= 0 ? cu_count(dev) : 256;
@@ -1503,7 +1433,8 @@ int ce_rows_launch(void* dlogits, float* loss_rows, const void* logits, const in
       constexpr int BLOCK = decltype(blk)::value;
       constexpr int NCH = decltype(nch)::value;
       auto run = [&](auto kern, int block) {
-        const dim3 grid((unsigned)resident_grid((const void*)kern, rows, block));
+        // the 1024-lane forms (one block a CU) take two rounds (see resident_grid)
+        const dim3 grid((unsigned)resident_grid((const void*)kern, rows, block, block == 1024 ? 2 : 1));
         hipLaunchKernelGGL(kern, grid, dim3(block), 0, st, (T*)dlogits, (const T*)logits, a);
         return check_launch("ce_fwd_grad_kernel");
       };

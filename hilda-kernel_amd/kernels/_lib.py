@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 F32, F16, BF16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
 DW_AUTO, DW_ATOMIC, DW_PARTIAL = 0, 1, 2
+COPY_FLAT, COPY_ROWS = 0, 1
 REDUCTION = {"none": 0, "mean": 1, "sum": 2}
 
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
@@ -34,6 +35,7 @@ SIGNATURES = {
     "hk_rms_norm_bwd_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32, _i32]),
     "hk_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
     "hk_rms_norm_bwd_noalloc": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
+    "hk_stream_copy": (_i32, [_p, _p, _i64, _i64, _i32, _p]),
     "hk_fused_add_rms_norm_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p]),
     "hk_fused_add_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
     "hk_rope": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

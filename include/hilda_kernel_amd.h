@@ -347,6 +347,20 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
                                   int64_t H, int64_t V, int64_t ignore_index, int reduction, int dtype, int64_t chunk,
                                   void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
+/* ----------------------------------------------------------------------- */
+/* Streaming copies (measurement references)                               */
+/* ----------------------------------------------------------------------- */
+#define HK_COPY_FLAT 0
+#define HK_COPY_ROWS 1
+
+/* No counterpart in the reference: a copy of rows * row_bytes bytes (rows of
+ * whole 16-byte vectors, 16-byte aligned, no overlap) that a benchmark times
+ * beside an HBM-bound op of the same bytes. HK_COPY_FLAT sweeps the buffer
+ * with the whole GPU in one contiguous front (the fastest order measured);
+ * HK_COPY_ROWS moves one row per CU at a time in the order of the
+ * register-resident row kernels (row_bytes <= 384 KiB). */
+int hk_stream_copy(void* dst, const void* src, int64_t rows, int64_t row_bytes, int mode, hk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

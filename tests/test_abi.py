@@ -110,6 +110,9 @@ def test_argument_validation_losses_without_gpu():
     _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 4, 16, 12, 1e-6, 2, None), "multiple of 8")
     _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 4, 16, 8 * 256 * 8 + 8, 1e-6, 2, None), "at most")
     _expect_einval(lib.hk_attn_res_bwd(p, p, p, p, p, p, p, p, p, 4, 16, 64, 2, ws, 8, None), "workspace too small")
+    _expect_einval(lib.hk_stream_copy(p, p, 4, 64, 7, None), "copy mode")
+    _expect_einval(lib.hk_stream_copy(p, p, 4, 24, _lib.COPY_FLAT, None), "16-byte")
+    _expect_einval(lib.hk_stream_copy(p, p, 4, 24 * 1024 * 16 + 16, _lib.COPY_ROWS, None), "at most")
 
 
 @needs_lib

@@ -561,6 +561,33 @@ def attach_copy(e, dev, reps, flush):
 # ---------------------------------------------------------------------------
 # the reference's own benchmark shapes, each op against a copy of its bytes
 # ---------------------------------------------------------------------------
+def dw_sweep(dev, reps):
+    """RMSNorm backward with the weight gradient by fp64 atomics on one row against fp32 partial rows summed in a
+    second pass, over rows x H, fp32 and bf16: the sweep behind HK_DW_AUTO's choice (the reference switches to
+    atomics when rows <= 8 x CU count, rms_norm.py:325-326). Median call time with a cache flush between calls, as
+    a markdown table on stdout."""
+    from kernels import rms_norm as rn, _lib
+    flush = Flusher(dev)
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    gen = torch.Generator(device=dev).manual_seed(0)
+    print(f"| dtype | rows | H | partial rows (us) | fp64 atomics (us) | atomics / partial |")
+    print("|---|---|---|---|---|---|")
+    for dt in (torch.float32, torch.bfloat16):
+        for H in (1024, 4096, 8192):
+            for rows in sorted({16, 64, 256, 1024, 2048, 8 * cu, 16384}):
+                x = torch.randn(rows, H, generator=gen, device=dev).to(dt)
+                w = torch.randn(H, generator=gen, device=dev).to(dt)
+                dy = torch.randn(rows, H, generator=gen, device=dev).to(dt)
+                _, xf, rs = rn.rms_norm_forward(x, w)
+                t = {}
+                for mode in (_lib.DW_PARTIAL, _lib.DW_ATOMIC):
+                    t[mode] = statistics.median(time_events(lambda: rn.rms_norm_backward(dy, xf, w, rs, mode), reps,
+                                                            flush)) * 1e3
+                print(f"| {str(dt).split('.')[-1]} | {rows} | {H} | {t[_lib.DW_PARTIAL]:.1f} | {t[_lib.DW_ATOMIC]:.1f} "
+                      f"| {t[_lib.DW_ATOMIC] / t[_lib.DW_PARTIAL]:.2f} |", flush=True)
+                del x, w, dy, xf, rs
+
+
 def reference_configs(dev, reps):
     """Every HBM-bound op on the shapes the reference's benchmarks time, fwd and bwd separately, with the
     algorithmic bytes of each call over a device copy of the same bytes; the fused-linear ops in TFLOP/s.
@@ -727,6 +754,9 @@ def main(argv=None):
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="finish with three plain 1 GiB device-to-device copies (reference kernel of known "
                          "traffic for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
+    ap.add_argument("--dw-sweep", action="store_true",
+                    help="instead of the step: RMSNorm backward, dW by fp64 atomics against partial rows over rows x H, "
+                         "as a markdown table")
     ap.add_argument("--reference-configs", action="store_true",
                     help="instead of the step: every op on the reference benchmarks' own shapes, as a markdown table")
     ap.add_argument("--only-copy", action="store_true",
@@ -754,6 +784,9 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.reference_configs:
         reference_configs(dev, max(3, args.op_reps // 2))
+        return 0
+    if args.dw_sweep:
+        dw_sweep(dev, args.op_reps)
         return 0
     if args.only:
         table = dict(op_table())

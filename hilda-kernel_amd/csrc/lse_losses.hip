@@ -598,40 +598,61 @@ __global__ __launch_bounds__(1024) void count_valid_kernel(int* __restrict__ n_v
 // The CrossEntropy launch plan, one block: *n_valid = the rows whose target is
 // not the ignore index (the divisor of 'mean') and rowmap[0 .. *n_live) the rows
 // that get a gradient (target not ignored and inside [0, V)), in order, so the
-// persistent grid can deal them out evenly. Per 1024 rows, a wave ballot and an
-// exclusive scan of the 16 wave counts; rows < 2^31 (the launcher checks).
+// persistent grid can deal them out evenly. Rows are taken 1024 at a time
+// (row s*1024 + thread, up to kSteps steps a pass): each wave's ballot of its
+// 64 rows is counted into LDS, one barrier, then every wave knows the live
+// rows before its own and writes its live rows packed (coalesced stores).
+// rows < 2^31 (the launcher checks).
 __global__ __launch_bounds__(1024) void ce_plan_kernel(int* __restrict__ n_valid, int* __restrict__ rowmap,
                                                        int* __restrict__ n_live, const int64_t* __restrict__ t,
                                                        int64_t rows, int64_t V, int64_t ignore_index,
                                                        int has_ignore) {
-  __shared__ int wcount[2][16];
+  constexpr int kSteps = 8;
+  __shared__ int cnt[kSteps][16];
+  __shared__ int vcnt[16];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  int live_base = 0, valid_base = 0;  // counts before this 1024-row step (the same in every lane)
-  for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
-    const int64_t r = r0 + threadIdx.x;
-    const int64_t tr = r < rows ? t[r] : ignore_index;
-    const bool valid = r < rows && (!has_ignore || tr != ignore_index);
-    const bool live = valid && tr >= 0 && tr < V;
-    const uint64_t bal = __ballot(live);
-    const uint64_t bv = __ballot(valid);
+  const uint64_t below = (1ull << lane) - 1ull;
+  int live_base = 0, valid_total = 0;  // the same in every lane
+  for (int64_t p0 = 0; p0 < rows; p0 += kSteps * 1024) {
+    uint64_t bal[kSteps];
+    int valid = 0;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int64_t r = p0 + s * 1024 + threadIdx.x;
+      const int64_t tr = r < rows ? t[r] : 0;
+      const bool v = r < rows && (!has_ignore || tr != ignore_index);
+      valid += v;
+      bal[s] = __ballot(v && tr >= 0 && tr < V);
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) valid += __shfl_xor(valid, o, kWave);
     if (lane == 0) {
-      wcount[0][wave] = __popcll(bal);
-      wcount[1][wave] = __popcll(bv);
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) cnt[s][wave] = __popcll(bal[s]);
+      vcnt[wave] = valid;
     }
     __syncthreads();
-    int before = live_base, total = live_base, vtotal = valid_base;
-    for (int w = 0; w < 16; ++w) {
-      before += w < wave ? wcount[0][w] : 0;
-      total += wcount[0][w];
-      vtotal += wcount[1][w];
+    // rowmap order: step, then wave, then lane
+    int run = live_base;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      int before = 0, step_total = 0;
+      for (int w = 0; w < 16; ++w) {
+        const int c = cnt[s][w];
+        step_total += c;
+        before += w < wave ? c : 0;
+      }
+      if (bal[s] >> lane & 1ull) rowmap[run + before + __popcll(bal[s] & below)] = (int)(p0 + s * 1024 + threadIdx.x);
+      run += step_total;
     }
-    if (live) rowmap[before + __popcll(bal & ((1ull << lane) - 1ull))] = (int)r;
-    live_base = total;
-    valid_base = vtotal;
-    __syncthreads();  // wcount is rewritten by the next step
+    int vt = 0;
+    for (int w = 0; w < 16; ++w) vt += vcnt[w];
+    live_base = run;
+    valid_total += vt;
+    __syncthreads();  // cnt and vcnt are rewritten by the next pass
   }
   if (threadIdx.x == 0) {
-    *n_valid = valid_base;
+    *n_valid = valid_total;
     *n_live = live_base;
   }
 }

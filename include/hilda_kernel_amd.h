@@ -197,7 +197,7 @@ size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int
 
 /* Replaces fused_linear_jsd_forward (fused_linear_jsd.py:114-205): per chunk of
  * `chunk` rows, student logits s_input[BT,H] * s_weight[V,H]^T and teacher
- * logits t_input[BT,Ht] * t_weight[V,Ht]^T on bf16/fp16 MFMA, both
+ * logits t_input[BT,Ht] * t_weight[V,Ht]^T on MFMA (fp32, bf16 or fp16), both
  * temperature log-softmaxes, JSD(beta) per row divided by
  * max(#labels != ignore_index, 1) (BT without labels), and (dinput, dweight
  * non-null) the student dlogits contracted into dinput [BT,H] and dweight
@@ -221,7 +221,7 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
 size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int dtype,
                                            int with_grad);
 
-/* hidden (B, L+1, H) and weight [V, H] (bf16 or fp16, contiguous): logits =
+/* hidden (B, L+1, H) and weight [V, H] (fp32, bf16 or fp16, contiguous): logits =
  * hidden weight^T, then exactly hk_grpo_loss_fwd's loss, kl_mean, clip_ratio
  * and per-token rows, and with dhidden (B, L+1, H) / dweight [V, H] (both or
  * neither) the gradients of the loss at unit upstream gradient (zero rows of
@@ -333,14 +333,14 @@ size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64
                                                     int with_grad);
 
 /* Replaces fused_linear_cross_entropy_forward (fused_linear_cross_entropy.py:103-171)
- * and its backward scaling (:192-210). hidden [BT,H], weight [V,H] (bf16 or
- * fp16, contiguous); targets [BT] int64; rows equal to ignore_index are ignored.
+ * and its backward scaling (:192-210). hidden [BT,H], weight [V,H] (fp32, bf16
+ * or fp16, contiguous); targets [BT] int64; rows equal to ignore_index are ignored.
  * loss_rows[r] = CE of row r (scaled by 1/max(n_valid,1) when gradients are
  * computed with reduction mean); loss_out (nullable) = sum, or mean over valid
  * rows. With dhidden/dweight (both or neither): the gradients of the reduced
  * loss at unit upstream gradient, each row's gradient further multiplied by
  * row_scale[r] when row_scale is given (reduction 'none' backward). Logits are
- * produced `chunk` rows at a time on bf16/fp16 MFMA, for the rows whose target
+ * produced `chunk` rows at a time on MFMA (fp32 inputs on the fp32 MFMA), for the rows whose target
  * is not ignore_index only (compacted on the device); dW is summed in fp32. */
 int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
                                   const void* weight, const int64_t* targets, const float* row_scale, int64_t BT,

@@ -252,6 +252,133 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
   }
 }
 
+// ------------------------------------------------------------------------
+// rows too long to hold in registers (more than 16 waves x 8 16-byte vectors:
+// fp32 rows over 32768 columns, 16-bit over 65536)
+// ------------------------------------------------------------------------
+constexpr int kStreamLanes = 1024;
+
+// Forward: one 1024-lane block per row, two passes over the row (the sum of
+// squares, then the normalised row; with ADD the first pass stores s = x + r
+// and the second reads s back). The arithmetic is the register form's.
+template <typename T, typename W, int VEC, bool ADD>
+__global__ __launch_bounds__(kStreamLanes) void rmsnorm_fwd_stream_kernel(
+    T* __restrict__ y, T* s_out, float* __restrict__ rstd_out, const T* __restrict__ x, const T* __restrict__ r,
+    const W* __restrict__ w, int cols, int64_t ld_x, int64_t ld_r, int64_t ld_y, int64_t ld_s, float eps) {
+  __shared__ float red[kStreamLanes / kWave];
+  const int64_t row = blockIdx.x;
+  float ss = 0.f;
+  for (int col = (int)threadIdx.x * VEC; col < cols; col += kStreamLanes * VEC) {
+    Pack<T, VEC> xv = load_pack<T, VEC>(x + row * ld_x + col);
+    float a[VEC];
+    unpack(xv, a);
+    if constexpr (ADD) {
+      float b[VEC];
+      unpack(load_pack<T, VEC>(r + row * ld_r + col), b);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) a[i] += b[i];
+      xv = pack<T, VEC>(a);
+      store_pack<T, VEC>(s_out + row * ld_s + col, xv);
+      unpack(xv, a);  // s as stored
+    }
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) ss = fmaf(a[i], a[i], ss);
+  }
+  ss = block_sum<kStreamLanes / kWave>(ss, red);
+  const float rstd = __builtin_amdgcn_rsqf(ss / (float)cols + eps);
+  if (threadIdx.x == 0) rstd_out[row] = rstd;
+  for (int col = (int)threadIdx.x * VEC; col < cols; col += kStreamLanes * VEC) {
+    // with ADD: this thread's own stores of the first pass
+    float a[VEC], wf[VEC];
+    unpack(load_pack<T, VEC>(ADD ? s_out + row * ld_s + col : x + row * ld_x + col), a);
+    unpack(load_pack<W, VEC>(w + col), wf);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) a[i] = round_through<T>(a[i] * rstd) * wf[i];
+    store_pack<T, VEC>(y + row * ld_y + col, pack<T, VEC>(a));
+  }
+}
+
+// Backward, first kernel: per row c = rstd^3 * <dy * w, x> / n (one
+// 1024-lane block per row).
+template <typename T, typename W, int VEC>
+__global__ __launch_bounds__(kStreamLanes) void rmsnorm_bwd_dot_kernel(float* __restrict__ coef,
+                                                                       const T* __restrict__ dy,
+                                                                       const T* __restrict__ x,
+                                                                       const W* __restrict__ w,
+                                                                       const float* __restrict__ rstd, int cols,
+                                                                       int64_t ld_dy, int64_t ld_x) {
+  __shared__ float red[kStreamLanes / kWave];
+  const int64_t row = blockIdx.x;
+  float dot = 0.f;
+  for (int col = (int)threadIdx.x * VEC; col < cols; col += kStreamLanes * VEC) {
+    float g[VEC], a[VEC], wf[VEC];
+    unpack(load_pack<T, VEC>(dy + row * ld_dy + col), g);
+    unpack(load_pack<T, VEC>(x + row * ld_x + col), a);
+    unpack(load_pack<W, VEC>(w + col), wf);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) dot = fmaf(g[i] * wf[i], a[i], dot);
+  }
+  dot = block_sum<kStreamLanes / kWave>(dot, red);
+  if (threadIdx.x == 0) {
+    const float rs = rstd[row];
+    coef[row] = rs * rs * rs * (dot / (float)cols);
+  }
+}
+
+// Backward, second kernel: block b takes column slice b % nslice (256 lanes x
+// kSliceVecs vectors) of the rows of group b / nslice, writes dX there and
+// sums its dW part over those rows in registers (A: fp64 for fp32 inputs),
+// one fp32 partial row slice per group.
+constexpr int kSliceLanes = 256, kSliceVecs = 4;
+template <typename T, typename W, typename A, int VEC, bool HAS_DS>
+__global__ __launch_bounds__(kSliceLanes) void rmsnorm_bwd_cols_kernel(
+    T* __restrict__ dx, float* __restrict__ part, const T* __restrict__ dy, const T* __restrict__ ds,
+    const T* __restrict__ x, const W* __restrict__ w, const float* __restrict__ rstd,
+    const float* __restrict__ coef, int64_t rows, int cols, int64_t ld_dy, int64_t ld_ds, int64_t ld_x,
+    int64_t ld_dx, int nslice, int64_t rows_per_group) {
+  const int64_t group = blockIdx.x / nslice;
+  const int c0 = (int)(blockIdx.x % nslice) * kSliceLanes * VEC * kSliceVecs;
+  A acc[kSliceVecs][VEC];
+  float wf[kSliceVecs][VEC];
+#pragma unroll
+  for (int j = 0; j < kSliceVecs; ++j) {
+    const int col = c0 + (j * kSliceLanes + (int)threadIdx.x) * VEC;
+    if (col < cols) unpack(load_pack<W, VEC>(w + col), wf[j]);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[j][i] = A(0);
+  }
+  const int64_t r0 = group * rows_per_group, r1 = min(rows, r0 + rows_per_group);
+  for (int64_t row = r0; row < r1; ++row) {
+    const float rs = rstd[row], c = coef[row];
+#pragma unroll
+    for (int j = 0; j < kSliceVecs; ++j) {
+      const int col = c0 + (j * kSliceLanes + (int)threadIdx.x) * VEC;
+      if (col < cols) {
+        float g[VEC], a[VEC], o[VEC];
+        unpack(load_pack<T, VEC>(dy + row * ld_dy + col), g);
+        unpack(load_pack<T, VEC>(x + row * ld_x + col), a);
+        if constexpr (HAS_DS) unpack(load_pack<T, VEC>(ds + row * ld_ds + col), o);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          float v = rs * (g[i] * wf[j][i]) - c * a[i];
+          if constexpr (HAS_DS) v += o[i];
+          o[i] = v;
+          acc[j][i] += A(g[i]) * A(a[i] * rs);
+        }
+        store_pack<T, VEC>(dx + row * ld_dx + col, pack<T, VEC>(o));
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kSliceVecs; ++j) {
+    const int col = c0 + (j * kSliceLanes + (int)threadIdx.x) * VEC;
+    if (col < cols) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) part[group * cols + col + i] = (float)acc[j][i];
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void fill_zero_f64(double* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 0.0;
@@ -385,9 +512,29 @@ int fwd_impl(void* y, void* s, float* rstd, const void* x, const void* r, const 
                 aligned_to(w, (size_t)ws * vec);
   if (add) vec_ok = vec_ok && rows_aligned(r, ld_r, es) && rows_aligned(s, ld_s, es);
   Geom g;
-  HK_REQUIRE(choose_geom(cols, es, vec_ok, &g), "cols=%lld exceeds the supported row length", (long long)cols);
-  const int64_t grid = cdiv(rows, g.rpb);
   hipStream_t st = (hipStream_t)stream;
+  if (!choose_geom(cols, es, vec_ok, &g)) {
+    // rows too long for the register form: two streaming passes per row
+    return dispatch_xw(dt_x, dt_w, [&](auto tx, auto tw) {
+      using T = typename decltype(tx)::type;
+      using W = typename decltype(tw)::type;
+      auto launch = [&](auto vec_c) {
+        constexpr int VEC = decltype(vec_c)::value;
+        if (add)
+          hipLaunchKernelGGL((rmsnorm_fwd_stream_kernel<T, W, VEC, true>), dim3((unsigned)rows), dim3(kStreamLanes),
+                             0, st, (T*)y, (T*)s, rstd, (const T*)x, (const T*)r, (const W*)w, (int)cols, ld_x, ld_r,
+                             ld_y, ld_s, eps);
+        else
+          hipLaunchKernelGGL((rmsnorm_fwd_stream_kernel<T, W, VEC, false>), dim3((unsigned)rows),
+                             dim3(kStreamLanes), 0, st, (T*)y, (T*)nullptr, rstd, (const T*)x, (const T*)nullptr,
+                             (const W*)w, (int)cols, ld_x, ld_x, ld_y, ld_y, eps);
+        return check_launch("rmsnorm_fwd_stream_kernel");
+      };
+      if (vec_ok) return launch(std::integral_constant<int, 16 / sizeof(T)>{});
+      return launch(std::integral_constant<int, 1>{});
+    });
+  }
+  const int64_t grid = cdiv(rows, g.rpb);
   int rc = dispatch_xw(dt_x, dt_w, [&](auto tx, auto tw) {
     using T = typename decltype(tx)::type;
     using W = typename decltype(tw)::type;
@@ -428,12 +575,35 @@ struct BwdPlan {
   int64_t parts;      // partial rows: one per block (rpb > 1) or per group
   bool atomic;
   size_t total;
+  // rows too long for the register form: rmsnorm_bwd_dot_kernel, then
+  // rmsnorm_bwd_cols_kernel over groups x nslice column slices (partial rows,
+  // whatever dw_mode asks), the per-row coefficients after the partial rows
+  bool stream = false;
+  int nslice = 0;
+  int vec = 1;
+  size_t coef_off = 0;
 };
 
 constexpr size_t kBwdLdsMax = 32 * 1024;
 
 bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int cu, BwdPlan* p) {
-  if (!choose_geom(cols, es, vec_ok, &p->g)) return false;
+  if (!choose_geom(cols, es, vec_ok, &p->g)) {
+    p->stream = true;
+    p->atomic = false;
+    p->vec = vec_ok ? 16 / es : 1;
+    const int64_t slice = (int64_t)kSliceLanes * kSliceVecs * p->vec;
+    p->nslice = (int)cdiv(cols, slice);
+    // about two blocks a CU in all; every group a run of whole rows
+    const int64_t want = std::max<int64_t>(1, cdiv(2 * (int64_t)(cu > 0 ? cu : 256), p->nslice));
+    p->groups = std::max<int64_t>(1, std::min<int64_t>(rows, want));
+    p->rpg = rows > 0 ? cdiv(rows, p->groups) : 0;
+    p->groups = rows > 0 ? cdiv(rows, p->rpg) : 1;
+    p->parts = p->groups;
+    p->grid = p->groups * p->nslice;
+    p->coef_off = ((size_t)p->parts * cols * sizeof(float) + 255) / 256 * 256;
+    p->total = p->coef_off + (size_t)std::max<int64_t>(rows, 1) * sizeof(float);
+    return true;
+  }
   const int64_t ncu = cu > 0 ? cu : 256;
   p->atomic = dw_mode == HK_DW_ATOMIC;
   // 1024-lane blocks of several row groups whose dW accumulators meet in LDS:
@@ -490,8 +660,7 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
   const int dev = current_device();
   if (dev < 0) return (int)hipErrorNoDevice;
   BwdPlan p;
-  HK_REQUIRE(plan_bwd(rows, cols, es, vec_ok, dw_mode, cu_count(dev), &p),
-             "cols=%lld exceeds the supported row length", (long long)cols);
+  plan_bwd(rows, cols, es, vec_ok, dw_mode, cu_count(dev), &p);
   HK_REQUIRE(workspace != nullptr && ws_bytes >= p.total, "workspace too small: need %zu bytes, got %zu", p.total,
              ws_bytes);
   HK_REQUIRE(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
@@ -502,6 +671,34 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
     using T = typename decltype(tx)::type;
     using W = typename decltype(tw)::type;
     using A = typename std::conditional<std::is_same<T, float>::value, double, float>::type;
+    if (p.stream) {
+      float* coef = (float*)((char*)workspace + p.coef_off);
+      if (rows > 0) {
+        auto launch = [&](auto vec_c) {
+          constexpr int VEC = decltype(vec_c)::value;
+          hipLaunchKernelGGL((rmsnorm_bwd_dot_kernel<T, W, VEC>), dim3((unsigned)rows), dim3(kStreamLanes), 0, st,
+                             coef, (const T*)dy, (const T*)x, (const W*)w, rstd, (int)cols, ld_dy, ld_x);
+          int rc = check_launch("rmsnorm_bwd_dot_kernel");
+          if (rc) return rc;
+          auto go = [&](auto hds_c) {
+            constexpr bool HDS = decltype(hds_c)::value;
+            hipLaunchKernelGGL((rmsnorm_bwd_cols_kernel<T, W, A, VEC, HDS>), dim3((unsigned)p.grid),
+                               dim3(kSliceLanes), 0, st, (T*)dx, (float*)part, (const T*)dy, (const T*)ds,
+                               (const T*)x, (const W*)w, rstd, coef, rows, (int)cols, ld_dy, ld_ds, ld_x, ld_dx,
+                               p.nslice, p.rpg);
+            return check_launch("rmsnorm_bwd_cols_kernel");
+          };
+          if (ds) return go(std::true_type{});
+          return go(std::false_type{});
+        };
+        const int rc = p.vec > 1 ? launch(std::integral_constant<int, 16 / sizeof(T)>{})
+                                 : launch(std::integral_constant<int, 1>{});
+        if (rc) return rc;
+      }
+      hipLaunchKernelGGL((reduce_partial_kernel<W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
+                         (const float*)part, rows > 0 ? p.parts : 0, (int)cols);
+      return check_launch("reduce_partial_kernel");
+    }
     if (p.atomic) {
       hipLaunchKernelGGL(fill_zero_f64, dim3((unsigned)cdiv(cols, 256)), dim3(256), 0, st, (double*)part, cols);
       int rc = check_launch("fill_zero_f64");

@@ -11,15 +11,18 @@
 // memory latency, not two.
 //
 // Backward saves only rstd (the forward's [rows] fp32 output) and recomputes
-// the normalised row. Each row group walks a run of R consecutive rows,
-// accumulating its dW contribution in registers: fp32 for 16-bit inputs, fp64
-// for fp32 inputs (a sum over thousands of rows in fp32 drifts by ~1e-4, more
-// than the 1e-5 fp32 tolerance allows). For 16-bit inputs a 1024-lane block
-// holds several groups (4 at H = 4096), one block a CU, and their accumulators
-// are summed in LDS in a fixed order; fp32 inputs run one group a block, two
-// blocks a CU. Each block's sum goes either into one fp32 partial row (a run
-// of rows rounds once), summed in fp64 by a separate pass, or into fp64
-// atomics on one [cols] accumulator. HK_DW_AUTO always takes the partial rows. The
+// the normalised row. Each of the G row groups walks rows g, g + G, g + 2G, ...
+// (so at any moment the whole GPU reads one contiguous window of G rows, as
+// the forward's one-row-a-block grid does; runs of consecutive rows per group
+// measured 10% slower at C2's bf16 [8192, 4096]), accumulating its dW
+// contribution in registers: fp32 for 16-bit inputs, fp64 for fp32 inputs (a
+// sum over thousands of rows in fp32 drifts by ~1e-4, more than the 1e-5 fp32
+// tolerance allows). For 16-bit inputs a 1024-lane block holds several groups
+// (4 at H = 4096), one block a CU, and their accumulators are summed in LDS in
+// a fixed order; fp32 inputs run one group a block, two blocks a CU. Each
+// block's sum goes either into one fp32 partial row (a group's rows round
+// once), summed in fp64 by a separate pass, or into fp64 atomics on one [cols]
+// accumulator. HK_DW_AUTO always takes the partial rows. The
 // reference switches to atomics when rows <= 8 * CU count (rms_norm.py:325-326);
 // here the groups' device-scope fp64 atomics on the one row measured 1.7-9x
 // slower than the partial rows at every size tried (16 to 4096 rows, H 1024 to
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(LB) void rmsnorm_fwd_kernel(
 }
 
 // ------------------------------------------------------------------------
-// backward: dx per row; dW accumulated per row group over R consecutive rows
+// backward: dx per row; dW accumulated per row group over rows g, g + G, ...
 // ------------------------------------------------------------------------
 template <typename T, typename W, typename A, int VEC, int NCH, bool HAS_DS, int LB>
 __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
   const int lr = (wave % wpr) * kWave + lane;
   const int gl = wpr * kWave;
   const int64_t group = (int64_t)blockIdx.x * rpb + rib;
-  const int64_t row0 = group * rows_per_group;
+  const int64_t ngroups = (int64_t)gridDim.x * rpb;
   const float inv_n = 1.f / (float)cols;
   Pack<W, VEC> wv[NCH];
   A acc[NCH][VEC];
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
   // The trip count is uniform over the block so every thread meets the barriers.
 #pragma unroll 1
   for (int64_t t = 0; t < rows_per_group; ++t) {
-    const int64_t row = row0 + t;
+    const int64_t row = group + t * ngroups;
     const bool valid = row < rows;
     const int64_t rr = valid ? row : rows - 1;  // loads stay unconditional
     const float rs = rstd[rr];
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
           if (atomic) {
-            if (row0 < rows) unsafeAtomicAdd(static_cast<double*>(dw_ws) + col + i, (double)acc[j][i]);
+            if (group < rows) unsafeAtomicAdd(static_cast<double*>(dw_ws) + col + i, (double)acc[j][i]);
           } else {
             static_cast<float*>(dw_ws)[group * cols + col + i] = (float)acc[j][i];
           }
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(LB) void rmsnorm_bwd_kernel(
     }
     __syncthreads();
   }
-  const bool any_row = (int64_t)blockIdx.x * rpb * rows_per_group < rows;
+  const bool any_row = (int64_t)blockIdx.x * rpb < rows;
   for (int c = threadIdx.x; c < cols; c += blockDim.x) {
     if (atomic) {
       if (any_row) unsafeAtomicAdd(static_cast<double*>(dw_ws) + c, (double)buf[c]);
@@ -607,16 +610,18 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   const int64_t ncu = cu > 0 ? cu : 256;
   p->atomic = dw_mode == HK_DW_ATOMIC;
   // 1024-lane blocks of several row groups whose dW accumulators meet in LDS:
-  // the partial rows (the dW pass's traffic) are one per block, not one per group
+  // the partial rows (the dW pass's traffic) are one per block, not one per
+  // group, and a CU holds 16 waves (256-lane single-group blocks, two a CU,
+  // measured up to 1.5x slower below 4096 rows and within 5% above, with dS or
+  // without). fp32 inputs keep one group a block: their fp64 accumulators make
+  // the 1024-lane form spill, and C1 measured 4% slower with it.
   const size_t acc_bytes = es == 4 ? sizeof(double) : sizeof(float);
   const int rpb = std::max(1, 1024 / (p->g.wpr * kWave));
-  // (fp32 inputs keep one group a block: their fp64 accumulators make the
-  // 1024-lane form spill, and C1 measured 4% slower with it)
   const bool combine = rpb > 1 && es != 4 && (size_t)cols * acc_bytes <= kBwdLdsMax;
   p->block = (combine ? rpb : 1) * p->g.wpr * kWave;  // without the LDS sum: one group a block
   p->rpb = p->block / (p->g.wpr * kWave);
   p->lds = combine ? (size_t)cols * acc_bytes : 0;
-  // Long runs of rows keep the partial rows few. One 1024-lane block a CU (the
+  // Many rows a group keep the partial rows few. One 1024-lane block a CU (the
   // 16-bit H = 4096 form needs ~100 VGPRs, so a second would not be resident);
   // without the LDS sum, two blocks of one group each.
   const int64_t blocks = (combine ? 1 : 2) * ncu;
@@ -625,7 +630,7 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   p->rpg = rows > 0 ? cdiv(rows, p->groups) : 0;
   p->groups = rows > 0 ? cdiv(rows, p->rpg) : 1;
   p->grid = cdiv(p->groups, (int64_t)p->rpb);
-  p->groups = p->grid * p->rpb;  // every launched group has a (possibly empty) run of rows
+  p->groups = p->grid * p->rpb;  // every launched group walks rpg rows (past the end: masked)
   p->parts = p->rpb > 1 ? p->grid : p->groups;
   p->total = p->atomic ? (size_t)cols * 8 : (size_t)p->parts * cols * sizeof(float);
   return true;

@@ -8,8 +8,14 @@
 //
 // 256 lanes per token. Each lane owns P 16-byte packs of the D columns. The
 // N per-block sums of a pass (sum of squares, then the scores; in the
-// backward <dh, v_i>, then <dk_i, v_i>) are reduced together: one wave
-// butterfly per value and one LDS exchange for all N.
+// backward <dh, v_i>, then <dk_i, v_i>) are reduced together and exchanged
+// through LDS once for all N: the streaming forms with one wave butterfly per
+// value, the register-resident forms with one transposed butterfly for all N.
+// For 16-bit inputs the sums whose both factors are 16-bit (v_i . v_i,
+// w_query . k_i, dh . v_i) use the hardware two-element dot product. With
+// per-element unpacking and fmas the forward issued 18 VALU instructions per
+// element at N = 8 and was bound by them (146 us at [8, 4, 2048, 4096] bf16);
+// at about 10 it runs within 6% of a copy kernel of its own access order.
 //
 // When a token's N rows fit in registers (N <= 8 and D <= 512*VEC, or
 // N <= 16 and D <= 256*VEC; VEC = 8 for bf16/fp16, 4 for fp32) the register-resident
@@ -19,9 +25,10 @@
 // N*D*es bytes stay in L2 between passes).
 //
 // In the backward each workgroup walks a run of tokens and keeps its
-// dW_query / dW_norm partials in registers (P*VEC columns per lane), writes
-// one fp32 partial row per workgroup, and a column reduction adds the rows in
-// fp64 (the reference uses fp32 atomics per token, attn_res.py:189-190).
+// dW_query / dW_norm partials in registers (P*VEC columns per lane; the
+// resident form keeps their common factor only), writes one fp32 partial row
+// pair per workgroup, and a column reduction adds the rows in fp64 (the
+// reference uses fp32 atomics per token, attn_res.py:189-190).
 #include "hk_common.h"
 #include "../../include/hilda_kernel_amd.h"
 
@@ -53,6 +60,36 @@ struct BlockSumsT {
     part = wave_sum(part);
     if ((threadIdx.x & (kWave - 1)) == 0) red[(threadIdx.x / kWave) * kMaxBlocks + i] = part;
   }
+  // add(i, v[i]) for every i < NB at once (NB a power of two): a transposed
+  // butterfly keeps, at the exchange with lane ^ 32, half of the values (the
+  // lane's half of the rows, plus the partner's copy of them), then half of
+  // those at lane ^ 16, and so on; after log2(NB) such steps v[0] holds the sum
+  // of row lane / (64 / NB) over the lanes differing in the top bits, and plain
+  // exchanges over the low bits finish it. NB - 1 + 6 - log2(NB) shuffles in
+  // all (10 for 8 rows) where NB separate wave sums take 6 NB.
+  template <int NB>
+  __device__ __forceinline__ void add_all(float (&v)[NB]) const {
+    static_assert(NB >= 1 && NB <= kWave && (NB & (NB - 1)) == 0, "NB must be a power of two <= 64");
+    const int lane = threadIdx.x & (kWave - 1);
+    int o = kWave / 2;
+#pragma unroll
+    for (int h = NB / 2; h >= 1; h /= 2, o /= 2) {
+      // all ones in the upper lanes of each pair of halves; a bitwise blend,
+      // as a select on the array would become indexing by a lane value
+      const uint32_t up = (lane & o) ? 0xffffffffu : 0u;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const uint32_t lo = f32_bits(v[i]), hi = f32_bits(v[i + h]);
+        const float keep = bits_f32((hi & up) | (lo & ~up));
+        const float give = bits_f32((lo & up) | (hi & ~up));
+        v[i] = keep + __shfl_xor(give, o, kWave);
+      }
+    }
+#pragma unroll
+    for (; o >= 1; o /= 2) v[0] += __shfl_xor(v[0], o, kWave);
+    constexpr int kSpan = kWave / NB;  // lanes that hold one row's sum
+    if (lane % kSpan == 0) red[(threadIdx.x / kWave) * kMaxBlocks + lane / kSpan] = v[0];
+  }
   __device__ __forceinline__ void finish(int n, float* out) const {
     __syncthreads();
     if ((int)threadIdx.x < n) {
@@ -65,6 +102,60 @@ struct BlockSumsT {
   }
 };
 using BlockSums = BlockSumsT<kNW>;
+
+// Two 16-bit elements (the low and high halves of a word) at once: the
+// hardware two-element dot product into fp32 (the products of 16-bit values
+// are exact in fp32).
+template <typename T>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (std::is_same<T, __bf16>::value) {
+    typedef __bf16 T2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(T2, a), __builtin_bit_cast(T2, b), c, false);
+  } else {
+    typedef _Float16 T2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(T2, a), __builtin_bit_cast(T2, b), c, false);
+  }
+}
+
+// acc + sum of the squares of a pack's elements
+template <typename T, int VEC>
+__device__ __forceinline__ float sumsq_pack(const Pack<T, VEC>& x, float acc) {
+  if constexpr (sizeof(T) == 2 && VEC % 2 == 0) {
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) acc = dot2<T>(x.w[k], x.w[k], acc);
+  } else {
+    float f[VEC];
+    unpack(x, f);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc = fmaf(f[e], f[e], acc);
+  }
+  return acc;
+}
+
+// acc + <w_query, round(round(x * r) * w_norm)> over a pack (attn_res.py:70-73),
+// w_norm already widened to fp32
+template <typename T, int VEC>
+__device__ __forceinline__ float score_pack(const Pack<T, VEC>& x, float r, const float (&wn)[VEC],
+                                            const Pack<T, VEC>& q, float acc) {
+  float f[VEC];
+  unpack(x, f);
+  if constexpr (sizeof(T) == 2 && VEC % 2 == 0) {
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) {
+      Pack<T, 2> k1;
+      k1.w[0] = pack2<T>(f[2 * k] * r, f[2 * k + 1] * r);
+      float g[2];
+      unpack(k1, g);
+      acc = dot2<T>(pack2<T>(g[0] * wn[2 * k], g[1] * wn[2 * k + 1]), q.w[k], acc);
+    }
+  } else {
+    float qf[VEC];
+    unpack(q, qf);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc = fmaf(qf[e], round_through<T>(round_through<T>(f[e] * r) * wn[e]), acc);
+  }
+  return acc;
+}
 
 template <typename T, int VEC>
 __global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
@@ -90,14 +181,8 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, 
         for (int u = 0; u < kU; ++u)
           if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-          if (i0 + u < N) {
-            float x[VEC];
-            unpack(pv[u], x);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) part[u] = fmaf(x[e], x[e], part[u]);
-          }
-        }
+        for (int u = 0; u < kU; ++u)
+          if (i0 + u < N) part[u] = sumsq_pack(pv[u], part[u]);
       }
     }
 #pragma unroll
@@ -122,19 +207,12 @@ __global__ __launch_bounds__(kNT) void attn_res_fwd_kernel(T* __restrict__ out, 
 #pragma unroll
         for (int u = 0; u < kU; ++u)
           if (i0 + u < N) pv[u] = load_pack<T, VEC>(v0 + (i0 + u) * bstride + c);
-        float q[VEC], w[VEC];
-        unpack(load_pack<T, VEC>(wq + c), q);
+        const Pack<T, VEC> q = load_pack<T, VEC>(wq + c);
+        float w[VEC];
         unpack(load_pack<T, VEC>(wn + c), w);
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-          if (i0 + u < N) {
-            float x[VEC];
-            unpack(pv[u], x);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e)
-              part[u] = fmaf(q[e], round_through<T>(round_through<T>(x[e] * r[u]) * w[e]), part[u]);
-          }
-        }
+        for (int u = 0; u < kU; ++u)
+          if (i0 + u < N) part[u] = score_pack(pv[u], r[u], w, q, part[u]);
       }
     }
 #pragma unroll
@@ -335,7 +413,8 @@ __global__ __launch_bounds__(kNT) void attn_res_bwd_kernel(T* __restrict__ dV, f
 
 // Register-resident forms, used when a token's N rows fit in NB*P packs per
 // lane (64 VGPRs at most): V is read once per direction, the passes work on
-// the registers. Same arithmetic, in the same order, as the streaming forms.
+// the registers. The per-element arithmetic is the streaming forms'; the
+// cross-lane sums run in another order (all N blocks in one butterfly).
 template <typename T, int VEC, int NB, int P, int NT>
 __global__ __launch_bounds__(NT) void attn_res_fwd_res_kernel(T* __restrict__ out, float* __restrict__ alpha_out,
                                                                float* __restrict__ rstd_out, const T* __restrict__ V,
@@ -363,45 +442,36 @@ __global__ __launch_bounds__(NT) void attn_res_fwd_res_kernel(T* __restrict__ ou
 #pragma unroll
     for (int j = 0; j < P; ++j)
       if (i < N && col_of<VEC, NT>(j) < D) pv[i][j] = load_pack<T, VEC>(v0 + i * bstride + col_of<VEC, NT>(j));
+  float part[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
+    float acc = 0.f;
     if (i < N) {
-      float part = 0.f;
 #pragma unroll
-      for (int j = 0; j < P; ++j) {
-        if (col_of<VEC, NT>(j) < D) {
-          float x[VEC];
-          unpack(pv[i][j], x);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) part = fmaf(x[e], x[e], part);
-        }
-      }
-      bs.add(i, part);
+      for (int j = 0; j < P; ++j)
+        if (col_of<VEC, NT>(j) < D) acc = sumsq_pack(pv[i][j], acc);
     }
+    part[i] = acc;
   }
+  bs.add_all(part);
   bs.finish(N, rs);
   if ((int)threadIdx.x < N) rs[threadIdx.x] = rsqrtf(rs[threadIdx.x] / (float)D + eps);
   __syncthreads();
+  float wf[P][VEC];  // w_norm widened once for every block
+#pragma unroll
+  for (int j = 0; j < P; ++j) unpack(wv[j], wf[j]);
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
+    float acc = 0.f;
     if (i < N) {
       const float r = rs[i];
-      float part = 0.f;
 #pragma unroll
-      for (int j = 0; j < P; ++j) {
-        if (col_of<VEC, NT>(j) < D) {
-          float x[VEC], q[VEC], w[VEC];
-          unpack(pv[i][j], x);
-          unpack(qv[j], q);
-          unpack(wv[j], w);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e)
-            part = fmaf(q[e], round_through<T>(round_through<T>(x[e] * r) * w[e]), part);
-        }
-      }
-      bs.add(i, part);
+      for (int j = 0; j < P; ++j)
+        if (col_of<VEC, NT>(j) < D) acc = score_pack(pv[i][j], r, wf[j], qv[j], acc);
     }
+    part[i] = acc;
   }
+  bs.add_all(part);
   bs.finish(N, al);
   float m = -INFINITY;
   for (int i = 0; i < N; ++i) m = fmaxf(m, al[i]);
@@ -438,6 +508,28 @@ __global__ __launch_bounds__(NT) void attn_res_fwd_res_kernel(T* __restrict__ ou
   }
 }
 
+// acc + <a, b> over two packs
+template <typename T, int VEC>
+__device__ __forceinline__ float dot_pack(const Pack<T, VEC>& a, const Pack<T, VEC>& b, float acc) {
+  if constexpr (sizeof(T) == 2 && VEC % 2 == 0) {
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) acc = dot2<T>(a.w[k], b.w[k], acc);
+  } else {
+    float x[VEC], y[VEC];
+    unpack(a, x);
+    unpack(b, y);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc = fmaf(x[e], y[e], acc);
+  }
+  return acc;
+}
+
+// The two weight gradients share one factor (attn_res.py:181-187):
+//   dW_query += ds_i * (v_i * rstd_i) * w_norm,  dW_norm += ds_i * w_query * (v_i * rstd_i)
+// so each lane accumulates S = sum over its tokens and blocks of ds_i * rstd_i * v_i
+// and the workgroup's partial rows are S * w_norm and S * w_query. dk_i =
+// ds_i * w_query * w_norm enters dV and <dk_i, v_i> through the per-lane
+// product w_query * w_norm, formed once.
 template <typename T, int VEC, int NB, int P, int NT>
 __global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV, float* __restrict__ part,
                                                                const T* __restrict__ dh, const T* __restrict__ V,
@@ -449,15 +541,19 @@ __global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV
   __shared__ float da[kMaxBlocks], kv[kMaxBlocks], ds[kMaxBlocks], al[kMaxBlocks], rs[kMaxBlocks];
   const BlockSumsT<NT / kWave> bs{red};
   const int64_t bstride = ntok * D;
-  Pack<T, VEC> qv[P], wv[P];
-  float dwq[P][VEC], dwn[P][VEC];
+  const float inv_d = 1.0f / (float)D;
+  float qw[P][VEC], S[P][VEC];
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) dwq[j][e] = dwn[j][e] = 0.f;
     const int64_t c = col_of<VEC, NT>(j) < D ? col_of<VEC, NT>(j) : 0;
-    qv[j] = load_pack<T, VEC>(wq + c);
-    wv[j] = load_pack<T, VEC>(wn + c);
+    float q[VEC], w[VEC];
+    unpack(load_pack<T, VEC>(wq + c), q);
+    unpack(load_pack<T, VEC>(wn + c), w);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      qw[j][e] = q[e] * w[e];
+      S[j][e] = 0.f;
+    }
   }
   const int64_t t0 = (int64_t)blockIdx.x * tpb, t1 = min(t0 + tpb, ntok);
   // the token's rows live in pv/gv; the next token's are loaded into them as the
@@ -478,29 +574,25 @@ __global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV
         if (i < N) load_token(t0, i, j);
     }
   }
+  float sums[NB];
   for (int64_t tok = t0; tok < t1; ++tok) {
     const int64_t nxt = tok + 1 < t1 ? tok + 1 : tok;
     if ((int)threadIdx.x < N) {
       al[threadIdx.x] = alpha[threadIdx.x * ntok + tok];
       rs[threadIdx.x] = rstd[threadIdx.x * ntok + tok];
     }
+    // d_alpha_i = <dh, v_i>
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
+      float acc = 0.f;
       if (i < N) {
-        float p = 0.f;
 #pragma unroll
-        for (int j = 0; j < P; ++j) {
-          if (col_of<VEC, NT>(j) < D) {
-            float x[VEC], y[VEC];
-            unpack(pv[i][j], x);
-            unpack(gv[j], y);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) p = fmaf(x[e], y[e], p);
-          }
-        }
-        bs.add(i, p);  // d_alpha_i = <dh, v_i>
+        for (int j = 0; j < P; ++j)
+          if (col_of<VEC, NT>(j) < D) acc = dot_pack(pv[i][j], gv[j], acc);
       }
+      sums[i] = acc;
     }
+    bs.add_all(sums);
     bs.finish(N, da);
     if ((int)threadIdx.x < N) {
       float sa = 0.f;
@@ -508,47 +600,44 @@ __global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV
       ds[threadIdx.x] = al[threadIdx.x] * (da[threadIdx.x] - sa);
     }
     __syncthreads();
+    // <dk_i, v_i> = ds_i <w_query * w_norm, v_i>
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
+      float acc = 0.f;
       if (i < N) {
-        float pk = 0.f;
 #pragma unroll
         for (int j = 0; j < P; ++j) {
           if (col_of<VEC, NT>(j) < D) {
-            float x[VEC], q[VEC], w[VEC];
+            float x[VEC];
             unpack(pv[i][j], x);
-            unpack(qv[j], q);
-            unpack(wv[j], w);
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) pk = fmaf(q[e] * w[e], x[e], pk);
+            for (int e = 0; e < VEC; ++e) acc = fmaf(qw[j][e], x[e], acc);
           }
         }
-        bs.add(i, pk * ds[i]);
+        acc *= ds[i];
       }
+      sums[i] = acc;
     }
+    bs.add_all(sums);
     bs.finish(N, kv);
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       const int64_t c = col_of<VEC, NT>(j);
-      float y[VEC], q[VEC], w[VEC];
+      float y[VEC];
       unpack(gv[j], y);
-      unpack(qv[j], q);
-      unpack(wv[j], w);
       load_token(nxt, -1, j);
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
         if (i < N) {
-          const float a = al[i], d = ds[i], r = rs[i];
-          const float coef = r * r * r * (kv[i] / (float)D);
+          const float a = al[i], r = rs[i], dr = ds[i] * r;
+          const float coef = r * r * r * (kv[i] * inv_d);  // rstd_i^3 <dk_i, v_i> / D
           float x[VEC];
           unpack(pv[i][j], x);
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
-            const float dk = d * q[e] * w[e];
-            const float vn = x[e] * r;
-            dwq[j][e] = fmaf(d, vn * w[e], dwq[j][e]);
-            dwn[j][e] = fmaf(d * q[e], vn, dwn[j][e]);
-            x[e] = a * y[e] + r * dk - coef * x[e];
+            S[j][e] = fmaf(dr, x[e], S[j][e]);
+            // alpha_i dh + rstd_i dk_i - rstd_i^3 <dk_i, v_i> / D v_i
+            x[e] = fmaf(a, y[e], fmaf(dr, qw[j][e], -coef * x[e]));
           }
           if (c < D) store_pack<T, VEC>(dV + i * bstride + tok * D + c, pack<T, VEC>(x));
           load_token(nxt, i, j);
@@ -562,10 +651,13 @@ __global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV
   for (int j = 0; j < P; ++j) {
     const int64_t c = col_of<VEC, NT>(j);
     if (c < D) {
+      float q[VEC], w[VEC];
+      unpack(load_pack<T, VEC>(wq + c), q);
+      unpack(load_pack<T, VEC>(wn + c), w);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        pq[c + e] = dwq[j][e];
-        pq[D + c + e] = dwn[j][e];
+        pq[c + e] = S[j][e] * w[e];
+        pq[D + c + e] = S[j][e] * q[e];
       }
     }
   }

@@ -145,6 +145,16 @@ __device__ __forceinline__ void unpack(const Pack<T, VEC>& r, float (&out)[VEC])
   }
 }
 
+// Two fp32 values rounded to a 16-bit T (nearest even), lo in the low half of
+// the word: one two-operand convert (v_cvt_pk_bf16_f32 for bf16) rather than
+// two converts and a merge.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  typedef float F2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){lo, hi}, T2));
+}
+
 template <typename T, int VEC>
 __device__ __forceinline__ Pack<T, VEC> pack(const float (&in)[VEC]) {
   Pack<T, VEC> r;
@@ -155,11 +165,7 @@ __device__ __forceinline__ Pack<T, VEC> pack(const float (&in)[VEC]) {
     r.h = __builtin_bit_cast(uint16_t, from_f32<T>(in[0]));
   } else {
 #pragma unroll
-    for (int k = 0; k < VEC / 2; ++k) {
-      const uint32_t lo = __builtin_bit_cast(uint16_t, from_f32<T>(in[2 * k]));
-      const uint32_t hi = __builtin_bit_cast(uint16_t, from_f32<T>(in[2 * k + 1]));
-      r.w[k] = lo | (hi << 16);
-    }
+    for (int k = 0; k < VEC / 2; ++k) r.w[k] = pack2<T>(in[2 * k], in[2 * k + 1]);
   }
   return r;
 }

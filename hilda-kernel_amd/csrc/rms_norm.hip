@@ -19,7 +19,7 @@
 // sum over thousands of rows in fp32 drifts by ~1e-4, more than the 1e-5 fp32
 // tolerance allows). For 16-bit inputs a 1024-lane block holds several groups
 // (4 at H = 4096), one block a CU, and their accumulators are summed in LDS in
-// a fixed order; fp32 inputs run one group a block, two blocks a CU. Each
+// a fixed order; fp32 inputs run up to 512 lanes a block, two blocks a CU. Each
 // block's sum goes either into one fp32 partial row (a group's rows round
 // once), summed in fp64 by a separate pass, or into fp64 atomics on one [cols]
 // accumulator. HK_DW_AUTO always takes the partial rows. The
@@ -498,6 +498,12 @@ int dispatch_lb(int block, F&& f) {
   if (block <= 256) return f(std::integral_constant<int, 256>{});
   return f(std::integral_constant<int, 1024>{});
 }
+template <typename F>
+int dispatch_lb_bwd(int block, F&& f) {
+  if (block <= 256) return f(std::integral_constant<int, 256>{});
+  if (block <= 512) return f(std::integral_constant<int, 512>{});
+  return f(std::integral_constant<int, 1024>{});
+}
 
 int fwd_impl(void* y, void* s, float* rstd, const void* x, const void* r, const void* w, int64_t rows,
              int64_t cols, int64_t ld_x, int64_t ld_r, int64_t ld_y, int64_t ld_s, int dt_x, int dt_w, float eps,
@@ -613,18 +619,21 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   // the partial rows (the dW pass's traffic) are one per block, not one per
   // group, and a CU holds 16 waves (256-lane single-group blocks, two a CU,
   // measured up to 1.5x slower below 4096 rows and within 5% above, with dS or
-  // without). fp32 inputs keep one group a block: their fp64 accumulators make
-  // the 1024-lane form spill, and C1 measured 4% slower with it.
+  // without). fp32 inputs: their fp64 accumulators make the 1024-lane form
+  // spill, so groups of 64 or 128 lanes (H <= 2048) share 512-lane blocks, two
+  // a CU (1.1-2x faster than a group a block); 256-lane groups run alone (two
+  // groups a 512-lane block measured 3-6% slower at H = 4096, C1 among them).
   const size_t acc_bytes = es == 4 ? sizeof(double) : sizeof(float);
-  const int rpb = std::max(1, 1024 / (p->g.wpr * kWave));
-  const bool combine = rpb > 1 && es != 4 && (size_t)cols * acc_bytes <= kBwdLdsMax;
+  const int rpb = es == 4 ? (p->g.wpr <= 2 ? 512 / (p->g.wpr * kWave) : 1)
+                          : std::max(1, 1024 / (p->g.wpr * kWave));
+  const bool combine = rpb > 1 && (size_t)cols * acc_bytes <= kBwdLdsMax;
   p->block = (combine ? rpb : 1) * p->g.wpr * kWave;  // without the LDS sum: one group a block
   p->rpb = p->block / (p->g.wpr * kWave);
   p->lds = combine ? (size_t)cols * acc_bytes : 0;
   // Many rows a group keep the partial rows few. One 1024-lane block a CU (the
   // 16-bit H = 4096 form needs ~100 VGPRs, so a second would not be resident);
-  // without the LDS sum, two blocks of one group each.
-  const int64_t blocks = (combine ? 1 : 2) * ncu;
+  // two of 512 lanes or fewer.
+  const int64_t blocks = (combine && p->block == 1024 ? 1 : 2) * ncu;
   const int64_t target = blocks * p->rpb;
   p->groups = std::max<int64_t>(1, std::min<int64_t>(rows, target));
   p->rpg = rows > 0 ? cdiv(rows, p->groups) : 0;
@@ -712,7 +721,7 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
     if (rows > 0) {
       int rc = dispatch_nch(p.g.nch, [&](auto nch_c) {
         constexpr int NCH = decltype(nch_c)::value;
-        return dispatch_lb(p.block, [&](auto lb_c) {
+        return dispatch_lb_bwd(p.block, [&](auto lb_c) {
           constexpr int LB = decltype(lb_c)::value;
           auto launch = [&](auto vec_c) {
             constexpr int VEC = decltype(vec_c)::value;

@@ -224,17 +224,46 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// wave64 reductions (butterfly over all 64 lanes; every lane gets the result)
+// wave64 reductions on DPP lane moves (no LDS round trips): within each quad
+// (lane ^ 1, lane ^ 2), then the half-row and row mirrors, then lane 15 of
+// rows 0 and 2 into rows 1 and 3 and lane 31 into rows 2 and 3, which leaves
+// the total in lane 63; every lane receives it through a readlane.
 // ---------------------------------------------------------------------------
+namespace dpp {
+constexpr int kXor1 = 0xb1;        // quad_perm [1, 0, 3, 2]
+constexpr int kXor2 = 0x4e;        // quad_perm [2, 3, 0, 1]
+constexpr int kHalfMirror = 0x141; // row_half_mirror
+constexpr int kMirror = 0x140;     // row_mirror
+constexpr int kBcast15 = 0x142;    // row_bcast:15
+constexpr int kBcast31 = 0x143;    // row_bcast:31
+}  // namespace dpp
+
+// lane value moved by the DPP pattern CTRL; rows outside ROW_MASK receive `old`
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float lane63(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  v += dpp_move<dpp::kXor1>(0.f, v);
+  v += dpp_move<dpp::kXor2>(0.f, v);
+  v += dpp_move<dpp::kHalfMirror>(0.f, v);
+  v += dpp_move<dpp::kMirror>(0.f, v);
+  v += dpp_move<dpp::kBcast15, 0xa>(0.f, v);
+  v += dpp_move<dpp::kBcast31, 0xc>(0.f, v);
+  return lane63(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  v = fmaxf(v, dpp_move<dpp::kXor1>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kXor2>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kHalfMirror>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kMirror>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kBcast15, 0xa>(v, v));
+  v = fmaxf(v, dpp_move<dpp::kBcast31, 0xc>(v, v));
+  return lane63(v);
 }
 
 // Sum over the NW waves of a block; `red` must hold NW floats of LDS.

@@ -30,6 +30,7 @@
 // pair per workgroup, and a column reduction adds the rows in fp64 (the
 // reference uses fp32 atomics per token, attn_res.py:189-190).
 #include "hk_common.h"
+#include "colsum.h"
 #include "../../include/hilda_kernel_amd.h"
 
 #include <algorithm>
@@ -663,37 +664,6 @@ __global__ __launch_bounds__(NT) void attn_res_bwd_res_kernel(T* __restrict__ dV
   }
 }
 
-// out_q[c] = sum_g part[g][0][c], out_n[c] = sum_g part[g][1][c] (fp64 sums)
-template <typename W>
-__global__ __launch_bounds__(1024) void attn_res_reduce_kernel(W* __restrict__ out_q, W* __restrict__ out_n,
-                                                               const float* __restrict__ part, int64_t groups,
-                                                               int64_t D) {
-  __shared__ double red[16][65];
-  const int c = threadIdx.x % 64, s = threadIdx.x / 64;
-  const int64_t col = (int64_t)blockIdx.x * 64 + c;  // in [0, 2D)
-  double t0 = 0.0, t1 = 0.0, t2 = 0.0, t3 = 0.0;
-  if (col < 2 * D) {
-    const float* pc = part + (col / D) * D + col % D;
-    int64_t g = s;
-    for (; g + 48 < groups; g += 64) {  // four independent chains
-      t0 += pc[g * 2 * D];
-      t1 += pc[(g + 16) * 2 * D];
-      t2 += pc[(g + 32) * 2 * D];
-      t3 += pc[(g + 48) * 2 * D];
-    }
-    for (; g < groups; g += 16) t0 += pc[g * 2 * D];
-  }
-  red[s][c] = (t0 + t1) + (t2 + t3);
-  __syncthreads();
-  if (s == 0 && col < 2 * D) {
-    double u = 0.0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) u += red[i][c];
-    if (col < D) out_q[col] = from_f32<W>((float)u);
-    else out_n[col - D] = from_f32<W>((float)u);
-  }
-}
-
 template <typename T> struct Tag { using type = T; };
 
 template <typename F>
@@ -837,9 +807,9 @@ int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, con
       }
       if (rc) return rc;
     }
-    hipLaunchKernelGGL((attn_res_reduce_kernel<T>), dim3((unsigned)cdiv(2 * D, 64)), dim3(1024), 0, st,
-                       (T*)dw_query, (T*)dw_norm, (const float*)part, used, D);
-    return check_launch("attn_res_reduce_kernel");
+    // partial row pairs [query | norm] of 2D columns
+    colsum_launch<T>((T*)dw_query, (T*)dw_norm, (const float*)part, used, 2 * D, 2 * D, D, st);
+    return check_launch("colsum_kernel");
   });
 }
 

@@ -28,6 +28,7 @@
 // slower than the partial rows at every size tried (16 to 4096 rows, H 1024 to
 // 8192), so atomics run only when HK_DW_ATOMIC asks for them.
 #include "hk_common.h"
+#include "colsum.h"
 #include "../../include/hilda_kernel_amd.h"
 
 #include <algorithm>
@@ -393,38 +394,6 @@ __global__ __launch_bounds__(256) void cast_f64_kernel(W* __restrict__ out, cons
     out[i] = from_f32<W>((float)in[i]);
 }
 
-// out[c] = sum_g part[g*cols + c] in fp64: a block of 64 columns x 16 group
-// slices, four independent partial sums per thread so its loads overlap. (A two-level
-// variant with an arrival ticket needs a device-scope fence per block, which
-// writes back the XCD's L2 and was an order of magnitude slower.)
-template <typename W>
-__global__ __launch_bounds__(1024) void reduce_partial_kernel(W* __restrict__ out, const float* __restrict__ part,
-                                                              int64_t groups, int cols) {
-  using A = double;
-  __shared__ A red[16][65];
-  const int c = threadIdx.x % 64, s = threadIdx.x / 64;
-  const int col = blockIdx.x * 64 + c;
-  A t0 = A(0), t1 = A(0), t2 = A(0), t3 = A(0);
-  if (col < cols) {
-    int64_t g = s;
-    for (; g + 48 < groups; g += 64) {
-      t0 += part[g * cols + col];
-      t1 += part[(g + 16) * cols + col];
-      t2 += part[(g + 32) * cols + col];
-      t3 += part[(g + 48) * cols + col];
-    }
-    for (; g < groups; g += 16) t0 += part[g * cols + col];
-  }
-  red[s][c] = (t0 + t1) + (t2 + t3);
-  __syncthreads();
-  if (s == 0 && col < cols) {
-    A u = A(0);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) u += red[i][c];
-    out[col] = from_f32<W>((float)u);
-  }
-}
-
 // ------------------------------------------------------------------------
 // host dispatch
 // ------------------------------------------------------------------------
@@ -709,9 +678,8 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
                                  : launch(std::integral_constant<int, 1>{});
         if (rc) return rc;
       }
-      hipLaunchKernelGGL((reduce_partial_kernel<W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
-                         (const float*)part, rows > 0 ? p.parts : 0, (int)cols);
-      return check_launch("reduce_partial_kernel");
+      colsum_launch<W>((W*)dw, nullptr, (const float*)part, rows > 0 ? p.parts : 0, cols, cols, cols, st);
+      return check_launch("colsum_kernel");
     }
     if (p.atomic) {
       hipLaunchKernelGGL(fill_zero_f64, dim3((unsigned)cdiv(cols, 256)), dim3(256), 0, st, (double*)part, cols);
@@ -748,9 +716,8 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
       return check_launch("cast_f64_kernel");
     }
     // (no rows: zero groups are summed and dW comes out zero)
-    hipLaunchKernelGGL((reduce_partial_kernel<W>), dim3((unsigned)cdiv(cols, 64)), dim3(1024), 0, st, (W*)dw,
-                       (const float*)part, rows > 0 ? p.parts : 0, (int)cols);
-    return check_launch("reduce_partial_kernel");
+    colsum_launch<W>((W*)dw, nullptr, (const float*)part, rows > 0 ? p.parts : 0, cols, cols, cols, st);
+    return check_launch("colsum_kernel");
   });
 }
 

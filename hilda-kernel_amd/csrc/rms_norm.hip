@@ -564,7 +564,7 @@ struct BwdPlan {
 
 constexpr size_t kBwdLdsMax = 32 * 1024;
 
-bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int cu, BwdPlan* p) {
+bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int cu, BwdPlan* p, bool has_ds) {
   if (!choose_geom(cols, es, vec_ok, &p->g)) {
     p->stream = true;
     p->atomic = false;
@@ -592,9 +592,13 @@ bool plan_bwd(int64_t rows, int64_t cols, int es, bool vec_ok, int dw_mode, int 
   // spill, so groups of 64 or 128 lanes (H <= 2048) share 512-lane blocks, two
   // a CU (1.1-2x faster than a group a block); 256-lane groups run alone (two
   // groups a 512-lane block measured 3-6% slower at H = 4096, C1 among them).
+  // The fused-add backward (a third input row, dS) of 256-lane 16-bit groups
+  // at 32 rows a CU or more runs one group a block too: 1-3% faster there
+  // (C2's [8192, 4096]: 46.4 -> 44.3 us), slower with 512-lane groups.
   const size_t acc_bytes = es == 4 ? sizeof(double) : sizeof(float);
+  const bool alone = has_ds && p->g.wpr == 4 && rows >= 32 * ncu;
   const int rpb = es == 4 ? (p->g.wpr <= 2 ? 512 / (p->g.wpr * kWave) : 1)
-                          : std::max(1, 1024 / (p->g.wpr * kWave));
+                          : (alone ? 1 : std::max(1, 1024 / (p->g.wpr * kWave)));
   const bool combine = rpb > 1 && (size_t)cols * acc_bytes <= kBwdLdsMax;
   p->block = (combine ? rpb : 1) * p->g.wpr * kWave;  // without the LDS sum: one group a block
   p->rpb = p->block / (p->g.wpr * kWave);
@@ -643,7 +647,7 @@ int bwd_impl(void* dx, void* dw, const void* dy, const void* ds, const void* x, 
   const int dev = current_device();
   if (dev < 0) return (int)hipErrorNoDevice;
   BwdPlan p;
-  plan_bwd(rows, cols, es, vec_ok, dw_mode, cu_count(dev), &p);
+  plan_bwd(rows, cols, es, vec_ok, dw_mode, cu_count(dev), &p, ds != nullptr);
   HK_REQUIRE(workspace != nullptr && ws_bytes >= p.total, "workspace too small: need %zu bytes, got %zu", p.total,
              ws_bytes);
   HK_REQUIRE(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
@@ -779,11 +783,13 @@ size_t hk_rms_norm_bwd_workspace_size(int64_t rows, int64_t cols, int dtype_x, i
   (void)dtype_w;
   if (rows < 0 || cols <= 0 || !valid_dtype(dtype_x)) return 0;
   BwdPlan p;
-  // The vector width only changes the geometry, so plan with full vectors
-  // and with scalars and take the larger.
+  // The vector width and the dS input only change the geometry, so plan every
+  // combination (this query serves both backwards) and take the largest.
   size_t best = 0;
   for (int v = 0; v < 2; ++v)
-    if (plan_bwd(rows, cols, dtype_size(dtype_x), v == 0, dw_mode, cu_count(device), &p)) best = std::max(best, p.total);
+    for (int d = 0; d < 2; ++d)
+      if (plan_bwd(rows, cols, dtype_size(dtype_x), v == 0, dw_mode, cu_count(device), &p, d == 1))
+        best = std::max(best, p.total);
   return best;
 }
 

@@ -596,9 +596,56 @@ def copy_ceiling(work, dev, reps, flush, row_bytes=None):
     return 2 * n / (ms * 1e-3) / 1e9
 
 
-def attach_copy(e, dev, reps, flush):
+# Each op's kernels as (streams read, streams written, bytes per stream), the large operands only: the byte
+# mix the op's own kernels move, which HBM serves at its own rate (more reads than writes runs faster than a
+# copy, eight read streams slower).
+_C1 = 4096 * 4096 * 4
+_C2 = 8192 * 4096 * 2
+_SW = 8192 * 14336 * 2
+_AR = 4 * 2048 * 4096 * 2
+MIX_PATTERNS = {
+    "rms_norm": [(1, 1, _C1), (2, 1, _C1)],                  # fwd x -> y; bwd dy, x -> dx
+    "fused_add_rms_norm": [(2, 2, _C2), (3, 1, _C2)],        # fwd x, r -> y, s; bwd dy, dS, s -> dx
+    "swiglu": [(2, 1, _SW), (3, 2, _SW)],                    # fwd a, b -> c; bwd a, b, dc -> da, db
+    "geglu": [(2, 1, _SW), (3, 2, _SW)],
+    "attn_res": [(8, 1, _AR), (9, 8, _AR)],                  # fwd 8 blocks -> h; bwd 8 blocks, dh -> 8 dV
+    "jsd": [(2, 1, 8192 * 128256 * 2)],                      # X, Y -> dX
+}
+
+
+MIX_PAD = 4352  # bytes between streams beyond their length: 64 MiB-spaced streams ran up to 8% slower
+
+
+def mix_ceiling(parts, dev, reps, flush):
+    """hk_stream_mix over every (reads, writes, bytes) part, the parts launched back to back in one timed call
+    as an op's kernels are (each part on buffers of its own, streams MIX_PAD bytes apart), timed like the ops;
+    median ms."""
+    from kernels import _lib
+    st = _lib.stream_of(dev)
+    bufs = [(torch.empty(r * (nbytes + MIX_PAD), dtype=torch.uint8, device=dev).fill_(1),
+             torch.empty(w * (nbytes + MIX_PAD), dtype=torch.uint8, device=dev), r, w, nbytes) for r, w, nbytes in parts]
+
+    def fn():
+        for src, dst, r, w, nbytes in bufs:
+            _lib.call("hk_stream_mix", dst.data_ptr(), src.data_ptr(), nbytes, nbytes + MIX_PAD, r, w, st)
+
+    fn()
+    torch.cuda.synchronize()
+    for src, dst, r, w, nbytes in bufs:
+        expect = (0x01010101 if r % 2 else 0) + w - 1  # every word of the last stream
+        last = (w - 1) * (nbytes + MIX_PAD) + nbytes
+        if int(dst[last - 4:last].view(torch.int32).item()) != expect:
+            raise RuntimeError("hk_stream_mix produced a wrong result")
+    ms = statistics.median(time_events(fn, reps, flush))
+    del bufs
+    torch.cuda.empty_cache()
+    return ms
+
+
+def attach_copy(e, dev, reps, flush, name=None):
     """e["copy_same_bytes"] (flat copy) and, for the row kernels' entries (e["row_bytes"]),
-    e["copy_rows_same_bytes"]: the op against copies of its own bytes."""
+    e["copy_rows_same_bytes"]: the op against copies of its own bytes; for the ops in MIX_PATTERNS,
+    e["mix_same_pattern"]: against streaming kernels of its own kernels' read/write mix."""
     cc = copy_ceiling(e["work"], dev, reps, flush)
     e["copy_same_bytes"] = {"value": round(cc, 1), "unit": "GB/s", "op_over_copy": round(e["value"] / cc, 3),
                             "kernel": "hk_stream_copy flat"}
@@ -606,6 +653,12 @@ def attach_copy(e, dev, reps, flush):
         cr = copy_ceiling(e["work"], dev, reps, flush, e["row_bytes"])
         e["copy_rows_same_bytes"] = {"value": round(cr, 1), "unit": "GB/s", "op_over_copy": round(e["value"] / cr, 3),
                                      "kernel": "hk_stream_copy rows of %d bytes" % e["row_bytes"]}
+    if name in MIX_PATTERNS:
+        t = mix_ceiling(MIX_PATTERNS[name], dev, reps, flush)
+        e["mix_same_pattern"] = {"ms": round(t, 5), "value": round(e["work"] / (t * 1e-3) / 1e9, 1), "unit": "GB/s",
+                                 "op_over_mix": round(t / e["ms"], 3),
+                                 "streams": ["%dR%dW x %d MB" % (r, w, b >> 20) for r, w, b in MIX_PATTERNS[name]],
+                                 "kernel": "hk_stream_mix"}
     return e
 
 
@@ -865,7 +918,7 @@ def main(argv=None):
                 out[name] = table[name][0](K, dev, args.op_reps, flush)
             torch.cuda.empty_cache()
             if args.only_copy and out[name].get("unit") == "GB/s":
-                attach_copy(out[name], dev, args.op_reps, flush)
+                attach_copy(out[name], dev, args.op_reps, flush, name)
         print(json.dumps(out), flush=True)
         return 0
     log(f"device: {torch.cuda.get_device_name(dev)}")
@@ -970,12 +1023,15 @@ def main(argv=None):
         for name, e in ops.items():
             if e["unit"] != "GB/s":
                 continue
-            attach_copy(e, dev, max(3, args.op_reps // 2), flush)
+            attach_copy(e, dev, max(3, args.op_reps // 2), flush, name)
             cc = e["copy_same_bytes"]["value"]
             extra = ""
             if "copy_rows_same_bytes" in e:
                 cr = e["copy_rows_same_bytes"]["value"]
                 extra = f"; row-order copy {cr:.0f} GB/s, op at {e['value'] / cr:.1%} of it"
+            if "mix_same_pattern" in e:
+                extra += f"; its stream mix {e['mix_same_pattern']['ms']:.4f} ms, op at " \
+                         f"{e['mix_same_pattern']['op_over_mix']:.1%} of it"
             log(f"  {name}: copy {cc:.0f} GB/s, op at {e['value'] / cc:.1%} of it{extra}")
         del flush
 

@@ -13,6 +13,13 @@
 //   issued with the loads of the block's next row (rows strided by the grid):
 //   the order of the CrossEntropy / GRPO gradient kernels, without their
 //   arithmetic.
+// hk_stream_mix: an op's byte mix without its arithmetic: n_read streams read
+//   and n_write streams written, all of one length, in the flat order, two
+//   256-lane blocks a CU, one 16-byte vector of every stream in flight per
+//   lane (the best launch shape measured for 2-9 read streams). An op that
+//   reads three rows and writes one (the fused-add norm backward) is compared
+//   with 3 reads + 1 write here, which HBM serves faster than a copy of the
+//   same bytes; one with 8 + 1 (the AttnRes forward), slower.
 #include "hk_common.h"
 #include "../../include/hilda_kernel_amd.h"
 
@@ -60,6 +67,28 @@ __global__ __launch_bounds__(1024) void copy_rows_kernel(u32x4* d, const u32x4* 
   }
 }
 
+constexpr int kMixMaxRead = 9, kMixMaxWrite = 8;
+
+// d[w][i] = (xor over k < n_read of s[k][i]) + w for every vector i of n, the
+// streams `stride` vectors apart.
+__global__ __launch_bounds__(256) void mix_kernel(u32x4* __restrict__ d, const u32x4* __restrict__ s, int64_t n,
+                                                  int64_t stride_v, int n_read, int n_write) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    u32x4 r[kMixMaxRead];
+#pragma unroll
+    for (int k = 0; k < kMixMaxRead; ++k)
+      if (k < n_read) r[k] = s[k * stride_v + i];
+    u32x4 a = r[0];
+#pragma unroll
+    for (int k = 1; k < kMixMaxRead; ++k)
+      if (k < n_read) a ^= r[k];
+#pragma unroll
+    for (int w = 0; w < kMixMaxWrite; ++w)
+      if (w < n_write) __builtin_nontemporal_store(a + (uint32_t)w, d + w * stride_v + i);
+  }
+}
+
 }  // namespace
 }  // namespace hk
 
@@ -92,4 +121,20 @@ extern "C" int hk_stream_copy(void* dst, const void* src, int64_t rows, int64_t 
   else
     hipLaunchKernelGGL(copy_rows_kernel<24>, grid, dim3(1024), 0, st, d, s, rows, cols);
   return check_launch("copy_rows_kernel");
+}
+
+extern "C" int hk_stream_mix(void* dst, const void* src, int64_t bytes, int64_t stride, int n_read, int n_write,
+                             hk_stream_t stream) {
+  HK_REQUIRE(n_read >= 1 && n_read <= kMixMaxRead && n_write >= 1 && n_write <= kMixMaxWrite,
+             "n_read=%d n_write=%d: 1..%d streams read, 1..%d written", n_read, n_write, kMixMaxRead, kMixMaxWrite);
+  HK_REQUIRE(bytes >= 0 && bytes % 16 == 0, "bytes=%lld: whole 16-byte vectors per stream", (long long)bytes);
+  HK_REQUIRE(stride >= bytes && stride % 16 == 0, "stride=%lld: at least bytes=%lld, a multiple of 16",
+             (long long)stride, (long long)bytes);
+  if (bytes == 0) return HK_OK;
+  HK_REQUIRE(dst && src && aligned_to(dst, 16) && aligned_to(src, 16), "16-byte aligned pointers required");
+  const int dev = current_device();
+  const int cu = dev >= 0 && cu_count(dev) > 0 ? cu_count(dev) : 256;
+  hipLaunchKernelGGL(mix_kernel, dim3((unsigned)(2 * cu)), dim3(256), 0, (hipStream_t)stream, (u32x4*)dst,
+                     (const u32x4*)src, bytes / 16, stride / 16, n_read, n_write);
+  return check_launch("mix_kernel");
 }

@@ -36,6 +36,7 @@ SIGNATURES = {
     "hk_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
     "hk_rms_norm_bwd_noalloc": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
     "hk_stream_copy": (_i32, [_p, _p, _i64, _i64, _i32, _p]),
+    "hk_stream_mix": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _p]),
     "hk_fused_add_rms_norm_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p]),
     "hk_fused_add_rms_norm_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _sz, _p]),
     "hk_rope": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

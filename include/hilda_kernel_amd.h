@@ -361,6 +361,16 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
  * register-resident row kernels (row_bytes <= 384 KiB). */
 int hk_stream_copy(void* dst, const void* src, int64_t rows, int64_t row_bytes, int mode, hk_stream_t stream);
 
+/* No counterpart in the reference: an op's byte mix without its arithmetic,
+ * timed beside it. n_read source streams and n_write destination streams of
+ * `bytes` each (whole 16-byte vectors) start `stride` bytes apart (>= bytes, a
+ * multiple of 16) from src and from dst (16-byte aligned, no overlap);
+ * destination stream w receives the XOR of the source streams' vectors at the
+ * same offset plus w in every 32-bit word. Flat order. 1 <= n_read <= 9,
+ * 1 <= n_write <= 8. */
+int hk_stream_mix(void* dst, const void* src, int64_t bytes, int64_t stride, int n_read, int n_write,
+                  hk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,6 +113,12 @@ def test_argument_validation_losses_without_gpu():
     _expect_einval(lib.hk_stream_copy(p, p, 4, 64, 7, None), "copy mode")
     _expect_einval(lib.hk_stream_copy(p, p, 4, 24, _lib.COPY_FLAT, None), "16-byte")
     _expect_einval(lib.hk_stream_copy(p, p, 4, 24 * 1024 * 16 + 16, _lib.COPY_ROWS, None), "at most")
+    _expect_einval(lib.hk_stream_mix(p, p, 64, 64, 0, 1, None), "streams read")
+    _expect_einval(lib.hk_stream_mix(p, p, 64, 64, 10, 1, None), "streams read")
+    _expect_einval(lib.hk_stream_mix(p, p, 64, 64, 2, 9, None), "streams read")
+    _expect_einval(lib.hk_stream_mix(p, p, 24, 32, 2, 1, None), "16-byte")
+    _expect_einval(lib.hk_stream_mix(p, p, 64, 48, 2, 1, None), "stride")
+    _expect_einval(lib.hk_stream_mix(p, p, 64, 72, 2, 1, None), "stride")
 
 
 @needs_lib

@@ -34,15 +34,15 @@ __device__ __forceinline__ float kl_term(float y, float t, float eps) {
 }
 
 // Visit row elements: f(width, x[], y[], first column) for VEC-wide packs
-// (all loads of a group issued first), then width-1 calls for the tail. NT
+// (U packs of each row issued first), then width-1 calls for the tail. NT
 // lanes share the row.
-template <typename T, int VEC, int NT = kThreads, class F>
+template <typename T, int VEC, int NT = kThreads, int U = kUnroll, class F>
 __device__ __forceinline__ void row_pairs(const T* __restrict__ a, const T* __restrict__ b, int64_t cols, F&& f) {
   const int64_t nvec = VEC > 1 ? cols / VEC : 0;
-  for (int64_t base = threadIdx.x; base < nvec; base += (int64_t)NT * kUnroll) {
-    Pack<T, VEC> av[kUnroll], bv[kUnroll];
+  for (int64_t base = threadIdx.x; base < nvec; base += (int64_t)NT * U) {
+    Pack<T, VEC> av[U], bv[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t i = base + (int64_t)u * NT;
       if (i < nvec) {
         av[u] = load_pack<T, VEC>(a + i * VEC);
@@ -50,7 +50,7 @@ __device__ __forceinline__ void row_pairs(const T* __restrict__ a, const T* __re
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t i = base + (int64_t)u * NT;
       if (i < nvec) {
         float x[VEC], y[VEC];
@@ -144,6 +144,11 @@ __device__ __forceinline__ float jsd_elem(float x, float y, float beta, float* a
 }
 
 // Loss and dX are divided by n = max(n_valid, 1) (all rows without labels).
+// One 256-lane workgroup a CU walks rows r, r + grid, ...: four waves a CU with
+// 8 packs of each row in flight a lane; a workgroup per row (up to 32 waves a
+// CU) measured 3.4% slower at [8192, 128256] bf16, as streaming copies slow
+// down with more waves a CU.
+constexpr int kJsdUnroll = 8;
 template <typename T, int VEC, int MODE>
 __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_rows, T* __restrict__ dX,
                                                        const T* __restrict__ X, const T* __restrict__ Y,
@@ -151,17 +156,18 @@ __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_
                                                        const int* __restrict__ n_valid, int64_t rows, float beta,
                                                        int64_t cols, int64_t ldx, int64_t ldy, int64_t ldd) {
   __shared__ float red[kWaves];
-  const int64_t row = blockIdx.x;
+  const float n = labels != nullptr ? (float)max(*n_valid, 1) : (float)rows;
+  const float inv_n = 1.0f / n;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {  // uniform over the block
   T* d = dX + row * ldd;
   if (labels != nullptr && labels[row] == ignore_index) {
     for (int64_t c = threadIdx.x; c < cols; c += kThreads) d[c] = from_f32<T>(0.f);
     if (threadIdx.x == 0) loss_rows[row] = 0.f;
-    return;
+    continue;
   }
-  const float n = labels != nullptr ? (float)max(*n_valid, 1) : (float)rows;
-  const float inv_n = 1.0f / n;
   float acc = 0.f;
-  row_pairs<T, VEC>(X + row * ldx, Y + row * ldy, cols, [&](auto wc, const float* x, const float* y, int64_t c0) {
+  row_pairs<T, VEC, kThreads, kJsdUnroll>(X + row * ldx, Y + row * ldy, cols,
+                                          [&](auto wc, const float* x, const float* y, int64_t c0) {
     constexpr int W = decltype(wc)::value;
     float g[W];
 #pragma unroll
@@ -175,6 +181,7 @@ __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_
   });
   acc = block_sum<kWaves>(acc, red);
   if (threadIdx.x == 0) loss_rows[row] = acc * inv_n;
+  }
 }
 
 // (max, sum) pair of a log-sum-exp in base 2, merged over the block: every
@@ -452,7 +459,9 @@ int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const
       const bool vec = rows_vec_ok<T>(X, ldx) && rows_vec_ok<T>(Y, ldy) && rows_vec_ok<T>(dX, ld_dx);
       const int mode = beta == 0.f ? 0 : beta == 1.f ? 1 : 2;  // the reference branches on these values (jsd.py:67-87)
       auto go = [&](auto vc, auto mc) {
-        hipLaunchKernelGGL((jsd_kernel<T, decltype(vc)::value, decltype(mc)::value>), dim3((unsigned)rows),
+        const int dev = current_device();
+        const int64_t cus = dev >= 0 && cu_count(dev) > 0 ? cu_count(dev) : 256;
+        hipLaunchKernelGGL((jsd_kernel<T, decltype(vc)::value, decltype(mc)::value>), dim3((unsigned)std::min(rows, cus)),
                            dim3(kThreads), 0, st, loss_rows, (T*)dX, (const T*)X, (const T*)Y, labels, ignore_index,
                            n_valid, rows, beta, cols, ldx, ldy, ld_dx);
       };

@@ -1027,58 +1027,92 @@ __global__ __launch_bounds__(1024) void grpo_prep_kernel(GrpoArgs a, GrpoTok* __
   }
 }
 
+// Finalize, first pass: one block per (sequence b, chunk c) of kFinChunk
+// tokens, one token a lane. Scatters the per-token rows and writes the chunk's
+// [sum m*loss, sum m, sum m*kl, sum m*clip] (fp64) to part[b * chunks + c].
+// Many small blocks: every load of the pass is in flight at once.
+constexpr int kFinChunk = 256;
+struct alignas(16) GrpoPart {
+  double loss, m, kl, clip;
+};
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__global__ __launch_bounds__(kFinChunk) void grpo_partial_kernel(GrpoArgs a, const GrpoTok* __restrict__ tok,
+                                                                 const GrpoOut* __restrict__ res,
+                                                                 GrpoPart* __restrict__ part, int64_t chunks) {
+  constexpr int NW = kFinChunk / kWave;
+  __shared__ double red[4][NW];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t b = blockIdx.x / chunks, c = blockIdx.x - b * chunks;
+  const int64_t l = c * kFinChunk + threadIdx.x;
+  double ls = 0.0, ms = 0.0, ks = 0.0, cs = 0.0;
+  if (l < a.L) {
+    const int64_t o = b * a.L + l;
+    const double m = tok[o].m;
+    const GrpoOut r = res[o];
+    ls = m * r.loss;
+    ms = m;
+    ks = m * r.kl;
+    cs = m * r.clip;
+    a.lse_rows[o] = r.lse;
+    a.loss_rows[o] = r.loss;
+    a.kl_rows[o] = r.kl;
+    a.clip_rows[o] = r.clip;
+  }
+  ls = wave_sum_f64(ls);
+  ms = wave_sum_f64(ms);
+  ks = wave_sum_f64(ks);
+  cs = wave_sum_f64(cs);
+  if (lane == 0) {
+    red[0][wave] = ls;
+    red[1][wave] = ms;
+    red[2][wave] = ks;
+    red[3][wave] = cs;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    GrpoPart p{0.0, 0.0, 0.0, 0.0};
+    for (int w = 0; w < NW; ++w) {
+      p.loss += red[0][w];
+      p.m += red[1][w];
+      p.kl += red[2][w];
+      p.clip += red[3][w];
+    }
+    part[blockIdx.x] = p;
+  }
+}
+
+// Finalize, second pass (one block):
 // out = [mean_b(sum_l m*loss / max(len_b,1)), sum m*kl / max(sum m,1), sum m*clip / max(sum m,1)]
-// (kernels/grpo_loss.py:290-295); also scatters the per-token rows. Each wave
-// owns whole sequences (b = wave, wave + 16, ...) and reduces them with
-// shuffles; one block-wide combine at the end.
-__global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const GrpoTok* __restrict__ tok,
-                                                             const GrpoOut* __restrict__ res, float* __restrict__ loss_out,
-                                                             float* __restrict__ kl_out, float* __restrict__ clip_out) {
+// (kernels/grpo_loss.py:290-295). Each wave owns whole sequences (b = wave,
+// wave + 16, ...) and sums their chunk partials; one block-wide combine at the
+// end. A fixed order throughout: the result does not depend on scheduling.
+__global__ __launch_bounds__(1024) void grpo_finalize_kernel(GrpoArgs a, const GrpoPart* __restrict__ part,
+                                                             int64_t chunks, float* __restrict__ loss_out,
+                                                             float* __restrict__ kl_out,
+                                                             float* __restrict__ clip_out) {
   __shared__ double red[4][16];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  auto wsum = [](double v) {
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-  };
   double loss = 0.0, msum = 0.0, kls = 0.0, clips = 0.0;
-  constexpr int U = 4;  // tokens a lane loads before it adds: four loads in flight, not one
   for (int64_t b = wave; b < a.B; b += 16) {
     double ls = 0.0, ms = 0.0, ks = 0.0, cs = 0.0;
-    for (int64_t l0 = lane; l0 < a.L; l0 += U * kWave) {
-      float mv[U];
-      GrpoOut rv[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t l = l0 + u * kWave;
-        if (l < a.L) {
-          mv[u] = tok[b * a.L + l].m;
-          rv[u] = res[b * a.L + l];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t l = l0 + u * kWave;
-        if (l < a.L) {
-          const int64_t o = b * a.L + l;
-          const double m = mv[u];
-          const GrpoOut r = rv[u];
-          ls += m * r.loss;
-          ms += m;
-          ks += m * r.kl;
-          cs += m * r.clip;
-          a.lse_rows[o] = r.lse;
-          a.loss_rows[o] = r.loss;
-          a.kl_rows[o] = r.kl;
-          a.clip_rows[o] = r.clip;
-        }
-      }
+    for (int64_t c = lane; c < chunks; c += kWave) {
+      const GrpoPart p = part[b * chunks + c];
+      ls += p.loss;
+      ms += p.m;
+      ks += p.kl;
+      cs += p.clip;
     }
-    ls = wsum(ls);
-    ms = wsum(ms);
+    ls = wave_sum_f64(ls);
+    ms = wave_sum_f64(ms);
     loss += ls / (ms > 1.0 ? ms : 1.0);
     msum += ms;
-    kls += wsum(ks);
-    clips += wsum(cs);
+    kls += wave_sum_f64(ks);
+    clips += wave_sum_f64(cs);
   }
   if (lane == 0) {
     red[0][wave] = loss;
@@ -1273,9 +1307,12 @@ GrpoArgs grpo_args(const GrpoInputs& in) {
 }
 }  // namespace
 
+int64_t grpo_fin_chunks(int64_t L) { return (L + kFinChunk - 1) / kFinChunk; }
+
 size_t grpo_scratch_bytes(int64_t B, int64_t L) {
-  // token records then per-token results
-  return (size_t)(B * L) * (sizeof(GrpoTok) + sizeof(GrpoOut)) + 256;
+  // token records, per-token results, then the finalize's chunk partials
+  return (size_t)(B * L) * (sizeof(GrpoTok) + sizeof(GrpoOut)) + (size_t)(B * grpo_fin_chunks(L)) * sizeof(GrpoPart) +
+         256;
 }
 
 int grpo_check(const GrpoInputs& in) {
@@ -1346,9 +1383,21 @@ int grpo_finalize_launch(const GrpoInputs& in, const void* scratch, float* loss_
   a.loss_rows = loss_rows;
   a.kl_rows = kl_rows;
   a.clip_rows = clip_rows;
+  const size_t n = (size_t)(in.B * in.L);
   const GrpoTok* tok = (const GrpoTok*)scratch;
-  const GrpoOut* res = (const GrpoOut*)((const char*)scratch + (size_t)(in.B * in.L) * sizeof(GrpoTok));
-  hipLaunchKernelGGL(grpo_finalize_kernel, dim3(1), dim3(1024), 0, st, a, tok, res, loss_out, kl_out, clip_out);
+  const GrpoOut* res = (const GrpoOut*)((const char*)scratch + n * sizeof(GrpoTok));
+  GrpoPart* part = (GrpoPart*)((char*)scratch + n * (sizeof(GrpoTok) + sizeof(GrpoOut)));
+  const int64_t chunks = grpo_fin_chunks(in.L);
+  HK_REQUIRE(in.B * chunks < (1LL << 31), "B=%lld L=%lld: too many finalize blocks", (long long)in.B,
+             (long long)in.L);
+  if (chunks > 0) {
+    hipLaunchKernelGGL(grpo_partial_kernel, dim3((unsigned)(in.B * chunks)), dim3(kFinChunk), 0, st, a, tok, res,
+                       part, chunks);
+    const int rc = check_launch("grpo_partial_kernel");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(grpo_finalize_kernel, dim3(1), dim3(1024), 0, st, a, (const GrpoPart*)part, chunks, loss_out,
+                     kl_out, clip_out);
   return check_launch("grpo_finalize_kernel");
 }
 

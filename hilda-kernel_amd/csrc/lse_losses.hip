@@ -661,8 +661,16 @@ __global__ __launch_bounds__(1024) void ce_plan_kernel(int* __restrict__ n_valid
 __global__ __launch_bounds__(1024) void sum_rows_kernel(float* __restrict__ out, const float* __restrict__ v,
                                                         int64_t n, const int* __restrict__ n_valid, int divide) {
   __shared__ double red[16];
+  constexpr int U = 8;  // loads of a lane in flight before its adds (the adds keep the order i, i + 1024, ...)
   double s = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += 1024) s += (double)v[i];
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += U * 1024) {
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = i0 + u * 1024 < n ? v[i0 + u * 1024] : 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * 1024 < n) s += (double)x[u];
+  }
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = s;
   __syncthreads();
@@ -676,26 +684,53 @@ __global__ __launch_bounds__(1024) void sum_rows_kernel(float* __restrict__ out,
 
 // out = in * g (g scalar or per row); with g_prev, out = in * g / g_prev (0 where g_prev = 0).
 // skip_if_one: a scalar g equal to 1 (and no g_prev) leaves the data untouched.
-template <typename T, int VEC>
-__global__ __launch_bounds__(256) void scale_rows_kernel(T* __restrict__ out, const T* __restrict__ in,
-                                                         const float* __restrict__ g, const float* __restrict__ g_prev,
-                                                         int per_row, int skip_if_one, int64_t rows, int64_t cols,
-                                                         int64_t ld_in, int64_t ld_out) {
+// A flat grid-stride walk with U loads of a lane in flight before its stores,
+// the shape of the fastest streaming copy (one 256-lane block per CU). out may
+// alias in: a lane reads each of its elements before it writes that element.
+template <typename T, int VEC, int U = 4>
+__global__ __launch_bounds__(256) void scale_rows_kernel(T* out, const T* in, const float* __restrict__ g,
+                                                         const float* __restrict__ g_prev, int per_row,
+                                                         int skip_if_one, int64_t rows, int64_t cols, int64_t ld_in,
+                                                         int64_t ld_out) {
   if (!per_row && skip_if_one && g_prev == nullptr && g[0] == 1.f && out == in) return;
   const int64_t nv = cols / VEC;
   const int64_t total = rows * nv;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / nv, cv = (i - r * nv) * VEC;
-    float f = per_row ? g[r] : g[0];
-    if (g_prev) {
-      const float p = per_row ? g_prev[r] : g_prev[0];
-      f = p != 0.f ? f / p : 0.f;
-    }
-    float x[VEC];
-    unpack(load_pack<T, VEC>(in + r * ld_in + cv), x);
+  const double rinv = 1.0 / (double)nv;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  float f0 = g[0];
+  if (!per_row && g_prev) f0 = g_prev[0] != 0.f ? f0 / g_prev[0] : 0.f;
+  for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < total; i0 += U * stride) {
+    Pack<T, VEC> x[U];
+    int64_t r[U], cv[U];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) x[e] *= f;
-    store_pack<T, VEC>(out + r * ld_out + cv, pack<T, VEC>(x));
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * stride;
+      // row of vector i: a double-precision quotient, corrected by one step
+      int64_t q = (int64_t)((double)i * rinv);
+      q -= q * nv > i;
+      q += (q + 1) * nv <= i;
+      r[u] = q;
+      cv[u] = (i - q * nv) * VEC;
+      if (i < total) x[u] = load_pack<T, VEC>(in + q * ld_in + cv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i0 + u * stride < total) {
+        float f = f0;
+        if (per_row) {
+          f = g[r[u]];
+          if (g_prev) {
+            const float pv = g_prev[r[u]];
+            f = pv != 0.f ? f / pv : 0.f;
+          }
+        }
+        float v[VEC];
+        unpack(x[u], v);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] *= f;
+        store_pack<T, VEC>(out + r[u] * ld_out + cv[u], pack<T, VEC>(v));
+      }
+    }
   }
 }
 
@@ -1620,11 +1655,11 @@ int hk_scale_rows(void* out, const void* in, const float* g, const float* g_prev
   return dispatch_t(dtype, [&](auto tt) {
     using T = typename decltype(tt)::type;
     const int64_t total = rows * (vec_ok ? cols / vec : cols);
-    // grid-stride over a few blocks per CU: a call that turns out to be a no-op
+    // grid-stride over one block per CU: a call that turns out to be a no-op
     // (g == 1, decided on the device) then costs one short launch, not 64K blocks
     const int dev = current_device();
     if (dev < 0) return (int)hipErrorNoDevice;
-    const int64_t cap = (int64_t)cu_count(dev) * 8;
+    const int64_t cap = (int64_t)cu_count(dev);
     const int64_t blocks = std::min<int64_t>(std::max<int64_t>(cdiv(total, 256 * 4), 1), cap);
     const dim3 grid((unsigned)blocks);
     if (vec_ok)

@@ -447,3 +447,43 @@ def test_grpo_c4_config():
         s = B * float(mask[b].sum())
         assert_close(grad[b].float() * s, d[0] * s, name=f"seq {b} grad", **tol(torch.bfloat16))
         assert rel_fro(grad[b], d[0]) < 1e-2
+
+
+# hk_scale_rows (the backward's upstream-gradient multiply): 16-byte vectors and
+# the per-element form, padded row strides, scalar and per-row factors, a
+# previous factor with zeros (rows that must come out 0), in place and out of
+# place, and a shape that takes several grid-stride passes. Expected: the fp32
+# product rounded to the dtype, bitwise.
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols,pad_in,pad_out,per_row,with_prev", [
+    (37, 1000, 0, 0, False, False),
+    (37, 1000, 8, 24, True, True),
+    (19, 1001, 3, 0, True, False),
+    (5, 7, 0, 5, False, True),
+    (4096, 4096, 0, 0, True, True),
+])
+def test_scale_rows(dtype, rows, cols, pad_in, pad_out, per_row, with_prev):
+    dev = gpu()
+    g = torch.Generator().manual_seed(rows * 131 + cols)
+    src_full = torch.randn(rows, cols + pad_in, generator=g).to(dtype)
+    dl = (torch.rand(rows, generator=g) + 0.5) if per_row else torch.tensor(1.75)
+    prev = None
+    if with_prev:
+        prev = (torch.rand(rows, generator=g) + 0.25) if per_row else torch.tensor(0.625)
+        if per_row:
+            prev[::3] = 0.0
+    src = src_full.to(dev)[:, :cols]
+    out = torch.full((rows, cols + pad_out), 7.0, dtype=dtype, device=dev)
+    ce_mod.scale_rows_(out[:, :cols], src, dl.to(dev), None if prev is None else prev.to(dev))
+    f = dl.float().reshape(-1, 1) if per_row else dl.float().reshape(1, 1)
+    if prev is not None:
+        p = prev.float().reshape(f.shape)
+        f = torch.where(p != 0, f / torch.where(p != 0, p, torch.ones_like(p)), torch.zeros_like(p))
+    want = (src_full[:, :cols].float() * f).to(dtype)
+    got = out.cpu()
+    assert torch.equal(got[:, :cols], want)
+    assert torch.all(got[:, cols:] == 7.0)  # the padding of the output rows is not written
+    # in place with a unit scalar: skipped on the device, data untouched
+    same = src.clone()
+    ce_mod.scale_rows_(same, same, torch.tensor(1.0, device=dev), None, skip_if_one=True)
+    assert torch.equal(same, src)

@@ -45,10 +45,12 @@ def log(*a):
 
 
 class TimingEvent:
-    """A HIP event created with hipEventDisableSystemFence, the flag HIP documents for events used only to
-    time: recording it takes no system-scope release/acquire (no L2 write-back and invalidate between the
-    kernels it sits between), so markers inside a timed region perturb it least. The elapsed time between two
-    such events spans the launches between them, as rocprofv3's kernel timestamps do."""
+    """A HIP timing event. By default created with hipEventDisableSystemFence, the flag HIP documents for
+    events used only to time: recording it takes no system-scope release/acquire (no L2 write-back and
+    invalidate between the kernels it sits between), so markers inside a timed region perturb it least. The
+    elapsed time between two such events spans the launches between them, as rocprofv3's kernel timestamps do.
+    fence=True gives a default event (the system-scope release that torch's timing events take): recorded at
+    the end of a timed region, the region then includes writing the op's dirty L2 lines back to HBM."""
     _hip = None
     _FLAGS = 0x20000000  # hipEventDisableSystemFence
 
@@ -65,11 +67,11 @@ class TimingEvent:
             cls._hip = hip
         return cls._hip
 
-    def __init__(self):
+    def __init__(self, fence=False):
         import ctypes
         self._ct = ctypes
         self.ev = ctypes.c_void_p()
-        rc = self._lib().hipEventCreateWithFlags(ctypes.byref(self.ev), self._FLAGS)
+        rc = self._lib().hipEventCreateWithFlags(ctypes.byref(self.ev), 0 if fence else self._FLAGS)
         if rc != 0:
             raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
 
@@ -192,18 +194,21 @@ class Flusher:
 
 
 def time_events(fn, reps, flush=None, warmup=2):
-    # Default (fenced) events: each rep starts after a flush and ends with the op's dirty L2 lines written
-    # back, so the op is charged for all of its writes.
+    # Each rep starts after a flush (a read of 512 MiB: the op's inputs come from HBM). The start event is
+    # fence-free: after a read-only flush the L2 holds nothing dirty, and a fenced record's write-back and
+    # invalidate (about 5 us) would be charged to the op. The end event is fenced, so the op is charged for
+    # writing all of its dirty L2 lines back to HBM.
     for _ in range(warmup):
         fn()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    stream = torch.cuda.current_stream()
+    starts = [TimingEvent() for _ in range(reps)]
+    ends = [TimingEvent(fence=True) for _ in range(reps)]
     for i in range(reps):
         if flush is not None:
             flush()
-        starts[i].record()
+        starts[i].record(stream)
         fn()
-        ends[i].record()
+        ends[i].record(stream)
     torch.cuda.synchronize()
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 

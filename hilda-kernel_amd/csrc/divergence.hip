@@ -143,6 +143,24 @@ __device__ __forceinline__ float jsd_elem(float x, float y, float beta, float* a
   }
 }
 
+// MODE 2 in base 2, the form jsd_kernel streams (fewer VALU slots an element:
+// the kernel is close to VALU-bound at HBM speed): with x2 = x log2(e),
+// y2 = y log2(e), t = (1-beta) q and lm2 = log2(beta p + t),
+//   loss term = ln2 (t (x2 - lm2) + beta p (y2 - lm2)),
+//   dX / n    = q (x2 - lm2) kg, kg = (1-beta) ln2 / n.
+// Adds t (x2 - lm2) to *acc_t and p (y2 - lm2) to *acc_p; returns dX / n.
+__device__ __forceinline__ float jsd_mix_elem2(float x, float y, float beta, float c1, float kg, float* acc_t,
+                                               float* acc_p) {
+  const float x2 = x * kLog2e, y2 = y * kLog2e;
+  const float q = exp2_fast(x2), p = exp2_fast(y2);
+  const float t = c1 * q;
+  const float lm2 = log2_fast(fmaf(beta, p, t));
+  const float dx2 = x2 - lm2, dy2 = y2 - lm2;
+  *acc_t = fmaf(t, dx2, *acc_t);
+  *acc_p = fmaf(p, dy2, *acc_p);
+  return (q * kg) * dx2;
+}
+
 // Loss and dX are divided by n = max(n_valid, 1) (all rows without labels).
 // One 256-lane workgroup a CU walks rows r, r + grid, ...: four waves a CU with
 // 8 packs of each row in flight a lane; a workgroup per row (up to 32 waves a
@@ -165,13 +183,17 @@ __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_
     if (threadIdx.x == 0) loss_rows[row] = 0.f;
     continue;
   }
-  float acc = 0.f;
+  float acc = 0.f, acc_p = 0.f;  // MODE 2: acc sums t (x2 - lm2), acc_p sums p (y2 - lm2)
+  const float c1 = 1.0f - beta, kg = c1 * kLn2 * inv_n;
   row_pairs<T, VEC, kThreads, kJsdUnroll>(X + row * ldx, Y + row * ldy, cols,
                                           [&](auto wc, const float* x, const float* y, int64_t c0) {
     constexpr int W = decltype(wc)::value;
     float g[W];
 #pragma unroll
-    for (int e = 0; e < W; ++e) g[e] = jsd_elem<MODE>(x[e], y[e], beta, &acc) * inv_n;
+    for (int e = 0; e < W; ++e) {
+      if constexpr (MODE == 2) g[e] = jsd_mix_elem2(x[e], y[e], beta, c1, kg, &acc, &acc_p);
+      else g[e] = jsd_elem<MODE>(x[e], y[e], beta, &acc) * inv_n;
+    }
     if constexpr (W == VEC && VEC > 1) {
       store_pack<T, VEC>(d + c0, pack<T, VEC>(g));
     } else {
@@ -179,6 +201,7 @@ __global__ __launch_bounds__(kThreads) void jsd_kernel(float* __restrict__ loss_
       for (int e = 0; e < W; ++e) d[c0 + e] = from_f32<T>(g[e]);
     }
   });
+  if constexpr (MODE == 2) acc = kLn2 * fmaf(beta, acc_p, acc);
   acc = block_sum<kWaves>(acc, red);
   if (threadIdx.x == 0) loss_rows[row] = acc * inv_n;
   }

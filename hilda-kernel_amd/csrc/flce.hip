@@ -169,23 +169,28 @@ __global__ __launch_bounds__(256) void finish_rows_kernel(u32x4* __restrict__ dX
 
 // out[c, r] = in[r, c] for a rows x cols matrix of a 16-bit type (row strides
 // ld_in, ld_out, both multiples of 8; cols a multiple of 8); output columns r
-// in [rows, rows_pad) are written as zeros (rows_pad a multiple of 8). 64x64
-// tiles: 16-byte global loads and stores, the tile staged in LDS with a pitch
-// of 66 elements (33 dwords), so the column-gathering 2-byte reads of a wave
-// fall in distinct banks.
+// in [rows, rows_pad) are written as zeros (rows_pad a multiple of 8).
+// 16-byte global loads and stores, the tile staged in LDS (layout below).
 // With lim (a compacted input whose first *lim - lim_off rows are live), rows
 // past that are read as zeros and zeros are written up to the next multiple
 // of 64 of the bound, both relative to lim_off and absolute: what a GEMM
 // whose K is cut by the same bound reads (at least 64 columns).
 template <typename T>
-__global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, const T* __restrict__ in, int64_t rows,
+__global__ __launch_bounds__(512) void transpose_kernel(T* __restrict__ out, const T* __restrict__ in, int64_t rows,
                                                         int64_t rows_pad, int64_t cols, int64_t ld_in,
                                                         int64_t ld_out, const int* __restrict__ lim,
                                                         int64_t lim_off) {
-  constexpr int P = 66;
-  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * P];
+  static_assert(sizeof(T) == 2, "16-bit elements");
+  // 128 x 128 tiles: 256-byte runs on both sides (a 64 x 64 tile's 128-byte
+  // input runs from 256 KB rows ran at 2.3 TB/s). Lane (q, k) of unit i loads
+  // input rows 2q and 2q+1 at 16-byte column chunk k; each column's pair of
+  // elements becomes one 32-bit word (v_perm), stored column-major: word
+  // (column j, pair q) at j*64 + (((q >> 2) ^ (j >> 3)) << 2 | (q & 3)). The XOR
+  // of 4-word groups keeps the word writes (16 chunks of a wave, 16 groups) and
+  // the 16-byte reads (16 lanes of one column, 16 groups) free of bank conflicts.
+  __shared__ __attribute__((aligned(16))) uint32_t tile[128 * 64];
   const int t = threadIdx.x;
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 128;
   if (lim) {
     const int64_t n = *lim, v = n - lim_off;
     rows = std::max<int64_t>(0, std::min<int64_t>(rows, v));
@@ -193,30 +198,40 @@ __global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, con
     rows_pad = std::min<int64_t>(rows_pad, z);
     if (r0 >= rows_pad) return;  // uniform
   }
+  const int k = t & 15;
+  u32x4 va[2], vb[2];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int rr = t / 8 + 32 * k, cc = (t % 8) * 8;
-    const int64_t r = r0 + rr, c = c0 + cc;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (r < rows && c < cols) v = *reinterpret_cast<const u32x4*>(in + r * ld_in + c);
-    uint32_t* tp = reinterpret_cast<uint32_t*>(tile + rr * P + cc);
-    tp[0] = v.x;
-    tp[1] = v.y;
-    tp[2] = v.z;
-    tp[3] = v.w;
+  for (int i = 0; i < 2; ++i) {
+    const int q = (t >> 4) + 32 * i;
+    const int64_t r = r0 + 2 * q, c = c0 + 8 * k;
+    va[i] = u32x4{0u, 0u, 0u, 0u};
+    vb[i] = u32x4{0u, 0u, 0u, 0u};
+    if (c < cols) {
+      if (r < rows) va[i] = *reinterpret_cast<const u32x4*>(in + r * ld_in + c);
+      if (r + 1 < rows) vb[i] = *reinterpret_cast<const u32x4*>(in + (r + 1) * ld_in + c);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = (t >> 4) + 32 * i;
+    const int slot = (((q >> 2) ^ k) << 2) | (q & 3);  // j >> 3 == k for the 8 columns of chunk k
+    const uint32_t a[4] = {va[i].x, va[i].y, va[i].z, va[i].w};
+    const uint32_t b[4] = {vb[i].x, vb[i].y, vb[i].z, vb[i].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // low half: row 2q's element of column 8k + e, high half: row 2q+1's
+      const uint32_t w = __builtin_amdgcn_perm(b[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
+      tile[(8 * k + e) * 64 + slot] = w;
+    }
   }
   __syncthreads();
+  const int m = t & 15;  // output chunk: rows 8m .. 8m+7 of the tile, words 4m .. 4m+3
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int oc = t / 8 + 32 * k, oq = (t % 8) * 8;
-    const int64_t c = c0 + oc, r = r0 + oq;
-    if (c < cols && r < rows_pad) {
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)tile[(oq + 2 * i) * P + oc] | ((uint32_t)tile[(oq + 2 * i + 1) * P + oc] << 16);
-      *reinterpret_cast<u32x4*>(out + c * ld_out + r) = u32x4{w[0], w[1], w[2], w[3]};
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int j = (t >> 4) + 32 * i;
+    const int64_t c = c0 + j, r = r0 + 8 * m;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(tile + j * 64 + ((m ^ (j >> 3)) << 2));
+    if (c < cols && r < rows_pad) *reinterpret_cast<u32x4*>(out + c * ld_out + r) = v;
   }
 }
 
@@ -359,13 +374,14 @@ int launch_transpose(T* out, const T* in, int64_t rows, int64_t rows_pad, int64_
   HK_REQUIRE(cols % 8 == 0 && rows_pad % 8 == 0 && ld_in % 8 == 0 && ld_out % 8 == 0 && aligned_to(in, 16) &&
                  aligned_to(out, 16),
              "transpose: 16-byte rows and chunks expected");
-  const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows_pad, 64));
   if constexpr (sizeof(T) == 4) {
+    const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows_pad, 64));
     hipLaunchKernelGGL(transpose32_kernel, grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out, lim,
                        lim_off);
     return check_launch("transpose32_kernel");
   } else {
-    hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out,
+    const dim3 grid((unsigned)cdiv(cols, 128), (unsigned)cdiv(rows_pad, 128));
+    hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(512), 0, st, out, in, rows, rows_pad, cols, ld_in, ld_out,
                        lim, lim_off);
     return check_launch("transpose_kernel");
   }

@@ -119,6 +119,34 @@ __global__ __launch_bounds__(kThreads) void kl_div_bwd_kernel(T* __restrict__ dy
   }
 }
 
+// The same with one scalar s over a contiguous array of n packs (the usual
+// 'batchmean' / 'sum' / 'mean' call): a flat walk, one 256-lane block a CU, U
+// packs of a lane in flight, the shape of the fastest streaming copy (the
+// per-row walk above runs this 1-read 1-write stream about 10% slower).
+template <typename T, int VEC, bool LOGT, int U = 4>
+__global__ __launch_bounds__(kThreads) void kl_div_bwd_flat_kernel(T* __restrict__ dy, const T* __restrict__ yt,
+                                                                   const float* __restrict__ g, float factor,
+                                                                   int64_t n) {
+  const float s = -g[0] * factor;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  auto scale = [&](const Pack<T, VEC>& v) {
+    float x[VEC];
+    unpack(v, x);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) x[e] = (LOGT ? exp_fast(x[e]) : x[e]) * s;
+    return pack<T, VEC>(x);
+  };
+  int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  for (; i + (U - 1) * stride < n; i += U * stride) {  // whole passes: loads unconditional
+    Pack<T, VEC> v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = load_pack<T, VEC>(yt + (i + u * stride) * VEC);
+#pragma unroll
+    for (int u = 0; u < U; ++u) store_pack<T, VEC>(dy + (i + u * stride) * VEC, scale(v[u]));
+  }
+  for (; i < n; i += stride) store_pack<T, VEC>(dy + i * VEC, scale(load_pack<T, VEC>(yt + i * VEC)));
+}
+
 // JSD(beta) of teacher P = e^Y and student Q = e^X, both log-probabilities:
 // MODE 0 (beta = 0): KL(P||Q) = sum P (Y - X),        dX = -P
 // MODE 1 (beta = 1): KL(Q||P) = sum Q (X - Y),        dX = Q (X - Y + 1)
@@ -444,6 +472,19 @@ int hk_kl_div_bwd(void* dy_pred, const void* y_true, const float* g, int per_row
     constexpr int V = 16 / sizeof(T);
     if (rows == 0 || cols == 0) return HK_OK;
     const bool vec = rows_vec_ok<T>(y_true, ld_true) && rows_vec_ok<T>(dy_pred, ld_out);
+    if (vec && !per_row && ld_true == cols && ld_out == cols) {  // one contiguous stream, one scale
+      const int dev = current_device();
+      const int64_t cus = dev >= 0 && cu_count(dev) > 0 ? cu_count(dev) : 256;
+      const int64_t n = rows * cols / V;
+      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(cus, (n + kThreads - 1) / kThreads)));
+      if (log_target)
+        hipLaunchKernelGGL((kl_div_bwd_flat_kernel<T, V, true>), grid, dim3(kThreads), 0, st, (T*)dy_pred,
+                           (const T*)y_true, g, factor, n);
+      else
+        hipLaunchKernelGGL((kl_div_bwd_flat_kernel<T, V, false>), grid, dim3(kThreads), 0, st, (T*)dy_pred,
+                           (const T*)y_true, g, factor, n);
+      return check_launch("kl_div_bwd_flat_kernel");
+    }
     auto go = [&](auto vc, auto lc) {
       hipLaunchKernelGGL((kl_div_bwd_kernel<T, decltype(vc)::value, decltype(lc)::value>), dim3((unsigned)rows),
                          dim3(kThreads), 0, st, (T*)dy_pred, (const T*)y_true, g, per_row, factor, cols, ld_true,

@@ -284,29 +284,43 @@ __device__ __forceinline__ float target_merge(float M, float R, float xtc, bool 
 // Streaming row log-sum-exp (any length): per-lane online (max, sum), then a
 // block combine. With REST, *rest = 1 - p_target from a second sum that leaves
 // the target column out (see reduce_lane).
+constexpr int kStreamU = 4;  // packs of a lane in flight in the streaming row forms
 template <typename T, int VEC, int BLOCK, bool REST = false>
 __device__ __forceinline__ float row_lse2_stream(const T* __restrict__ row, int n, float c, float* red,
                                                  int target = -1, float* rest = nullptr) {
   float m = -INFINITY, s = 0.f, r = 0.f;
-  for (int col = (int)threadIdx.x * VEC; col < n; col += BLOCK * VEC) {
-    float x[VEC];
-    unpack(load_pack<T, VEC>(row + col), x);
-    float tm = x[0];
+  // kStreamU packs of a lane loaded before any is used (one memory round trip
+  // for up to kStreamU x BLOCK packs), then folded in the same order as one at a time
+  constexpr int U = kStreamU;
+  const int nv = n / VEC;
+  for (int i0 = (int)threadIdx.x; i0 < nv; i0 += BLOCK * U) {
+    Pack<T, VEC> pk[U];
 #pragma unroll
-    for (int e = 1; e < VEC; ++e) tm = fmaxf(tm, x[e]);
-    const float mn = fmaxf(m, tm * c);
-    const float sc = m == -INFINITY ? 0.f : exp2_fast(m - mn);
-    float add = 0.f, add_r = 0.f;
-    const int rel = target - col;
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * BLOCK < nv) pk[u] = load_pack<T, VEC>(row + (i0 + u * BLOCK) * VEC);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float p = exp2_fast(fmaf(x[e], c, -mn));
-      add += p;
-      if constexpr (REST) add_r += e == rel ? 0.f : p;
+    for (int u = 0; u < U; ++u) {
+      const int col = (i0 + u * BLOCK) * VEC;
+      if (col >= n) break;
+      float x[VEC];
+      unpack(pk[u], x);
+      float tm = x[0];
+#pragma unroll
+      for (int e = 1; e < VEC; ++e) tm = fmaxf(tm, x[e]);
+      const float mn = fmaxf(m, tm * c);
+      const float sc = m == -INFINITY ? 0.f : exp2_fast(m - mn);
+      float add = 0.f, add_r = 0.f;
+      const int rel = target - col;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float p = exp2_fast(fmaf(x[e], c, -mn));
+        add += p;
+        if constexpr (REST) add_r += e == rel ? 0.f : p;
+      }
+      s = s * sc + add;
+      if constexpr (REST) r = r * sc + add_r;
+      m = mn;
     }
-    s = s * sc + add;
-    if constexpr (REST) r = r * sc + add_r;
-    m = mn;
   }
   const float M = block_max<BLOCK / kWave>(m, red);
   const float f = (m == -INFINITY) ? 0.f : exp2_fast(m - M);

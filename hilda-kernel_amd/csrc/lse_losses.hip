@@ -403,7 +403,7 @@ __device__ __forceinline__ void lse_rows_resident(int n, float c, int64_t rows, 
 struct RowForm {
   int block, nch;
 };
-constexpr RowForm kRowForms[] = {{256, 1},   {256, 2},   {256, 4},    {256, 8},    {256, 12},   {256, 16},
+constexpr RowForm kRowForms[] = {{256, 1},   {256, 2},   {256, 4},    {256, 8},    {256, 12},   {512, 8},
                                  {512, 12},  {512, 16},  {1024, 12},  {1024, 16},  {1024, 20},  {1024, 24}};
 
 // Vectors per lane that are full in every row a form serves: such a row is
@@ -1273,10 +1273,10 @@ int dispatch_cfg(const RowCfg& c, F&& f) {
       case 4: return f(integral_constant<int, 256>{}, integral_constant<int, 4>{});
       case 8: return f(integral_constant<int, 256>{}, integral_constant<int, 8>{});
       case 12: return f(integral_constant<int, 256>{}, integral_constant<int, 12>{});
-      case 16: return f(integral_constant<int, 256>{}, integral_constant<int, 16>{});
     }
   } else if (c.block == 512) {
     switch (c.nch) {
+      case 8: return f(integral_constant<int, 512>{}, integral_constant<int, 8>{});
       case 12: return f(integral_constant<int, 512>{}, integral_constant<int, 12>{});
       case 16: return f(integral_constant<int, 512>{}, integral_constant<int, 16>{});
     }

@@ -32,7 +32,7 @@ CE_CONFIGS = [
     (8000, BF16),     # 256 x 4
     (12000, BF16),    # 256 x 8
     (20000, BF16),    # 256 x 12
-    (32000, BF16),    # 256 x 16
+    (32000, BF16),    # 512 x 8
     (45000, BF16),    # 512 x 12
     (60000, BF16),    # 512 x 16
     (90000, BF16),    # 1024 x 12
@@ -89,7 +89,7 @@ def test_cross_entropy_row_configs(V, dtype):
 GRPO_CONFIGS = [
     (8000, BF16),     # 256 x 4
     (20000, BF16),    # 256 x 12
-    (32000, BF16),    # 256 x 16
+    (32000, BF16),    # 512 x 8
     (45000, BF16),    # 512 x 12
     (60000, BF16),    # 512 x 16
     (90000, BF16),    # 1024 x 12

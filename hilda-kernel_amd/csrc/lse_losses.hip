@@ -927,7 +927,12 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
       if (l < a.L && threadIdx.x == 0) a.out[b * a.L + l] = GrpoOut{0.f, 0.f, 0.f, 0.f};
     }
   }
-  if constexpr (RESIDENT && GRAD) {
+  if constexpr (RESIDENT && (GRAD || BLOCK < 1024)) {
+    // Without the gradient (256/512 lanes) the same loop minus the stores, the
+    // next row's loads issued right after this row's lane reduction: the same
+    // reduction, exchange and merge as with the gradient, so the losses are
+    // equal bit for bit, and no per-row global load (token record, id logit)
+    // waits behind the row's vector loads.
     // Live rows, pipelined as in the CE kernel: the register refill rides
     // with the gradient stores, the per-row records are scalar loads (the
     // search for the row after next runs at the end of the iteration) and the
@@ -967,54 +972,33 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
       const GrpoTok tk = load_tok(a.tok + cur.tok_i);
       float m, s, xt, M, R, X, rest;
       r.reduce_lane(n, c, id, &m, &s, &xt);
+      if constexpr (!GRAD) {
+        r.opaque();
+        __builtin_amdgcn_sched_barrier(0);  // the refill may not start before the row is reduced (register reuse)
+        if (next.row < rows) r.load(src, n);
+      }
       block_lse2_ms<BLOCK / kWave>(m, s, red, parity, &M, &R, xt, Regs::owns_target(id), &X);
       const float xid = id >= 0 ? X : 0.f;
       const float lse2 = target_merge(M, R, xid * c, id >= 0, &rest);
       parity ^= 1;
-      r.opaque();
+      if constexpr (GRAD) r.opaque();
       const float lse = lse2 * kLn2;
       const float logp = id >= 0 ? xid * a.inv_T - lse : NAN;
       float dlogp;
       const GrpoOut res = grpo_terms(a, tk, lse, logp, &dlogp);
-      // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
-      const float g = -dlogp * tk.gs;
-      T* out = dlogits + row * a.V;
-      r.store_prob_grad_then_load(out, n, c, lse2, g, src);
-      // the id element: (p_id - 1) * g = -(1 - p_id) * g (see reduce_lane)
-      if (Regs::owns_target(id)) out[id] = from_f32<T>(-rest * g);
+      if constexpr (GRAD) {
+        // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
+        const float g = -dlogp * tk.gs;
+        T* out = dlogits + row * a.V;
+        r.store_prob_grad_then_load(out, n, c, lse2, g, src);
+        // the id element: (p_id - 1) * g = -(1 - p_id) * g (see reduce_lane)
+        if (Regs::owns_target(id)) out[id] = from_f32<T>(-rest * g);
+      }
       if (threadIdx.x == 0) a.out[cur.tok_i] = res;
       if (next.row >= rows) break;
       cur = next;
       next = next_live(cur.row + G);
     }
-  } else if constexpr (RESIDENT && BLOCK < 1024) {
-    // forward only: the same (max, sum) arithmetic as the gradient path, so
-    // both give bitwise equal results; the next row loads during the combine
-    auto next_live = [&](int64_t from) {
-      int64_t q = from;
-      GrpoTok t{};
-      while (q < rows && !live(q, &t)) q += G;
-      return q;
-    };
-    struct Ctx {
-      GrpoTok tk;
-      float xid;
-    };
-    auto pre = [&](int64_t row) {
-      const GrpoTok tk = a.tok[token(row)];
-      return Ctx{tk, tk.id >= 0 ? to_f32<T>(logits[row * a.V + tk.id]) : 0.f};
-    };
-    auto emit = [&](int64_t row, float lse2, const Ctx& x) {
-      const float lse = lse2 * kLn2;
-      const float logp = x.tk.id >= 0 ? x.xid * a.inv_T - lse : NAN;
-      float dlogp;
-      const GrpoOut res = grpo_terms(a, x.tk, lse, logp, &dlogp);
-      if (threadIdx.x == 0) a.out[token(row)] = res;
-    };
-    auto target_of = [&](const Ctx& x) { return RowTarget{x.tk.id, x.xid * c}; };
-    lse_rows_resident<T, VEC, NCH, BLOCK>(
-        row_len(a.V), c, rows, red, [&](int64_t row) { return logits + row * a.V; }, next_live, pre, target_of,
-        emit);
   } else {
     // streaming, or forward only on 1024-lane rows: there the refill's extra
     // register pressure spills, so each row loads after the previous one

@@ -2,28 +2,48 @@
 // lm_head GEMMs on MFMA (bf16/fp16, or fp32 for fp32 inputs) with the loss
 // gradient produced chunk by chunk, so the full (BT, V) logits never exist.
 //
-// Every contraction is one "NT" GEMM (gemm_nt.h), C[M,N] = A[M,K] * B[N,K]^T
-// with both operands K-contiguous, the layout the MFMA operand fetch wants:
-//   logits_c = X_c  * W^T          A = X_c  [C,H],  B = W   [V,H]
-//   dX_c     = D_c  * (W^T)^T      A = D_c  [C,V],  B = W^T [H,V]
-//   dW      += D_c^T * X_c          A = D_c^T[V,C],  B = X^T [H,C] (columns of X^T)
-// W^T and X^T are transposed once per call, D_c^T once per chunk (tiled LDS
-// transposes, HBM-bound and small next to the GEMMs). dW is either one GEMM
-// over all rows after the chunk loop (every chunk's D_c^T kept side by side,
-// when that needs no more memory than the alternative) or accumulated in fp32
-// across chunks (the GEMM epilogue reads and writes the accumulator in
-// coalesced 16-byte chunks; the last chunk's epilogue writes the input dtype).
+// Per chunk of C rows (fused_linear_cross_entropy.py:130-161):
+//   logits_c = X_c W^T          into the chunk buffer [C, ldl]
+//   row step                    the loss and, with gradients, D_c over the logits
+//   dX_c     = D_c W            A = D_c [C, V], B = W^T [H, V] or W read MN-contiguous
+//   dW      += D_c^T X_c        A = D_c^T [V, C] or D_c read MN-contiguous, B = X_c^T [H, C]
+//
+// How much memory that takes is a plan (FlPlan), chosen per call from a byte
+// budget by a cost model. The forms, from most to least memory:
+//   * every chunk's D_c^T kept side by side and dW one GEMM over all rows
+//     after the loop (deferred): no dW read-modify-write, a (V, BT) buffer;
+//   * dW accumulated across chunks in an fp32 [V, H] buffer;
+//   * dW accumulated in the output itself (fp32 inputs: an exact fp32 sum;
+//     16-bit inputs: rounded per chunk, as the reference's bf16 addmm does);
+// each with W^T (a weight-sized copy) or W read MN-contiguous by the dX GEMM
+// (ds_read_b64_tr_b16), and D_c^T (a chunk-sized copy) or D_c read
+// MN-contiguous by the dW GEMM. The default budget is what the reference's
+// chunk (fused_linear_cross_entropy.py:112-114: chunk logits about the size of
+// the hidden states) costs, in the leanest form.
 //
 // Rows that need no logits (ignored targets or labels, masked GRPO positions)
-// are compacted away on the device first; the GEMMs, transposes and row
-// kernels read the live count from device memory, so the host never waits.
+// are compacted away on the device first; each chunk gathers its live rows,
+// and the GEMMs, transposes and row kernels read the live count from device
+// memory, so the host never waits.
+//
+// Any H and V: the chunk buffer's row stride is V rounded up to 64 (its
+// columns past V are -inf or zero, see EpiLogits, and zero past the row
+// step's width), hidden rows are gathered into rows of H rounded up to 8
+// (zero filled), the weight is copied once into such rows when H is not a
+// multiple of 8 or it is not 16-byte aligned, and the output epilogues store
+// element by element where a row is not 16-byte aligned.
 #include "hk_common.h"
 #include "hk_internal.h"
 #include "gemm_nt.h"
 #include "../../include/hilda_kernel_amd.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
 #include <type_traits>
+#include <vector>
 
 namespace hk {
 namespace {
@@ -31,10 +51,11 @@ namespace {
 using gemm::f32x4_t;
 struct NoPrior {};
 
-// Stores n (<= 4) fp32 values at p in T, one 8- or 16-byte store when n == 4.
+// n (<= 4) fp32 values stored at p in T: one 8- (16-bit) or 16-byte (fp32)
+// store when n == 4 and vec (the address is aligned for it), else element by element.
 template <typename T>
-__device__ __forceinline__ void store4(T* p, const float* v, int n) {
-  if (n == 4) {
+__device__ __forceinline__ void store4(T* p, const float* v, int n, bool vec) {
+  if (n == 4 && vec) {
     if constexpr (sizeof(T) == 4) *reinterpret_cast<f32x4_t*>(p) = f32x4_t{v[0], v[1], v[2], v[3]};
     else *reinterpret_cast<u32x2*>(p) = u32x2{gemm::pack2<T>(v[0], v[1]), gemm::pack2<T>(v[2], v[3])};
   } else {
@@ -42,100 +63,167 @@ __device__ __forceinline__ void store4(T* p, const float* v, int n) {
   }
 }
 
-// C (T) = acc, in 16-byte chunks (8 columns of a 16-bit type, 4 of fp32).
+// n (<= 4) values of T at p widened to fp32 (zeros past n); one load when n == 4 and vec.
 template <typename T>
-struct EpiStore {
+__device__ __forceinline__ f32x4_t load4(const T* p, int n, bool vec) {
+  f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+  if (n == 4 && vec) {
+    if constexpr (sizeof(T) == 4) {
+      x = *reinterpret_cast<const f32x4_t*>(p);
+    } else {
+      struct alignas(8) Q { T v[4]; };
+      const Q q = *reinterpret_cast<const Q*>(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = to_f32<T>(q.v[e]);
+    }
+  } else {
+    for (int e = 0; e < n; ++e) x[e] = to_f32<T>(p[e]);
+  }
+  return x;
+}
+
+// The logits GEMM's epilogue: C (T) = acc in 16-byte chunks (ldc a multiple of
+// 8, C 16-byte aligned). The chunk that straddles column N is completed with
+// `pad` past N: -inf for the CrossEntropy and GRPO row steps, which then read
+// the row to the next multiple of 16 bytes (a -inf logit has probability 0,
+// so the loss is unchanged and its gradient entry is 0), 0 for the JSD step.
+template <typename T>
+struct EpiLogits {
   using Stage = T;
   using Prior = NoPrior;
   static constexpr bool kReads = false;
   T* C;
-  int64_t ldc;  // a multiple of 8, so full chunks are 16-byte aligned
+  int64_t ldc;
+  float pad;
   __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
   __device__ __forceinline__ void store(int row, int col, const T* v, int n, const Prior&) const {
+    constexpr int E = 16 / (int)sizeof(T);
     T* p = C + (int64_t)row * ldc + col;
-    if (n == 16 / (int)sizeof(T)) {
+    if (n == E) {
       *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(v);
     } else {
-      for (int e = 0; e < n; ++e) p[e] = v[e];
+      const T fill = from_f32<T>(pad);
+      for (int e = 0; e < E; ++e) p[e] = e < n ? v[e] : fill;
     }
   }
 };
 
-// C (T) = acc with GEMM row r stored at row rows[r] of C (the live rows of a
-// compacted operand back in place), in 16-byte chunks.
+// The dX GEMM's epilogue (M = chunk rows, N = the padded hidden size). GEMM row
+// r goes to row rows[r] of C (rows nullable: row r); only columns < cols are
+// stored. Unsplit (the GEMM's split count is 1) it stores the tile; split, split
+// s stores fp32 partial sums at part + (s * m + row) * ld (m the GEMM's bounded
+// row count, ld its N) and splitk_sum_kernel adds them up.
 template <typename T>
-struct EpiScatter {
-  using Stage = T;
+struct EpiDx {
+  using Stage = float;
   using Prior = NoPrior;
   static constexpr bool kReads = false;
   T* C;
-  int64_t ldc;  // a multiple of 8
+  int64_t ldc;
   const int* rows;
+  float* part;
+  int64_t ld;   // a multiple of 4
+  int cols;
+  bool vec;     // C rows 8-byte (16-bit) / 16-byte (fp32) aligned at every 4th column
+  int split = 0, nsplit = 1, m = 0;
+  __device__ __forceinline__ void set_split(int s, int ns, int bounded_m) {
+    split = s;
+    nsplit = ns;
+    m = bounded_m;
+  }
   __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
-  __device__ __forceinline__ void store(int row, int col, const T* v, int n, const Prior&) const {
-    T* p = C + (int64_t)rows[row] * ldc + col;
-    if (n == 16 / (int)sizeof(T)) {
-      *reinterpret_cast<u32x4*>(p) = *reinterpret_cast<const u32x4*>(v);
+  __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior&) const {
+    if (nsplit == 1) {
+      n = min(n, cols - col);
+      if (n > 0) store4<T>(C + (int64_t)(rows ? rows[row] : row) * ldc + col, v, n, vec);
+      return;
+    }
+    float* p = part + ((int64_t)split * m + row) * ld + col;
+    if (n == 4) {
+      *reinterpret_cast<f32x4_t*>(p) = f32x4_t{v[0], v[1], v[2], v[3]};
     } else {
       for (int e = 0; e < n; ++e) p[e] = v[e];
     }
   }
 };
 
-// fp32 accumulator across calls, 4 columns per chunk; the last call writes T.
-// MODE 0: acc = v; 1: acc += v; 2: out = acc + v
+// The dW GEMM's epilogue (M = vocabulary rows, N = the padded hidden size);
+// rows < rows_lim and columns < cols_lim are kept. MODE:
+//   0: out = v                       (one chunk, or the deferred GEMM)
+//   1: out = out + v                 (accumulation in the output, rounded per chunk)
+//   2: acc = v,  3: acc += v         (the fp32 accumulator, chunks before the last)
+//   4: out = acc + v                 (the last chunk)
 template <typename T, int MODE>
-struct EpiAccum {
+struct EpiDw {
   using Stage = float;
   using Prior = f32x4_t;
-  static constexpr bool kReads = MODE != 0;
-  float* acc;
+  static constexpr bool kReads = MODE == 1 || MODE == 3 || MODE == 4;
   T* out;
-  int64_t ld;  // a multiple of 8
+  int64_t ldo;
+  float* acc;
+  int64_t lda;  // a multiple of 4
+  int rows_lim, cols_lim;
+  bool vec;     // out rows aligned for 4-element stores
   __device__ __forceinline__ Prior load(int row, int col, int n) const {
-    const float* p = acc + (int64_t)row * ld + col;
+    if (row >= rows_lim || col >= cols_lim) return Prior{0.f, 0.f, 0.f, 0.f};
+    n = min(n, cols_lim - col);
+    if constexpr (MODE == 1) return load4<T>(out + (int64_t)row * ldo + col, n, vec);
+    const float* p = acc + (int64_t)row * lda + col;
     if (n == 4) return *reinterpret_cast<const f32x4_t*>(p);
     Prior x = {0.f, 0.f, 0.f, 0.f};
     for (int e = 0; e < n; ++e) x[e] = p[e];
     return x;
   }
   __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior& x) const {
-    const int64_t o = (int64_t)row * ld + col;
+    if (row >= rows_lim || col >= cols_lim) return;
+    n = min(n, cols_lim - col);
     float r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = MODE == 0 ? v[e] : x[e] + v[e];
-    if constexpr (MODE == 2) {
-      store4<T>(out + o, r, n);
-    } else {
+    for (int e = 0; e < 4; ++e) r[e] = kReads ? x[e] + v[e] : v[e];
+    if constexpr (MODE == 2 || MODE == 3) {
+      float* p = acc + (int64_t)row * lda + col;
       if (n == 4) {
-        *reinterpret_cast<f32x4_t*>(acc + o) = f32x4_t{r[0], r[1], r[2], r[3]};
+        *reinterpret_cast<f32x4_t*>(p) = f32x4_t{r[0], r[1], r[2], r[3]};
       } else {
-        for (int e = 0; e < n; ++e) acc[o + e] = r[e];
+        for (int e = 0; e < n; ++e) p[e] = r[e];
       }
+    } else {
+      store4<T>(out + (int64_t)row * ldo + col, r, n, vec);
     }
   }
 };
 
-// n16 16-byte words of zeros
-__global__ __launch_bounds__(256) void zero16_kernel(u32x4* __restrict__ p, int64_t n16) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0, 0, 0, 0};
-}
-
-// Compacted rows (rows of n16 16-byte words): out[i] = in[rowmap[i]] for
-// i < *n_live, zero rows for i in [*n_live, rows).
-__global__ __launch_bounds__(256) void gather_rows_kernel(u32x4* __restrict__ out, const u32x4* __restrict__ in,
+// Rows [0, rows) of out (row stride ldo, width wo; 16-byte aligned rows when
+// VEC): row i is input row src(i) = rowmap[row0 + i] (rowmap nullable: row0 + i)
+// for i below the live rows (*n_live - row0, or live_rows - row0 without
+// n_live), its w elements followed by zeros up to wo; the rows after are zero.
+// VEC: the input rows are 16-byte aligned with w a multiple of 16 bytes.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void gather_rows_kernel(T* __restrict__ out, int64_t ldo, int64_t wo,
+                                                          const T* __restrict__ in, int64_t ldi, int64_t w,
                                                           const int* __restrict__ rowmap,
-                                                          const int* __restrict__ n_live, int64_t rows, int64_t n16) {
-  const int64_t n = *n_live;
+                                                          const int* __restrict__ n_live, int64_t live_rows,
+                                                          int64_t row0, int64_t rows) {
+  constexpr int E = 16 / (int)sizeof(T);
+  const int64_t lv = n_live ? (int64_t)*n_live : live_rows;
+  const int64_t live = std::max<int64_t>(0, std::min<int64_t>(rows, lv - row0));
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    u32x4* o = out + r * n16;
-    if (r < n) {
-      const u32x4* src = in + (int64_t)rowmap[r] * n16;
-      for (int64_t w = threadIdx.x; w < n16; w += 256) o[w] = src[w];
-    } else {
-      for (int64_t w = threadIdx.x; w < n16; w += 256) o[w] = u32x4{0, 0, 0, 0};
+    T* o = out + r * ldo;
+    int64_t c0 = 0;
+    if (r < live) {
+      const T* s = in + (int64_t)(rowmap ? rowmap[row0 + r] : row0 + r) * ldi;
+      if constexpr (VEC) {
+        for (int64_t j = threadIdx.x; j < w / E; j += 256)
+          reinterpret_cast<u32x4*>(o)[j] = reinterpret_cast<const u32x4*>(s)[j];
+      } else {
+        for (int64_t j = threadIdx.x; j < w; j += 256) o[j] = s[j];
+      }
+      c0 = w;
     }
+    // zeros from c0 (a row start or w) to wo: elements up to a 16-byte boundary, then 16-byte stores
+    const int64_t cv = std::min<int64_t>(wo, (c0 + E - 1) / E * E);
+    for (int64_t j = c0 + threadIdx.x; j < cv; j += 256) o[j] = from_f32<T>(0.f);
+    for (int64_t j = cv / E + threadIdx.x; j < wo / E; j += 256) reinterpret_cast<u32x4*>(o)[j] = u32x4{0, 0, 0, 0};
   }
 }
 
@@ -152,18 +240,37 @@ __global__ __launch_bounds__(256) void gather_ce_kernel(int64_t* __restrict__ t_
   }
 }
 
+// Columns [c0, c1) of `rows` rows (row stride ld) set to zero.
+template <typename T>
+__global__ __launch_bounds__(256) void zero_cols_kernel(T* __restrict__ p, int64_t ld, int64_t c0, int64_t c1,
+                                                        int64_t rows) {
+  const int64_t w = c1 - c0, n = rows * w;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / w;
+    p[r * ld + c0 + (i - r * w)] = from_f32<T>(0.f);
+  }
+}
+
 // Rows of the original order after a compacted pass: dead rows (inv[r] < 0)
-// get a zero dX row (when dX) and loss 0; live rows take their loss from the
-// compacted losses (when loss_rows).
-__global__ __launch_bounds__(256) void finish_rows_kernel(u32x4* __restrict__ dX, int64_t n16,
+// get a zero dX row of H elements (when dX) and loss 0; live rows take their
+// loss from the compacted losses (when loss_rows). VEC: dX rows are whole
+// 16-byte aligned vectors.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void finish_rows_kernel(T* __restrict__ dX, int64_t H,
                                                           float* __restrict__ loss_rows,
                                                           const float* __restrict__ loss_c,
                                                           const int* __restrict__ inv, int64_t rows) {
+  constexpr int E = 16 / (int)sizeof(T);
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const int k = inv[r];
     if (loss_rows && threadIdx.x == 0) loss_rows[r] = k >= 0 ? loss_c[k] : 0.f;
-    if (dX && k < 0)
-      for (int64_t w = threadIdx.x; w < n16; w += 256) dX[r * n16 + w] = u32x4{0, 0, 0, 0};
+    if (dX && k < 0) {
+      if constexpr (VEC) {
+        for (int64_t w = threadIdx.x; w < H / E; w += 256) reinterpret_cast<u32x4*>(dX + r * H)[w] = u32x4{0, 0, 0, 0};
+      } else {
+        for (int64_t w = threadIdx.x; w < H; w += 256) dX[r * H + w] = from_f32<T>(0.f);
+      }
+    }
   }
 }
 
@@ -273,98 +380,51 @@ __global__ __launch_bounds__(256) void transpose32_kernel(float* __restrict__ ou
   }
 }
 
-// The dX GEMM's epilogue when it may split K. Unsplit (the GEMM's split count
-// is 1), it stores the tile like EpiScatter / EpiStore, 4 columns a chunk; split,
-// split s stores fp32 partial sums at part + (s * m + row) * ld, m the GEMM's
-// bounded row count, and splitk_sum_kernel adds them up.
-template <typename T>
-struct EpiDx {
-  using Stage = float;
-  using Prior = NoPrior;
-  static constexpr bool kReads = false;
-  T* C;
-  int64_t ldc;       // a multiple of 8
-  const int* rows;   // nullable: GEMM row r goes to row rows[r] of C
-  float* part;
-  int64_t ld;        // a multiple of 4
-  int split = 0, nsplit = 1, m = 0;
-  __device__ __forceinline__ void set_split(int s, int ns, int bounded_m) {
-    split = s;
-    nsplit = ns;
-    m = bounded_m;
-  }
-  __device__ __forceinline__ Prior load(int, int, int) const { return {}; }
-  __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior&) const {
-    if (nsplit == 1) {
-      store4<T>(C + (int64_t)(rows ? rows[row] : row) * ldc + col, v, n);
-      return;
-    }
-    float* p = part + ((int64_t)split * m + row) * ld + col;
-    if (n == 4) {
-      *reinterpret_cast<f32x4_t*>(p) = f32x4_t{v[0], v[1], v[2], v[3]};
-    } else {
-      for (int e = 0; e < n; ++e) p[e] = v[e];
-    }
-  }
-};
-
-// C[rows ? rows[r] : r] = sum over the splits of the partials (rounded once to
-// T), 8 columns a thread, for r below the device-bounded M. The split count is
-// the GEMM's own (auto_splits of its bounded tiles); unsplit, the GEMM stored
-// C itself and this returns at once.
+// C[rows ? rows[r] : r, 0:cols) = sum over the splits of the partials (rounded
+// once to T), 4 columns a thread, for r below the device-bounded M. The split
+// count is the GEMM's own (auto_splits of its bounded tiles); unsplit, the
+// GEMM stored C itself and this returns at once. Partials have row stride N.
 template <typename T>
 __global__ __launch_bounds__(256) void splitk_sum_kernel(T* __restrict__ C, int64_t ldc, const int* __restrict__ rows,
                                                          const float* __restrict__ part, int M, int N, int KT,
-                                                         int max_s, const int* lim, int lim_off) {
+                                                         int max_s, const int* lim, int lim_off, int cols, int vec) {
   if (lim) M = min(M, max(0, *lim - lim_off));
   const int S = gemm::auto_splits(((M + 255) / 256) * ((N + 255) / 256), KT, max_s);
   if (S == 1) return;
-  const int n8 = N / 8;
-  const int64_t total = (int64_t)M * n8, stride = (int64_t)M * N;
+  const int n4 = (cols + 3) / 4;
+  const int64_t total = (int64_t)M * n4, stride = (int64_t)M * N;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int r = (int)(i / n8), c = (int)(i - (int64_t)r * n8) * 8;
+    const int r = (int)(i / n4), c = (int)(i - (int64_t)r * n4) * 4;
     const float* p = part + (int64_t)r * N + c;
-    f32x4_t a = *reinterpret_cast<const f32x4_t*>(p), b = *reinterpret_cast<const f32x4_t*>(p + 4);
-    for (int s = 1; s < S; ++s) {
-      a += *reinterpret_cast<const f32x4_t*>(p + s * stride);
-      b += *reinterpret_cast<const f32x4_t*>(p + s * stride + 4);
-    }
-    T* o = C + (int64_t)(rows ? rows[r] : r) * ldc + c;
-    const float va[4] = {a[0], a[1], a[2], a[3]}, vb[4] = {b[0], b[1], b[2], b[3]};
-    store4<T>(o, va, 4);
-    store4<T>(o + 4, vb, 4);
+    f32x4_t a = *reinterpret_cast<const f32x4_t*>(p);
+    for (int s = 1; s < S; ++s) a += *reinterpret_cast<const f32x4_t*>(p + s * stride);
+    const float v[4] = {a[0], a[1], a[2], a[3]};
+    store4<T>(C + (int64_t)(rows ? rows[r] : r) * ldc + c, v, min(4, cols - c), vec != 0);
   }
 }
 
-// lim (nullable): a device-side bound on M (or K with lim_k), see gemm::Shape
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
 template <typename T, class Epi>
 int launch_gemm(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
-                const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1) {
-  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st, lim, lim_off, lim_k, ksplit);
+                const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1, int kb = 0) {
+  return gemm::launch<T>(A, B, M, N, K, lda, ldb, epi, st, lim, lim_off, lim_k, ksplit, 0, kb);
 }
 
-// Most K splits the dX GEMM (M = chunk rows, N = H, K = V) may take; the
-// kernel picks auto_splits() of the tiles left after the live-row bound, so a
-// short or mostly ignored chunk (a 2048-row chunk at H = 4096 is 128 output
-// tiles) still fills the chip. 1: never split.
-// bk: the GEMM's stage depth (K elements per K tile) for the input type.
-int dx_max_splits(int64_t H, int64_t V, int bk) {
-  if (V % bk != 0 || H % 8 != 0) return 1;
-  return (int)std::min<int64_t>(8, V / bk / 16);
-}
-
-// fp32 partial-sum bytes the dX GEMM of a chunk of up to C rows can need: the
-// largest splits x rows over the row counts it may be cut to.
-size_t dx_part_bytes(int64_t C, int64_t H, int64_t V, int bk) {
-  const int smax = dx_max_splits(H, V, bk);
-  if (smax <= 1) return 0;
-  size_t best = 0;
-  const int64_t ntn = cdiv(H, 256), kt = V / bk;
-  for (int64_t mt = 1; mt <= cdiv(C, 256); ++mt) {
-    const int s = gemm::auto_splits((int)(mt * ntn), (int)kt, smax);
-    if (s > 1) best = std::max(best, (size_t)s * (size_t)std::min<int64_t>(C, mt * 256) * H * 4);
+// An MN-contiguous operand (16-bit inputs only: the plans never take one for fp32).
+template <typename T, bool AMN, bool BMN, class Epi>
+int launch_gemm_mn(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
+                   const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1, int kb = 0,
+                   int ka = 0) {
+  if constexpr (sizeof(T) == 2) {
+    return gemm::launch<T, gemm::CfgFor<T>, AMN, BMN>(A, B, M, N, K, lda, ldb, epi, st, lim, lim_off, lim_k, ksplit,
+                                                      ka, kb);
+  } else {
+    set_error("internal: an MN-contiguous fp32 operand");
+    return HK_EINVAL;
   }
-  return best;
 }
 
 template <typename T>
@@ -388,6 +448,8 @@ int launch_transpose(T* out, const T* in, int64_t rows, int64_t rows_pad, int64_
 }
 
 int64_t pad8(int64_t x) { return (x + 7) & ~(int64_t)7; }
+int64_t pad64(int64_t x) { return (x + 63) & ~(int64_t)63; }
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Input dtypes of the fused-linear ops: bf16 and fp16 (16-bit MFMA) and fp32 (fp32 MFMA).
 bool fl_dtype_ok(int dt) { return dt == HK_BF16 || dt == HK_F16 || dt == HK_F32; }
@@ -407,97 +469,29 @@ int fl_dispatch(int dt, F&& f) {
 // large power-of-two offset.
 int64_t ld_t(int64_t k) { return pad8(k) + 64; }
 
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-struct FlceLayout {
-  size_t wt, xt, lg, dt, dwacc, nvalid, extra, total;
-  int ksplit;   // most K splits of the dX GEMM (dx_max_splits), their fp32 partial sums at `part`
-  size_t part;
-  bool defer;  // the whole D^T [V, BTp] is kept and dW is one GEMM after the chunk loop
-  // the compaction of the live rows: row map, inverse map, live count, compacted hidden rows;
-  // for CrossEntropy also the compacted targets, row scales and losses
-  size_t rowmap, inv, nlive, xc, tc, sc, lc;
-};
-
-// extra: bytes for the row step's own scratch (16-byte aligned); ce: room for the
-// compacted CrossEntropy row inputs and outputs
-FlceLayout flce_layout(int64_t BT, int64_t H, int64_t V, int64_t chunk, int es, bool grad, size_t extra = 0,
-                       bool ce = false) {
-  FlceLayout L{};
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off += align256(bytes);
-    return o;
-  };
-  L.nvalid = take(256);
-  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
-  L.nlive = take(256);
-  L.rowmap = take(bt * 4);
-  L.inv = take(bt * 4);
-  L.xc = take((size_t)pad8(BT) * H * es);
-  if (ce) {
-    L.tc = take(bt * 8);
-    L.sc = take(bt * 4);
-    L.lc = take(bt * 4);
-  }
-  L.lg = take((size_t)chunk * V * es);
-  if (grad) {
-    L.wt = take((size_t)H * V * es);
-    L.xt = take((size_t)H * ld_t(BT) * es);
-    // Several chunks: keep every chunk's D^T and run dW as one GEMM over K = BT
-    // (no fp32 accumulator round trips) when that takes no more memory than
-    // one chunk's D^T plus the fp32 accumulator; otherwise accumulate per chunk.
-    L.defer = BT > chunk && pad8(BT) <= pad8(chunk) + 2 * H;
-    if (L.defer) {
-      L.dt = take((size_t)V * ld_t(BT) * es);
-    } else {
-      L.dt = take((size_t)V * ld_t(chunk) * es);
-      L.dwacc = BT > chunk ? take((size_t)V * H * 4) : 0;
-    }
-    const int bk = es == 4 ? gemm::F32Cfg::BK : gemm::DefaultCfg::BK;
-    const size_t pb = dx_part_bytes(chunk, H, V, bk);
-    L.ksplit = pb ? dx_max_splits(H, V, bk) : 1;
-    L.part = pb ? take(pb) : 0;
-  }
-  L.extra = extra ? take(extra) : 0;
-  L.total = off;
-  return L;
-}
-
-// FusedLinearJSD: the shared chunk engine's workspace, then the JSD pieces:
-// per-row losses (compacted order with labels), the teacher logits chunk, and
-// with labels the compacted teacher rows and labels.
-struct FljsdLayout {
-  FlceLayout base;
-  size_t lc, lt, xtc, labc, total;
-};
-
-FljsdLayout fljsd_layout(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int es, bool grad) {
-  FljsdLayout L{};
-  L.base = flce_layout(BT, H, V, chunk, es, grad);
-  size_t off = L.base.total;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off += align256(bytes);
-    return o;
-  };
-  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
-  L.lc = take(bt * 4);
-  L.lt = take((size_t)chunk * V * es);
-  L.xtc = take((size_t)pad8(BT) * Ht * es);
-  L.labc = take(bt * 8);
-  L.total = off;
-  return L;
-}
-
-// The compacted hidden rows (live rows in order, zero rows after them).
+// Rows of out from rows of in (see gather_rows_kernel).
 template <typename T>
-int gather_rows(T* Xc, const T* X, const int* rowmap, const int* n_live, int64_t BT, int64_t H, hipStream_t st) {
-  if (BT == 0) return HK_OK;
-  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<int64_t>(BT, 4096)), dim3(256), 0, st, (u32x4*)Xc,
-                     (const u32x4*)X, rowmap, n_live, BT, H * (int64_t)sizeof(T) / 16);
+int gather_rows(T* out, int64_t ldo, int64_t wo, const T* in, int64_t ldi, int64_t w, const int* rowmap,
+                const int* n_live, int64_t live_rows, int64_t row0, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return HK_OK;
+  constexpr int E = 16 / (int)sizeof(T);
+  const dim3 grid((unsigned)std::min<int64_t>(rows, 8192));
+  if (w % E == 0 && ldi % E == 0 && aligned_to(in, 16))
+    hipLaunchKernelGGL((gather_rows_kernel<T, true>), grid, dim3(256), 0, st, out, ldo, wo, in, ldi, w, rowmap, n_live,
+                       live_rows, row0, rows);
+  else
+    hipLaunchKernelGGL((gather_rows_kernel<T, false>), grid, dim3(256), 0, st, out, ldo, wo, in, ldi, w, rowmap,
+                       n_live, live_rows, row0, rows);
   return check_launch("gather_rows_kernel");
+}
+
+template <typename T>
+int zero_cols(T* p, int64_t ld, int64_t c0, int64_t c1, int64_t rows, hipStream_t st) {
+  if (c1 <= c0 || rows <= 0) return HK_OK;
+  const int64_t n = (c1 - c0) * rows;
+  hipLaunchKernelGGL((zero_cols_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 4096)), dim3(256), 0, st, p,
+                     ld, c0, c1, rows);
+  return check_launch("zero_cols_kernel");
 }
 
 // Zero dX rows of the dead rows and, with loss_rows, the losses back in the original order.
@@ -505,113 +499,433 @@ template <typename T>
 int finish_rows(T* dX, float* loss_rows, const float* loss_c, const int* inv, int64_t BT, int64_t H,
                 hipStream_t st) {
   if (BT == 0 || (!dX && !loss_rows)) return HK_OK;
-  hipLaunchKernelGGL(finish_rows_kernel, dim3((unsigned)std::min<int64_t>(BT, 4096)), dim3(256), 0, st, (u32x4*)dX,
-                     H * (int64_t)sizeof(T) / 16, loss_rows, loss_c, inv, BT);
+  constexpr int E = 16 / (int)sizeof(T);
+  const dim3 grid((unsigned)std::min<int64_t>(BT, 4096));
+  if (!dX || (H % E == 0 && aligned_to(dX, 16)))
+    hipLaunchKernelGGL((finish_rows_kernel<T, true>), grid, dim3(256), 0, st, dX, H, loss_rows, loss_c, inv, BT);
+  else
+    hipLaunchKernelGGL((finish_rows_kernel<T, false>), grid, dim3(256), 0, st, dX, H, loss_rows, loss_c, inv, BT);
   return check_launch("finish_rows_kernel");
 }
 
-// Rows per chunk: a multiple of 8 (chunk starts stay 16-byte aligned in X^T), at most BT.
-int64_t flce_chunk(int64_t BT, int64_t chunk) {
-  if (chunk <= 0) chunk = 8192;
-  chunk = std::max<int64_t>(8, chunk & ~(int64_t)7);
-  return std::min<int64_t>(chunk, BT > 0 ? BT : 1);
+// ---------------------------------------------------------------------------
+// The plan
+// ---------------------------------------------------------------------------
+
+enum DwMode { kDwDefer = 0, kDwAcc = 1, kDwOut = 2 };
+
+// What a fused-linear op asks of the chunk engine.
+struct FlShape {
+  int64_t BT, H, V;
+  int es;
+  bool grad;
+  bool compact;        // live rows compacted through a row map (CE, GRPO, JSD with labels)
+  bool x_ok;           // hidden rows readable in place: 16-byte aligned, H a multiple of 8
+  bool w_ok;           // weight rows readable in place: the same for W
+  bool ce;             // room for the compacted CrossEntropy targets, row scales and losses
+  size_t fixed_extra;  // the row step's own scratch, bytes
+  size_t row_extra;    // and per chunk row
+  int64_t chunk_cap;   // rows per chunk at most (<= 0: no cap below 8192)
+};
+
+struct FlPlan {
+  int64_t C = 0, nch = 0;
+  int64_t Hp = 0;   // H rounded up to 8: the hidden rows' width in the GEMMs
+  int64_t V8 = 0;   // V rounded up to 8: rows of D^T, M of an MN-contiguous dW GEMM
+  int64_t Vr = 0;   // the CE / GRPO row steps' width: V rounded up to a 16-byte multiple
+  int64_t ldl = 0;  // chunk buffer row stride: V rounded up to 64 (the dX GEMM's K)
+  bool gather = false, wpad = false, wt = false, dt = false;
+  int dw = kDwOut;
+  int ksplit = 1;   // most K splits of the dX GEMM
+  size_t nvalid = 0, nlive = 0, rowmap = 0, inv = 0, tc = 0, sc = 0, lc = 0;
+  size_t xg = 0, xt = 0, lg = 0, wtp = 0, wp = 0, dtp = 0, acc = 0, part = 0, extra = 0, total = 0;
+  double cost = 0;
+};
+
+int dx_bk(int es) { return es == 4 ? gemm::F32Cfg::BK : gemm::DefaultCfg::BK; }
+
+// fp32 partial-sum bytes the dX GEMM of a chunk of up to C rows can need with at
+// most smax splits: the largest splits x rows over the row counts it may be cut to.
+size_t dx_part_bytes(int64_t C, int64_t Hp, int64_t ldl, int bk, int smax) {
+  if (smax <= 1) return 0;
+  size_t best = 0;
+  const int64_t ntn = cdiv(Hp, 256), kt = ldl / bk;
+  for (int64_t mt = 1; mt <= cdiv(C, 256); ++mt) {
+    const int s = gemm::auto_splits((int)(mt * ntn), (int)kt, smax);
+    if (s > 1) best = std::max(best, (size_t)s * (size_t)std::min<int64_t>(C, mt * 256) * Hp * 4);
+  }
+  return best;
 }
 
-// The chunked lm_head shared by the fused-linear losses. Per chunk of C rows:
-// logits_c = X_c W^T into the chunk buffer; row_step(Lg, r0, cs) produces the
-// row losses and, with gradients, the dlogits D_c written over the logits;
-// then dX_c = D_c W, and dW = sum_c D_c^T X_c either as one GEMM over all rows
-// after the loop (the chunks' D_c^T side by side, lay.defer) or per chunk into
-// an fp32 accumulator, the result rounded once into dWo. X [BT, H] and W [V, H]
-// are K-contiguous.
+// The workspace layout of one candidate (C rows a chunk, the forms, the split cap).
+FlPlan fl_layout(const FlShape& s, int64_t C, bool wt, bool dt, int dw, int smax) {
+  FlPlan p;
+  p.C = C;
+  p.nch = s.BT > 0 ? cdiv(s.BT, C) : 0;
+  p.Hp = pad8(s.H);
+  p.V8 = pad8(s.V);
+  p.Vr = (s.V + 16 / s.es - 1) / (16 / s.es) * (16 / s.es);
+  p.ldl = pad64(s.V);
+  p.gather = s.compact || !s.x_ok;
+  p.wpad = !s.w_ok;
+  p.wt = s.grad && wt;
+  p.dt = s.grad && dt;
+  p.dw = dw;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t es = (size_t)s.es, bt = (size_t)std::max<int64_t>(s.BT, 1);
+  p.nvalid = take(256);
+  p.nlive = take(256);
+  if (s.compact) {
+    p.rowmap = take(bt * 4);
+    p.inv = take(bt * 4);
+  }
+  if (s.ce) {
+    p.tc = take(bt * 8);
+    p.sc = take(bt * 4);
+    p.lc = take(bt * 4);
+  }
+  p.lg = take((size_t)C * p.ldl * es);
+  if (p.gather) p.xg = take((size_t)C * p.Hp * es);
+  if (p.wpad) p.wp = take((size_t)s.V * p.Hp * es);
+  if (s.grad) {
+    const bool defer = dw == kDwDefer;
+    p.xt = take((size_t)p.Hp * ld_t(defer ? s.BT : C) * es);
+    if (p.wt) p.wtp = take((size_t)p.Hp * p.ldl * es);
+    if (p.dt) p.dtp = take((size_t)p.V8 * ld_t(defer ? s.BT : C) * es);
+    if (dw == kDwAcc) p.acc = take((size_t)s.V * p.Hp * 4);
+    const size_t pb = dx_part_bytes(C, p.Hp, p.ldl, dx_bk(s.es), smax);
+    p.ksplit = pb ? smax : 1;
+    p.part = pb ? take(pb) : 0;
+  }
+  p.extra = take(s.fixed_extra + (size_t)C * s.row_extra);
+  p.total = off;
+  return p;
+}
+
+// Modelled time (seconds) of a candidate: GEMMs at a kk-kernel rate, 15% more
+// for a GEMM with an MN-contiguous operand, tile waste of a short chunk, a dX
+// GEMM that leaves CUs idle, and the HBM bytes of the transposes, the dW
+// read-modify-writes, the split partials and the gathers, plus launches.
+double fl_cost(const FlShape& s, const FlPlan& p) {
+  const double Rg = 1.25e15, Rm = 5.0e12, pen = 1.15, launch = 5e-6;
+  const double es = s.es, BT = (double)s.BT, Hp = (double)p.Hp, V = (double)s.V;
+  const double F = 2.0 * BT * Hp * V;
+  const double q = (double)(cdiv(p.C, 256) * 256) / (double)p.C;
+  const double nch = (double)p.nch;
+  double t = F / Rg * q + nch * 6 * launch;
+  if (p.gather) t += 2.0 * es * BT * Hp / Rm;
+  if (p.wpad) t += 2.0 * es * V * Hp / Rm;
+  if (s.grad) {
+    const int64_t tiles = cdiv(p.C, 256) * cdiv(p.Hp, 256);
+    const int sp = gemm::auto_splits((int)tiles, (int)(p.ldl / dx_bk(s.es)), p.ksplit);
+    const double util = std::min(1.0, (double)(tiles * sp) / 256.0);
+    t += F / Rg * q / util * (p.wt ? 1.0 : pen);
+    if (sp > 1) t += nch * 2.0 * sp * (double)p.C * Hp * 4 / Rm;
+    t += F / Rg * (p.dt ? 1.0 : pen);
+    double rmw = es * V * Hp;
+    if (p.dw == kDwAcc && p.nch > 1) rmw = 8.0 * V * Hp * (nch - 1) + es * V * Hp;
+    if (p.dw == kDwOut) rmw = es * V * Hp * (2 * nch - 1);
+    t += rmw / Rm;
+    if (p.wt) t += 2.0 * es * V * Hp / Rm;
+    if (p.dt) t += 2.0 * es * BT * (double)p.V8 / Rm;
+    t += 2.0 * es * BT * Hp / Rm + nch * 4 * launch;
+  }
+  return t;
+}
+
+// The reference's chunk rule (fused_linear_cross_entropy.py:112-114): chunk
+// logits about the size of the hidden states; at least 64 and at most 8192 rows.
+int64_t ref_chunk(int64_t BT, int64_t H, int64_t V) {
+  const int64_t per = std::max<int64_t>(1, cdiv(BT, cdiv(V, H)));
+  int64_t c = 1;
+  while (c < per) c <<= 1;
+  return std::min<int64_t>(8192, std::max<int64_t>(64, c));
+}
+
+// Candidates in order of preference for a given chunk size (the leanest last).
+template <typename F>
+void fl_forms(const FlShape& s, int64_t nch, F&& f) {
+  if (!s.grad) {
+    f(false, false, kDwOut);
+    return;
+  }
+  const bool mn_ok = s.es == 2;  // MN-contiguous operands are 16-bit only
+  for (int dw : {kDwDefer, kDwAcc, kDwOut}) {
+    if (dw == kDwDefer && nch < 2) continue;
+    if (dw == kDwAcc && (nch < 2 || s.es == 4)) continue;  // fp32: the output is the fp32 accumulator
+    for (int wt = 1; wt >= 0; --wt)
+      for (int dt = 1; dt >= 0; --dt) {
+        if ((!wt || !dt) && !mn_ok) continue;
+        if (dw == kDwDefer && !dt) continue;
+        f(wt != 0, dt != 0, dw);
+      }
+  }
+}
+
+// A debugging override of the form (like MIOpen's MIOPEN_DEBUG_* variables):
+// HILDA_FL_FORM="<dw>,<w>,<d>" with dw one of defer / acc / out, w one of wt /
+// wmn, d one of dt / dmn restricts the plan to that form (the chunk still from
+// the budget). Returns false when unset; *bad when it does not parse.
+bool forced_form(int* dw, bool* wt, bool* dt, bool* bad) {
+  const char* e = std::getenv("HILDA_FL_FORM");
+  *bad = false;
+  if (!e || !*e) return false;
+  char a[16] = {0}, b[16] = {0}, c[16] = {0};
+  if (std::sscanf(e, "%15[^,],%15[^,],%15s", a, b, c) != 3) {
+    *bad = true;
+    return true;
+  }
+  const std::string sa(a), sb(b), sc(c);
+  *dw = sa == "defer" ? kDwDefer : sa == "acc" ? kDwAcc : sa == "out" ? kDwOut : -1;
+  *wt = sb == "wt";
+  *dt = sc == "dt";
+  *bad = *dw < 0 || (sb != "wt" && sb != "wmn") || (sc != "dt" && sc != "dmn");
+  return true;
+}
+
+// Default budget floor: below this much chunk memory there is nothing worth
+// saving, and small problems then run in one chunk (or with an fp32 dW
+// accumulator). 40 MiB keeps the reference's tightest memory config
+// (bench_fused_linear_ce.py:270-274: N 4096, V 128256, fp16) 47.7% below the
+// unfused path, the low end of the reference's claim (README.md:42).
+constexpr size_t kSmallWorkspace = (size_t)40 << 20;
+
+// dW summed in fp32 (or computed whole): every form but accumulation in a
+// 16-bit output over several chunks.
+bool exact_dw(const FlShape& s, const FlPlan& p) { return !s.grad || p.dw != kDwOut || p.nch <= 1 || s.es == 4; }
+
+// The plan for a byte budget: budget == 0 the default (at most the larger of
+// kSmallWorkspace and what the reference's chunk costs in the leanest form),
+// budget < 0 unlimited, else at most `budget` bytes. Within the budget: the
+// fastest candidate by fl_cost whose dW is summed in fp32; only when none
+// fits, the fastest one that accumulates dW in the 16-bit output (the
+// reference's arithmetic, fused_linear_cross_entropy.py:161). HK_EINVAL when
+// nothing fits.
+int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
+  int f_dw = 0;
+  bool f_wt = false, f_dt = false, f_bad = false;
+  const bool forced = s.grad && forced_form(&f_dw, &f_wt, &f_dt, &f_bad);
+  HK_REQUIRE(!f_bad, "HILDA_FL_FORM: expected <defer|acc|out>,<wt|wmn>,<dt|dmn>");
+  const int64_t cmax_rows = std::min<int64_t>(8192, s.chunk_cap > 0 ? s.chunk_cap : 8192);
+  const int64_t cmax = std::max<int64_t>(8, std::min<int64_t>(cmax_rows & ~(int64_t)7, pad8(std::max<int64_t>(s.BT, 1))));
+  const int smax_full = s.grad ? (int)std::max<int64_t>(1, std::min<int64_t>(8, pad64(s.V) / dx_bk(s.es) / 16)) : 1;
+  auto lean = [&](int64_t C, int sm) {
+    const bool mn_ok = s.es == 2;
+    return fl_layout(s, C, !mn_ok, !mn_ok, kDwOut, sm);
+  };
+  size_t cap;
+  if (budget == 0) {
+    const int64_t C0 = std::min<int64_t>(cmax, ref_chunk(s.BT, s.H, s.V));
+    // the reference's chunk logits, the gathered rows and their transpose, and an
+    // eighth of the chunk's bytes for the dX GEMM's split partials
+    const FlPlan b = lean(C0, 1);
+    cap = std::max(kSmallWorkspace, b.total + (size_t)C0 * pad64(s.V) * s.es / 8);
+  } else {
+    cap = budget < 0 ? SIZE_MAX : (size_t)budget;
+  }
+  bool found = false;
+  FlPlan best;
+  std::vector<int64_t> cs;
+  for (int64_t C = cmax; C >= 8; C = (C > 64 ? (C - 1) / 64 * 64 : C / 2 & ~(int64_t)7)) {
+    cs.push_back(C);
+    if (C <= 8) break;
+  }
+  for (int64_t C : cs) {
+    const int64_t nch = s.BT > 0 ? cdiv(s.BT, C) : 0;
+    fl_forms(s, nch, [&](bool wt, bool dt, int dw) {
+      if (forced && (dw != f_dw || wt != f_wt || dt != f_dt)) return;
+      for (int sm = smax_full; sm >= 1; sm = sm > 1 ? sm / 2 : 0) {
+        FlPlan p = fl_layout(s, C, wt, dt, dw, sm);
+        if (p.total > cap) continue;
+        p.cost = fl_cost(s, p);
+        const bool ex = exact_dw(s, p), bex = found && exact_dw(s, best);
+        const bool better = !found || (ex && !bex) ||
+                            (ex == bex && (p.cost < best.cost || (p.cost == best.cost && p.total < best.total)));
+        if (better) {
+          best = p;
+          found = true;
+        }
+        break;  // fewer splits only if more do not fit
+      }
+    });
+  }
+  if (!found && forced) {
+    set_error("HILDA_FL_FORM: the forced form does not apply to this call (dtype, chunk count or budget)");
+    return HK_EINVAL;
+  }
+  if (!found) {
+    const FlPlan small = lean(cs.back(), 1);
+    set_error("workspace budget %lld bytes is below the smallest plan (%zu bytes)", (long long)budget, small.total);
+    return HK_EINVAL;
+  }
+  *out = best;
+  return HK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The chunk loop shared by the fused-linear losses.
 //
-// With rowmap, the rows are compacted first: X holds the live rows of the
-// caller's hidden states in order (rowmap[i] is row i's original row), zero
-// rows after them, and *n_live (device memory) is their count. Every GEMM is
-// cut to the live rows on the device (tiles past them exit, the dW GEMM's K
-// stops at them), and dX_c is stored straight into the original rows; the
-// caller zeroes the dead rows of dX. Without rowmap (n_live null too) every
-// row of X is processed in place.
+// X [BT, H] (row stride H) and W [V, H] are the caller's hidden states and
+// weight. With rowmap, the rows are compacted first: rowmap[i] is compacted
+// row i's original row, *n_live (device memory) their count; each chunk
+// gathers its live rows (zero rows after them) and every GEMM is cut to the
+// live rows on the device (tiles past them exit, the dW GEMM's K stops at
+// them); dX_c is stored straight into the original rows and the caller zeroes
+// the dead rows of dX. Without rowmap (n_live null too) every row is live.
+//
+// row_step(Lg, r0, cs): the chunk's logits Lg (compacted rows r0 .. r0 + cs,
+// row stride plan.ldl) to row losses and, with gradients, the dlogits D_c
+// written over them (zero past the row step's width). pad: what the logits
+// epilogue writes past V in the straddling 16-byte chunk.
 template <typename T, class RowStep>
-int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, int64_t C, char* ws,
-                    const FlceLayout& lay, bool grad, T* dX, T* dWo, const int* n_live, const int* rowmap,
-                    RowStep&& row_step, hipStream_t st) {
-  const int64_t BTp = pad8(BT), ldx = ld_t(BT);
-  T* Lg = (T*)(ws + lay.lg);
-  T* Wt = grad ? (T*)(ws + lay.wt) : nullptr;
-  T* Xt = grad ? (T*)(ws + lay.xt) : nullptr;
-  T* Dt = grad ? (T*)(ws + lay.dt) : nullptr;
-  float* dwacc = (grad && lay.dwacc) ? (float*)(ws + lay.dwacc) : nullptr;
+int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, char* ws, const FlPlan& p, bool grad,
+                    T* dX, T* dWo, const int* n_live, const int* rowmap, float pad, RowStep&& row_step,
+                    hipStream_t st) {
+  constexpr int E = 16 / (int)sizeof(T);
+  const int64_t C = p.C, Hp = p.Hp, ldl = p.ldl;
+  const bool defer = grad && p.dw == kDwDefer;
+  T* Lg = (T*)(ws + p.lg);
+  T* Xg = p.gather ? (T*)(ws + p.xg) : nullptr;
+  T* Wp = p.wpad ? (T*)(ws + p.wp) : nullptr;
+  T* Wt = p.wt ? (T*)(ws + p.wtp) : nullptr;
+  T* Xt = grad ? (T*)(ws + p.xt) : nullptr;
+  T* Dt = p.dt ? (T*)(ws + p.dtp) : nullptr;
+  float* acc = (grad && p.dw == kDwAcc) ? (float*)(ws + p.acc) : nullptr;
+  const T* Wk = p.wpad ? Wp : W;  // K-contiguous weight rows
+  const int64_t ldw = p.wpad ? Hp : H;
   int rc = HK_OK;
-  if (grad) {
-    rc = launch_transpose<T>(Wt, W, V, V, H, H, V, st);  // W^T [H, V]
-    if (rc) return rc;
-    rc = launch_transpose<T>(Xt, X, BT, BTp, H, H, ldx, st);  // X^T [H, BTp] (row stride ldx), zero padded
+  if (p.wpad) {  // the weight rows at a 16-byte multiple, zero filled past H
+    rc = gather_rows<T>(Wp, Hp, Hp, W, H, H, nullptr, nullptr, V, 0, V, st);
     if (rc) return rc;
   }
-  const int64_t nchunks = BT > 0 ? cdiv(BT, C) : 0;
-  for (int64_t ci = 0; ci < nchunks; ++ci) {
+  // the chunk buffer's columns the row step never writes are the dX GEMM's K padding: zero
+  rc = zero_cols<T>(Lg, ldl, p.Vr, ldl, C, st);
+  if (rc) return rc;
+  if (grad && p.wt) {
+    rc = launch_transpose<T>(Wt, Wk, V, ldl, Hp, ldw, ldl, st);  // W^T [Hp, ldl], zero columns past V
+    if (rc) return rc;
+  }
+  const int64_t BTp = pad8(BT), ldxt = ld_t(defer ? BT : C);
+  const bool dvec = H % 4 == 0 && aligned_to(dX, 16);    // 4-element stores of dX rows
+  const bool wvec = H % 4 == 0 && aligned_to(dWo, 16);   // and of dW rows
+  const int kt_dx = (int)(ldl / gemm::CfgFor<T>::BK);
+  for (int64_t ci = 0; ci < p.nch; ++ci) {
     const int64_t r0 = ci * C;
     const int64_t cs = std::min<int64_t>(C, BT - r0);
+    // the chunk's hidden rows, K-contiguous
+    const T* Xc = X + r0 * H;
+    int64_t ldxc = H;
+    if (p.gather) {
+      rc = gather_rows<T>(Xg, Hp, Hp, X, H, H, rowmap, n_live, BT, r0, cs, st);
+      if (rc) return rc;
+      Xc = Xg;
+      ldxc = Hp;
+    }
     // logits_c = X_c W^T (live rows only)
-    rc = launch_gemm<T>(X + r0 * H, W, (int)cs, (int)V, (int)H, H, H, EpiStore<T>{Lg, V}, st, n_live, (int)r0);
+    rc = launch_gemm<T>(Xc, Wk, (int)cs, (int)V, (int)Hp, ldxc, ldw, EpiLogits<T>{Lg, ldl, pad}, st, n_live,
+                        (int)r0);
     if (rc) return rc;
     rc = row_step(Lg, r0, cs);
     if (rc) return rc;
     if (!grad) continue;
     // dX_c = D_c W, stored into the live rows' original places; a short chunk
-    // splits K (= V) and sums the splits' fp32 partials in a second pass
-    if (lay.ksplit > 1) {
-      float* part = (float*)(ws + lay.part);
-      T* dst = rowmap ? dX : dX + r0 * H;
-      const int* map = rowmap ? rowmap + r0 : nullptr;
-      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiDx<T>{dst, H, map, part, H}, st, n_live,
-                          (int)r0, false, lay.ksplit);
-      if (rc) return rc;
-      const int64_t work = cs * (H / 8);
-      hipLaunchKernelGGL((splitk_sum_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(work, 256), 8192)), dim3(256),
-                         0, st, dst, H, map, part, (int)cs, (int)H, (int)(V / gemm::CfgFor<T>::BK), lay.ksplit,
-                         n_live, (int)r0);
-      rc = check_launch("splitk_sum_kernel");
-    } else if (rowmap) {
-      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiScatter<T>{dX, H, rowmap + r0}, st, n_live,
-                          (int)r0);
-    } else {
-      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)H, (int)V, V, V, EpiStore<T>{dX + r0 * H, H}, st);
-    }
+    // splits K (= ldl) and sums the splits' fp32 partials in a second pass
+    T* dst = rowmap ? dX : dX + r0 * H;
+    const int* map = rowmap ? rowmap + r0 : nullptr;
+    float* part = p.ksplit > 1 ? (float*)(ws + p.part) : nullptr;
+    const EpiDx<T> edx{dst, H, map, part, Hp, (int)H, dvec};
+    if (p.wt)
+      rc = launch_gemm<T>(Lg, Wt, (int)cs, (int)Hp, (int)ldl, ldl, ldl, edx, st, n_live, (int)r0, false, p.ksplit);
+    else  // W [V, ldw] read MN-contiguous: k = the vocabulary row, past V zero
+      rc = launch_gemm_mn<T, false, true>(Lg, Wk, (int)cs, (int)Hp, (int)ldl, ldl, ldw, edx, st, n_live, (int)r0,
+                                          false, p.ksplit, (int)V);
     if (rc) return rc;
-    if (lay.defer) {
-      // D_c^T into columns [r0, r0 + cs) of D^T [V, BTp]; zeros past the live rows
-      rc = launch_transpose<T>(Dt + r0, Lg, cs, ci + 1 < nchunks ? cs : BTp - r0, V, V, ldx, st, n_live, r0);
+    if (p.ksplit > 1) {
+      const int64_t work = cs * cdiv(H, 4);
+      hipLaunchKernelGGL((splitk_sum_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(work, 256), 8192)), dim3(256),
+                         0, st, dst, H, map, part, (int)cs, (int)Hp, kt_dx, p.ksplit, n_live, (int)r0, (int)H,
+                         dvec ? 1 : 0);
+      rc = check_launch("splitk_sum_kernel");
+      if (rc) return rc;
+    }
+    // X_c^T (zeros past the live rows) into X^T: columns [r0, r0 + cs) of [Hp, BT] when
+    // deferred, else [Hp, C]
+    const int64_t csp = pad8(cs);
+    T* xt_dst = defer ? Xt + r0 : Xt;
+    const int64_t xrp = defer ? (ci + 1 < p.nch ? cs : BTp - r0) : csp;
+    rc = launch_transpose<T>(xt_dst, Xc, cs, xrp, Hp, ldxc, ldxt, st, n_live, r0);
+    if (rc) return rc;
+    if (defer) {
+      // D_c^T into columns [r0, r0 + cs) of D^T [V8, BTp]; zeros past the live rows
+      rc = launch_transpose<T>(Dt + r0, Lg, cs, xrp, p.V8, ldl, ldxt, st, n_live, r0);
       if (rc) return rc;
       continue;
     }
-    // dW += D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands, and cut
+    // dW (+)= D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands, and cut
     // on the device to the live rows
-    const int64_t csp = pad8(cs), ldd = ld_t(cs);
-    rc = launch_transpose<T>(Dt, Lg, cs, csp, V, V, ldd, st, n_live, r0);
-    if (rc) return rc;
     auto dw_gemm = [&](auto epi) {
-      return launch_gemm<T>(Dt, Xt + r0, (int)V, (int)H, (int)csp, ldd, ldx, epi, st, n_live, (int)r0, true);
+      if (p.dt)
+        return launch_gemm<T>(Dt, Xt, (int)V, (int)Hp, (int)csp, ldxt, ldxt, epi, st, n_live, (int)r0, true);
+      // D_c [cs, ldl] read MN-contiguous (k = the chunk row, m = the vocabulary column); its rows stop at
+      // cs (the chunk buffer's rows past it were never written), or at the live rows on the device
+      return launch_gemm_mn<T, true, false>(Lg, Xt, (int)p.V8, (int)Hp, (int)csp, ldl, ldxt, epi, st, n_live,
+                                            (int)r0, true, 1, 0, (int)cs);
     };
-    if (nchunks == 1) rc = dw_gemm(EpiStore<T>{dWo, H});
-    else if (ci == 0) rc = dw_gemm(EpiAccum<T, 0>{dwacc, dWo, H});
-    else if (ci + 1 < nchunks) rc = dw_gemm(EpiAccum<T, 1>{dwacc, dWo, H});
-    else rc = dw_gemm(EpiAccum<T, 2>{dwacc, dWo, H});
+    if (p.dt) {
+      rc = launch_transpose<T>(Dt, Lg, cs, csp, p.V8, ldl, ldxt, st, n_live, r0);
+      if (rc) return rc;
+    }
+    const int vl = (int)V, hl = (int)H;
+    if (p.nch == 1) rc = dw_gemm(EpiDw<T, 0>{dWo, H, nullptr, Hp, vl, hl, wvec});
+    else if (p.dw == kDwOut) rc = ci == 0 ? dw_gemm(EpiDw<T, 0>{dWo, H, nullptr, Hp, vl, hl, wvec})
+                                          : dw_gemm(EpiDw<T, 1>{dWo, H, nullptr, Hp, vl, hl, wvec});
+    else if (ci == 0) rc = dw_gemm(EpiDw<T, 2>{dWo, H, acc, Hp, vl, hl, wvec});
+    else if (ci + 1 < p.nch) rc = dw_gemm(EpiDw<T, 3>{dWo, H, acc, Hp, vl, hl, wvec});
+    else rc = dw_gemm(EpiDw<T, 4>{dWo, H, acc, Hp, vl, hl, wvec});
     if (rc) return rc;
   }
-  if (grad && lay.defer && nchunks > 0) {
-    rc = launch_gemm<T>(Dt, Xt, (int)V, (int)H, (int)BTp, ldx, ldx, EpiStore<T>{dWo, H}, st, n_live, 0, true);
+  if (defer && p.nch > 0) {
+    rc = launch_gemm<T>(Dt, Xt, (int)V, (int)Hp, (int)BTp, ldxt, ldxt,
+                        EpiDw<T, 0>{dWo, H, nullptr, Hp, (int)V, (int)H, wvec}, st, n_live, 0, true);
     if (rc) return rc;
   }
-  if (grad && nchunks == 0) {
+  if (grad && p.nch == 0 && V > 0) {
     // no rows: the weight gradient is zero (dX is empty)
-    const int64_t n16 = V * H * (int64_t)sizeof(T) / 16;
-    hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n16, 256), 4096)), dim3(256), 0, st,
-                       (u32x4*)dWo, n16);
-    rc = check_launch("zero16_kernel");
+    rc = zero_cols<T>(dWo, H, 0, H, V, st);
+    if (rc) return rc;
   }
+  (void)E;
   return rc;
+}
+
+// Shape checks shared by the fused-linear entry points.
+int fl_check_dims(int64_t BT, int64_t H, int64_t V) {
+  HK_REQUIRE(BT >= 0 && H > 0 && V > 0, "invalid shape BT=%lld H=%lld V=%lld", (long long)BT, (long long)H,
+             (long long)V);
+  HK_REQUIRE(BT < (1LL << 31) - 8192 && H < (1LL << 30) && V < (1LL << 31) - 4096, "dimension too large");
+  return HK_OK;
+}
+
+FlShape flce_shape(int64_t BT, int64_t H, int64_t V, int dtype, bool grad, int64_t chunk, const void* hidden,
+                   const void* weight) {
+  FlShape s{};
+  s.BT = BT;
+  s.H = H;
+  s.V = V;
+  s.es = fl_esize(dtype);
+  s.grad = grad;
+  s.compact = true;
+  // (rows of a multiple of 8 elements: the padded width Hp is then H itself)
+  s.x_ok = H % 8 == 0 && (!hidden || aligned_to(hidden, 16));
+  s.w_ok = H % 8 == 0 && (!weight || aligned_to(weight, 16));
+  s.ce = true;
+  s.chunk_cap = chunk;
+  return s;
 }
 
 }  // namespace
@@ -621,30 +935,55 @@ using namespace hk;
 
 extern "C" {
 
-size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype,
-                                                    int with_grad) {
-  if (BT < 0 || H <= 0 || V <= 0 || !fl_dtype_ok(dtype)) return 0;
-  return flce_layout(BT, H, V, flce_chunk(BT, chunk), fl_esize(dtype), with_grad != 0, 0, true).total;
+size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk,
+                                                    int64_t workspace_budget, int dtype, int with_grad,
+                                                    const void* hidden, const void* weight) {
+  if (!fl_dtype_ok(dtype) || fl_check_dims(BT, H, V) != HK_OK) return 0;
+  FlPlan p;
+  if (fl_plan(flce_shape(BT, H, V, dtype, with_grad != 0, chunk, hidden, weight), workspace_budget, &p) != HK_OK)
+    return 0;
+  return p.total;
+}
+
+int hk_fused_linear_cross_entropy_plan(int64_t BT, int64_t H, int64_t V, int64_t chunk, int64_t workspace_budget,
+                                       int dtype, int with_grad, const void* hidden, const void* weight,
+                                       int64_t* info) {
+  HK_REQUIRE(fl_dtype_ok(dtype), "fused linear cross entropy supports fp32, bf16 and fp16 (got %d)", dtype);
+  if (const int rc = fl_check_dims(BT, H, V)) return rc;
+  HK_REQUIRE(info, "null pointer argument");
+  FlPlan p;
+  if (const int rc = fl_plan(flce_shape(BT, H, V, dtype, with_grad != 0, chunk, hidden, weight), workspace_budget,
+                             &p))
+    return rc;
+  info[0] = p.C;
+  info[1] = p.nch;
+  info[2] = p.dw;
+  info[3] = p.wt ? 1 : 0;
+  info[4] = p.dt ? 1 : 0;
+  info[5] = p.ksplit;
+  info[6] = (int64_t)p.total;
+  info[7] = (int64_t)(p.cost * 1e9);
+  return HK_OK;
 }
 
 int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
                                   const void* weight, const int64_t* targets, const float* row_scale, int64_t BT,
                                   int64_t H, int64_t V, int64_t ignore_index, int reduction, int dtype, int64_t chunk,
-                                  void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+                                  int64_t workspace_budget, void* workspace, size_t workspace_bytes,
+                                  hk_stream_t stream) {
   HK_REQUIRE(fl_dtype_ok(dtype), "fused linear cross entropy supports fp32, bf16 and fp16 (got %d)", dtype);
-  HK_REQUIRE(BT >= 0 && H > 0 && V > 0, "invalid shape BT=%lld H=%lld V=%lld", (long long)BT, (long long)H,
-             (long long)V);
-  HK_REQUIRE(H % 8 == 0 && V % 8 == 0, "H and V must be multiples of 8 (16-byte rows)");
-  HK_REQUIRE(BT < (1LL << 31) && H < (1LL << 31) && V < (1LL << 31) - 4096, "dimension too large");
+  if (const int rc = fl_check_dims(BT, H, V)) return rc;
   HK_REQUIRE(reduction >= HK_REDUCTION_NONE && reduction <= HK_REDUCTION_SUM, "invalid reduction %d", reduction);
   const bool grad = dhidden != nullptr || dweight != nullptr;
   HK_REQUIRE(!grad || (dhidden && dweight), "dhidden and dweight are computed together");
   HK_REQUIRE(loss_rows && hidden && weight && targets, "null pointer argument");
-  HK_REQUIRE(aligned_to(hidden, 16) && aligned_to(weight, 16) && (!grad || (aligned_to(dhidden, 16) &&
-                                                                             aligned_to(dweight, 16))),
-             "hidden, weight and gradients must be 16-byte aligned");
-  const int64_t C = flce_chunk(BT, chunk);
-  const FlceLayout lay = flce_layout(BT, H, V, C, fl_esize(dtype), grad, 0, true);
+  const int es = fl_esize(dtype);
+  HK_REQUIRE(aligned_to(hidden, es) && aligned_to(weight, es) &&
+                 (!grad || (aligned_to(dhidden, es) && aligned_to(dweight, es))),
+             "hidden, weight and gradients must be aligned to their element size");
+  FlPlan lay;
+  if (const int rc = fl_plan(flce_shape(BT, H, V, dtype, grad, chunk, hidden, weight), workspace_budget, &lay))
+    return rc;
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
@@ -663,15 +1002,12 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
 
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
-    T* Xc = (T*)(ws + lay.xc);
     int rc = HK_OK;
     if (BT > 0) {
       rc = count_valid_launch(n_valid, targets, BT, ignore_index, has_ignore, st);
       if (rc) return rc;
-      // the non-ignored rows, compacted: their hidden rows, targets and row scales
+      // the non-ignored rows, compacted: their targets and row scales (each chunk gathers its hidden rows)
       rc = ce_compact_launch(rowmap, inv, n_live, targets, BT, ignore_index, st);
-      if (rc) return rc;
-      rc = gather_rows<T>(Xc, (const T*)hidden, rowmap, n_live, BT, H, st);
       if (rc) return rc;
       hipLaunchKernelGGL(gather_ce_kernel, dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 1024)), dim3(256), 0, st,
                          tc, sc, targets, row_scale, rowmap, n_live);
@@ -679,14 +1015,14 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
       if (rc) return rc;
     }
     // per-row loss of the compacted rows; with gradients, D_c = (softmax - onehot) * s * row_scale
-    // written over the logits
+    // written over the logits (the -inf padding past V to the row width gives exact zeros)
     auto ce_step = [&](T* Lg, int64_t r0, int64_t cs) {
-      return ce_rows_launch(grad ? (void*)Lg : nullptr, lc + r0, Lg, tc + r0, cs, V, V, V, ignore_index, has_ignore,
-                            n_valid, grad && reduction == HK_REDUCTION_MEAN, row_scale ? sc + r0 : nullptr, dtype, st,
-                            n_live, r0);
+      return ce_rows_launch(grad ? (void*)Lg : nullptr, lc + r0, Lg, tc + r0, cs, lay.Vr, lay.ldl, lay.ldl,
+                            ignore_index, has_ignore, n_valid, grad && reduction == HK_REDUCTION_MEAN,
+                            row_scale ? sc + r0 : nullptr, dtype, st, n_live, r0);
     };
-    rc = chunked_lm_head<T>(Xc, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden, (T*)dweight, n_live,
-                            rowmap, ce_step, st);
+    rc = chunked_lm_head<T>((const T*)hidden, (const T*)weight, BT, H, V, ws, lay, grad, (T*)dhidden, (T*)dweight,
+                            n_live, rowmap, -__builtin_huge_valf(), ce_step, st);
     if (rc) return rc;
     // losses back in row order (ignored rows 0); ignored rows of dhidden are zero
     rc = finish_rows<T>(grad ? (T*)dhidden : nullptr, loss_rows, lc, inv, BT, H, st);
@@ -701,87 +1037,164 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
   return fl_dispatch(dtype, run);
 }
 
+// ---------------------------------------------------------------------------
+// FusedLinearJSD: the engine with a row step that runs the teacher GEMM on the
+// chunk's (gathered) teacher rows into a second chunk buffer, then one row
+// kernel (both temperature log-softmaxes, JSD, the student dlogits).
+// Extra workspace: per-row losses and compacted labels (BT each), the teacher
+// logits chunk and gathered teacher rows (per chunk row) and a padded copy of
+// the teacher weight when its rows are not 16-byte multiples.
+// ---------------------------------------------------------------------------
+namespace {
+struct JsdExtra {
+  size_t lc, labc, lt, xtc, wtp, total;
+};
+JsdExtra jsd_extra(int64_t BT, int64_t Ht, int64_t V, int64_t C, int es, bool t_gather, bool t_wpad) {
+  JsdExtra e{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
+  e.lc = take(bt * 4);
+  e.labc = take(bt * 8);
+  e.lt = take((size_t)C * pad64(V) * es);
+  e.xtc = t_gather ? take((size_t)C * pad8(Ht) * es) : 0;
+  e.wtp = t_wpad ? take((size_t)V * pad8(Ht) * es) : 0;
+  e.total = off;
+  return e;
+}
 
-size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int dtype,
-                                          int with_grad) {
-  if (BT < 0 || H <= 0 || Ht <= 0 || V <= 0 || !fl_dtype_ok(dtype)) return 0;
-  return fljsd_layout(BT, H, Ht, V, flce_chunk(BT, chunk), fl_esize(dtype), with_grad != 0).total;
+FlShape fljsd_shape(int64_t BT, int64_t H, int64_t Ht, int64_t V, int dtype, bool grad, int64_t chunk, bool labels,
+                    const void* s_in, const void* s_w, const void* t_in, const void* t_w, bool* t_gather,
+                    bool* t_wpad) {
+  FlShape s{};
+  s.BT = BT;
+  s.H = H;
+  s.V = V;
+  s.es = fl_esize(dtype);
+  s.grad = grad;
+  s.compact = labels;
+  s.x_ok = H % 8 == 0 && (!s_in || aligned_to(s_in, 16));
+  s.w_ok = H % 8 == 0 && (!s_w || aligned_to(s_w, 16));
+  *t_gather = labels || Ht % 8 != 0 || (t_in && !aligned_to(t_in, 16));
+  *t_wpad = Ht % 8 != 0 || (t_w && !aligned_to(t_w, 16));
+  const JsdExtra e0 = jsd_extra(BT, Ht, V, 0, s.es, *t_gather, *t_wpad);
+  s.fixed_extra = e0.total + 4 * 256;
+  s.row_extra = (size_t)pad64(V) * s.es + (*t_gather ? (size_t)pad8(Ht) * s.es : 0);
+  s.chunk_cap = chunk;
+  return s;
+}
+}  // namespace
+
+size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk,
+                                          int64_t workspace_budget, int dtype, int with_grad, int with_labels,
+                                          const void* s_input, const void* s_weight, const void* t_input,
+                                          const void* t_weight) {
+  if (!fl_dtype_ok(dtype) || Ht <= 0 || Ht >= (1LL << 30) || fl_check_dims(BT, H, V) != HK_OK) return 0;
+  bool tg, tw;
+  FlPlan p;
+  if (fl_plan(fljsd_shape(BT, H, Ht, V, dtype, with_grad != 0, chunk, with_labels != 0, s_input, s_weight, t_input,
+                          t_weight, &tg, &tw),
+              workspace_budget, &p) != HK_OK)
+    return 0;
+  return p.total;
 }
 
 int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
                         const void* t_input, const void* t_weight, const int64_t* labels, int64_t BT, int64_t H,
                         int64_t Ht, int64_t V, int64_t ignore_index, float beta, float temperature, int dtype,
-                        int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+                        int64_t chunk, int64_t workspace_budget, void* workspace, size_t workspace_bytes,
+                        hk_stream_t stream) {
   HK_REQUIRE(fl_dtype_ok(dtype), "fused linear JSD supports fp32, bf16 and fp16 (got %d)", dtype);
-  HK_REQUIRE(BT >= 0 && H > 0 && Ht > 0 && V > 0, "invalid shape BT=%lld H=%lld Ht=%lld V=%lld", (long long)BT,
-             (long long)H, (long long)Ht, (long long)V);
-  HK_REQUIRE(H % 8 == 0 && Ht % 8 == 0 && V % 8 == 0, "H, Ht and V must be multiples of 8 (16-byte rows)");
-  HK_REQUIRE(BT < (1LL << 31) && H < (1LL << 31) && Ht < (1LL << 31) && V < (1LL << 31) - 4096,
-             "dimension too large");
+  if (const int rc = fl_check_dims(BT, H, V)) return rc;
+  HK_REQUIRE(Ht > 0 && Ht < (1LL << 30), "invalid teacher hidden size Ht=%lld", (long long)Ht);
   HK_REQUIRE(beta >= 0.f && beta <= 1.f, "beta must lie in [0, 1] (got %g)", (double)beta);
   HK_REQUIRE(temperature > 0.f, "temperature must be positive (got %g)", (double)temperature);
   const bool grad = dinput != nullptr || dweight != nullptr;
   HK_REQUIRE(!grad || (dinput && dweight), "dinput and dweight are computed together");
   HK_REQUIRE(loss_out && s_input && s_weight && t_input && t_weight, "null pointer argument");
-  HK_REQUIRE(aligned_to(s_input, 16) && aligned_to(s_weight, 16) && aligned_to(t_input, 16) &&
-                 aligned_to(t_weight, 16) && (!grad || (aligned_to(dinput, 16) && aligned_to(dweight, 16))),
-             "inputs, weights and gradients must be 16-byte aligned");
-  const int64_t C = flce_chunk(BT, chunk);
-  const FljsdLayout lay = fljsd_layout(BT, H, Ht, V, C, fl_esize(dtype), grad);
+  const int es = fl_esize(dtype);
+  HK_REQUIRE(aligned_to(s_input, es) && aligned_to(s_weight, es) && aligned_to(t_input, es) &&
+                 aligned_to(t_weight, es) && (!grad || (aligned_to(dinput, es) && aligned_to(dweight, es))),
+             "inputs, weights and gradients must be aligned to their element size");
+  bool t_gather, t_wpad;
+  const FlShape shp = fljsd_shape(BT, H, Ht, V, dtype, grad, chunk, labels != nullptr, s_input, s_weight, t_input,
+                                  t_weight, &t_gather, &t_wpad);
+  FlPlan lay;
+  if (const int rc = fl_plan(shp, workspace_budget, &lay)) return rc;
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
+  const JsdExtra je = jsd_extra(BT, Ht, V, lay.C, es, t_gather, t_wpad);
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  const FlceLayout& lb = lay.base;
-  int* n_valid = (int*)(ws + lb.nvalid);
+  char* ex = ws + lay.extra;
+  int* n_valid = (int*)(ws + lay.nvalid);
   // with labels the ignored rows are compacted away (the engine's row map and live count)
-  int* n_live = labels ? (int*)(ws + lb.nlive) : nullptr;
-  int* rowmap = labels ? (int*)(ws + lb.rowmap) : nullptr;
-  int* inv = (int*)(ws + lb.inv);
-  float* lc = (float*)(ws + lay.lc);
-  int64_t* labc = (int64_t*)(ws + lay.labc);
+  int* n_live = labels ? (int*)(ws + lay.nlive) : nullptr;
+  int* rowmap = labels ? (int*)(ws + lay.rowmap) : nullptr;
+  int* inv = labels ? (int*)(ws + lay.inv) : nullptr;
+  float* lc = (float*)(ex + je.lc);
+  int64_t* labc = (int64_t*)(ex + je.labc);
+  const int64_t Htp = pad8(Ht), ldl = lay.ldl;
 
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
     const T* Xs = (const T*)s_input;
     const T* Xt_in = (const T*)t_input;
-    const T* Wt_in = (const T*)t_weight;
-    T* Lt = (T*)(ws + lay.lt);
-    T* Xtc = (T*)(ws + lay.xtc);
-    T* Xsc = (T*)(ws + lb.xc);
+    T* Lt = (T*)(ex + je.lt);
+    T* Xtc = t_gather ? (T*)(ex + je.xtc) : nullptr;
+    T* Wtp = t_wpad ? (T*)(ex + je.wtp) : nullptr;
+    const T* Wt_k = t_wpad ? Wtp : (const T*)t_weight;
+    const int64_t ldwt = t_wpad ? Htp : Ht;
     int rc = HK_OK;
+    if (t_wpad) {
+      rc = gather_rows<T>(Wtp, Htp, Htp, (const T*)t_weight, Ht, Ht, nullptr, nullptr, V, 0, V, st);
+      if (rc) return rc;
+    }
     if (labels && BT > 0) {
       // n counts the labels that are not ignore_index over all BT rows (fused_linear_jsd.py:137-141)
       rc = count_valid_launch(n_valid, labels, BT, ignore_index, 1, st);
       if (rc) return rc;
       rc = ce_compact_launch(rowmap, inv, n_live, labels, BT, ignore_index, st);
       if (rc) return rc;
-      rc = gather_rows<T>(Xsc, Xs, rowmap, n_live, BT, H, st);
-      if (rc) return rc;
-      rc = gather_rows<T>(Xtc, Xt_in, rowmap, n_live, BT, Ht, st);
-      if (rc) return rc;
       hipLaunchKernelGGL(gather_ce_kernel, dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 1024)), dim3(256), 0, st,
                          labc, nullptr, labels, nullptr, rowmap, n_live);
       rc = check_launch("gather_ce_kernel");
       if (rc) return rc;
     }
-    float* lrows = labels ? lc : (float*)(ws + lay.lc);
     // row step: the teacher logits of the chunk's rows (fused_linear_jsd.py:159-160), then the log-softmaxes,
-    // JSD and, with gradients, the student dlogits over the student logits (:163-199)
+    // JSD and, with gradients, the student dlogits over the student logits (:163-199); both chunk
+    // buffers hold zeros past V, which the row kernel does not read
     auto jsd_step = [&](T* Ls, int64_t r0, int64_t cs) {
-      const T* xt = (labels ? Xtc : Xt_in) + r0 * Ht;
-      int r = launch_gemm<T>(xt, Wt_in, (int)cs, (int)V, (int)Ht, Ht, Ht, EpiStore<T>{Lt, V}, st, n_live, (int)r0);
+      const T* xt = Xt_in + r0 * Ht;
+      int64_t ldx = Ht;
+      if (t_gather) {
+        int r = gather_rows<T>(Xtc, Htp, Htp, Xt_in, Ht, Ht, rowmap, n_live, BT, r0, cs, st);
+        if (r) return r;
+        xt = Xtc;
+        ldx = Htp;
+      }
+      int r = launch_gemm<T>(xt, Wt_k, (int)cs, (int)V, (int)Htp, ldx, ldwt, EpiLogits<T>{Lt, ldl, 0.f}, st, n_live,
+                             (int)r0);
       if (r) return r;
-      return jsd_logits_launch(lrows + r0, Ls, Lt, labels ? labc + r0 : nullptr, ignore_index, n_valid, BT, beta,
-                               temperature, cs, V, V, grad ? 1 : 0, dtype, st, n_live, r0);
+      return jsd_logits_launch(lc + r0, Ls, Lt, labels ? labc + r0 : nullptr, ignore_index, n_valid, BT, beta,
+                               temperature, cs, V, ldl, grad ? 1 : 0, dtype, st, n_live, r0);
     };
-    rc = chunked_lm_head<T>(labels ? Xsc : Xs, (const T*)s_weight, BT, H, V, C, ws, lb, grad, (T*)dinput,
-                            (T*)dweight, n_live, rowmap, jsd_step, st);
+    if (BT > 0) {
+      rc = zero_cols<T>(Lt, ldl, V, ldl, lay.C, st);
+      if (rc) return rc;
+    }
+    rc = chunked_lm_head<T>(Xs, (const T*)s_weight, BT, H, V, ws, lay, grad, (T*)dinput, (T*)dweight, n_live, rowmap,
+                            0.f, jsd_step, st);
     if (rc) return rc;
+    float* lrows = lc;
     if (labels) {
       // losses back in row order (ignored rows 0); ignored rows of dinput are zero
-      float* rows_out = (float*)(ws + lay.labc);  // the compacted labels are no longer needed
+      float* rows_out = (float*)(ex + je.labc);  // the compacted labels are no longer needed
       rc = finish_rows<T>(grad ? (T*)dinput : nullptr, rows_out, lc, inv, BT, H, st);
       if (rc) return rc;
       lrows = rows_out;
@@ -792,12 +1205,29 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
   return fl_dispatch(dtype, run);
 }
 
-size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int dtype,
-                                           int with_grad) {
-  if (B <= 0 || L < 0 || H <= 0 || V <= 0 || !fl_dtype_ok(dtype)) return 0;
-  const int64_t BT = B * (L + 1);
-  return flce_layout(BT, H, V, flce_chunk(BT, chunk), fl_esize(dtype), with_grad != 0, grpo_scratch_bytes(B, L))
-      .total;
+// ---------------------------------------------------------------------------
+// FusedLinear-GRPO
+// ---------------------------------------------------------------------------
+namespace {
+FlShape flgrpo_shape(int64_t B, int64_t L, int64_t H, int64_t V, int dtype, bool grad, int64_t chunk,
+                     const void* hidden, const void* weight) {
+  FlShape s = flce_shape(B * (L + 1), H, V, dtype, grad, chunk, hidden, weight);
+  s.ce = false;
+  s.fixed_extra = grpo_scratch_bytes(B, L);
+  return s;
+}
+}  // namespace
+
+size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk,
+                                           int64_t workspace_budget, int dtype, int with_grad, const void* hidden,
+                                           const void* weight) {
+  if (B <= 0 || L < 0 || B > (1LL << 31) || L > (1LL << 31) || !fl_dtype_ok(dtype) ||
+      fl_check_dims(B * (L + 1), H, V) != HK_OK)
+    return 0;
+  FlPlan p;
+  if (fl_plan(flgrpo_shape(B, L, H, V, dtype, with_grad != 0, chunk, hidden, weight), workspace_budget, &p) != HK_OK)
+    return 0;
+  return p.total;
 }
 
 int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float* lse_rows, float* loss_rows,
@@ -807,24 +1237,25 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
                          const float* ref_logp, int64_t ref_sB, int64_t ref_sL, const void* mask, int mask_dtype,
                          int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t H, int64_t V,
                          float temperature, float beta, float eps_low, float eps_high, int dtype, int64_t chunk,
-                         void* workspace, size_t workspace_bytes, hk_stream_t stream) {
+                         int64_t workspace_budget, void* workspace, size_t workspace_bytes, hk_stream_t stream) {
   HK_REQUIRE(fl_dtype_ok(dtype), "fused linear GRPO supports fp32, bf16 and fp16 (got %d)", dtype);
   const GrpoInputs in{ids,    ids_sB, ids_sL, advantages, old_logp, old_sB,      old_sL, ref_logp,
                       ref_sB, ref_sL, mask,   mask_dtype, mask_sB,  mask_sL,     B,      L,
                       V,      temperature,    beta,       eps_low,  eps_high};
   if (const int rc = grpo_check(in)) return rc;
-  HK_REQUIRE(H > 0 && H % 8 == 0 && V % 8 == 0, "H and V must be positive multiples of 8 (16-byte rows)");
-  HK_REQUIRE(B * (L + 1) < (1LL << 31) && H < (1LL << 31), "dimension too large");
+  if (const int rc = fl_check_dims(B * (L + 1), H, V)) return rc;
   const bool grad = dhidden != nullptr || dweight != nullptr;
   HK_REQUIRE(!grad || (dhidden && dweight), "dhidden and dweight are computed together");
   HK_REQUIRE(loss_out && clip_out && hidden && weight && (L == 0 || (lse_rows && loss_rows && kl_rows && clip_rows)),
              "null pointer argument");
-  HK_REQUIRE(aligned_to(hidden, 16) && aligned_to(weight, 16) && (!grad || (aligned_to(dhidden, 16) &&
-                                                                             aligned_to(dweight, 16))),
-             "hidden, weight and gradients must be 16-byte aligned");
+  const int es = fl_esize(dtype);
+  HK_REQUIRE(aligned_to(hidden, es) && aligned_to(weight, es) &&
+                 (!grad || (aligned_to(dhidden, es) && aligned_to(dweight, es))),
+             "hidden, weight and gradients must be aligned to their element size");
   const int64_t BT = B * (L + 1);
-  const int64_t C = flce_chunk(BT, chunk);
-  const FlceLayout lay = flce_layout(BT, H, V, C, fl_esize(dtype), grad, grpo_scratch_bytes(B, L));
+  FlPlan lay;
+  if (const int rc = fl_plan(flgrpo_shape(B, L, H, V, dtype, grad, chunk, hidden, weight), workspace_budget, &lay))
+    return rc;
   HK_REQUIRE(workspace && workspace_bytes >= lay.total, "workspace too small: need %zu bytes, got %zu", lay.total,
              workspace_bytes);
   HK_REQUIRE(aligned_to(workspace, 256), "workspace must be 256-byte aligned");
@@ -836,21 +1267,19 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
   int* inv = (int*)(ws + lay.inv);
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
-    T* Xc = (T*)(ws + lay.xc);
     int rc = grpo_prep_launch(in, scratch, st);
     if (rc) return rc;
     // the live positions (l < L, mask != 0), compacted: only their logits are computed
     rc = grpo_compact_launch(rowmap, inv, n_live, in, st);
     if (rc) return rc;
-    rc = gather_rows<T>(Xc, (const T*)hidden, rowmap, n_live, BT, H, st);
-    if (rc) return rc;
     // compacted row q of a chunk is position rowmap[r0 + q]: the GRPO row kernel
     // writes that token's results and, with gradients, its dlogits over the logits
     auto grpo_step = [&](T* Lg, int64_t r0, int64_t cs) {
-      return grpo_rows_launch(grad ? (void*)Lg : nullptr, Lg, r0, cs, in, scratch, dtype, st, rowmap, n_live);
+      return grpo_rows_launch(grad ? (void*)Lg : nullptr, Lg, r0, cs, in, scratch, dtype, st, rowmap, n_live, lay.Vr,
+                              lay.ldl);
     };
-    rc = chunked_lm_head<T>(Xc, (const T*)weight, BT, H, V, C, ws, lay, grad, (T*)dhidden, (T*)dweight, n_live,
-                            rowmap, grpo_step, st);
+    rc = chunked_lm_head<T>((const T*)hidden, (const T*)weight, BT, H, V, ws, lay, grad, (T*)dhidden, (T*)dweight,
+                            n_live, rowmap, -__builtin_huge_valf(), grpo_step, st);
     if (rc) return rc;
     // masked tokens and position L: zero rows of dhidden
     rc = finish_rows<T>(grad ? (T*)dhidden : nullptr, nullptr, nullptr, inv, BT, H, st);

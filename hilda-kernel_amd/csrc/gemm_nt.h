@@ -63,12 +63,16 @@ struct Shape {
   const int* lim = nullptr;
   int lim_off = 0;
   int lim_k = 0;
-  // split-K (gemm_kk_kernel only): at most ksplit workgroups per output tile.
-  // The kernel takes auto_splits() of the tiles left after the bound, so a GEMM
-  // cut short on the device still fills the chip; split s sums K tiles
-  // [s * per, (s + 1) * per), per = ceil(K / BK / splits), and the epilogue is
-  // told (Epi::set_split) its split, the split count and the bounded M.
+  // split-K: at most ksplit workgroups per output tile. The kernel takes
+  // auto_splits() of the tiles left after the bound, so a GEMM cut short on the
+  // device still fills the chip; split s sums K tiles [s * per, (s + 1) * per),
+  // per = ceil(K / BK / splits), and the epilogue is told (Epi::set_split) its
+  // split, the split count and the bounded M.
   int ksplit = 1;
+  // K extent of each operand's stored matrix when it is shorter than K
+  // (gemm_nt_kernel): k at or past it reads as zero. 0: K. A device-side K
+  // bound (lim_k) also cuts both to the unrounded live count.
+  int ka = 0, kb = 0;
 };
 
 // Splits for a GEMM of `tiles` output tiles and `kt` K tiles, at most max_s:
@@ -93,10 +97,17 @@ __device__ __forceinline__ void apply_split(Epi&, int, int, int, long) {}
 
 // Applies Shape::lim (a uniform scalar load); kq: the K granule of the kernel.
 __device__ __forceinline__ void apply_bound(Shape& g, int kq) {
+  if (g.ka <= 0) g.ka = g.K;
+  if (g.kb <= 0) g.kb = g.K;
   if (!g.lim) return;
   const int v = max(0, *g.lim - g.lim_off);
-  if (g.lim_k) g.K = min(g.K, max(kq, (v + kq - 1) / kq * kq));
-  else g.M = min(g.M, v);
+  if (g.lim_k) {
+    g.K = min(g.K, max(kq, (v + kq - 1) / kq * kq));
+    g.ka = min(g.ka, v);
+    g.kb = min(g.kb, v);
+  } else {
+    g.M = min(g.M, v);
+  }
 }
 
 // EPC: elements of the input type in a 16-byte chunk (8 for bf16/fp16, 4 for
@@ -265,7 +276,7 @@ struct Operand {
   int key[I];  // K-contiguous: first column of the chunk in the stage; MN: first row of the chunk
   const T* p;
   int64_t ld;
-  int r0, rows_valid, K;
+  int r0, rows_valid, K;  // K: the stored matrix's K extent
 
   __device__ __forceinline__ void init(const T* ptr, int64_t ld_, int r0_, int nrows, int K_, int wave, int lane) {
     p = ptr;
@@ -290,12 +301,14 @@ struct Operand {
     }
   }
 
-  // Stage kst (a stage at or past KT is a zero-length buffer: the loads
-  // return zeros without touching memory) into `tile`.
-  __device__ __forceinline__ void issue(T* tile, int kst, int KT, int wave) const {
+  // Stage kst of this workgroup's K range, which starts at K tile kt0 (a stage
+  // at or past KT, or wholly past the stored K, is a zero-length buffer: the
+  // loads return zeros without touching memory) into `tile`.
+  __device__ __forceinline__ void issue(T* tile, int kst, int KT, int kt0, int wave) const {
 #if defined(__HIP_DEVICE_COMPILE__)
-    const bool live = kst < KT;
-    const int k0 = live ? kst * C::BK : 0;
+    const int k0x = (kt0 + kst) * C::BK;
+    const bool live = kst < KT && k0x < K;
+    const int k0 = live ? k0x : 0;
     if constexpr (!MN) {
       const int lim = K - k0;  // columns of this stage inside the matrix
       const int nrec = live ? (int)(rows_valid * ld * (int64_t)sizeof(T)) : 0;
@@ -454,10 +467,20 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 
   apply_bound(g, 8);
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
-  if ((int)blockIdx.x >= nbm * nbn) return;  // uniform: past a device-side bound
+  const int tiles = nbm * nbn;
+  const int KTall = (g.K + C::BK - 1) / C::BK;  // >= 1 (checked by the launcher)
+  const int nsplit = auto_splits(tiles, KTall, g.ksplit);
+  if ((int)blockIdx.x >= tiles * nsplit) return;  // uniform: past a device-side bound
+  const int split = (int)blockIdx.x / tiles;
   int tm, tn;
-  tile_of_block<C::GROUP_M>((int)blockIdx.x, nbm, nbn, &tm, &tn);
+  tile_of_block<C::GROUP_M>((int)blockIdx.x - split * tiles, nbm, nbn, &tm, &tn);
   const int m0 = tm * C::BM, n0 = tn * C::BN;
+  int KT = KTall, kt0 = 0;
+  if (nsplit > 1) {  // this split's K tiles (auto_splits keeps every split non-empty)
+    const int per = (KTall + nsplit - 1) / nsplit;
+    kt0 = split * per;
+    KT = min(per, KTall - kt0);
+  }
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the LDS base of a load lives in M0
@@ -474,17 +497,16 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int KT = (g.K + C::BK - 1) / C::BK;  // >= 1 (checked by the launcher)
   const int fr = lane & 31, fk = lane >> 5;
 
   Operand<T, C, C::BM, AMN> opa;
   Operand<T, C, C::BN, BMN> opb;
-  opa.init(A, g.lda, m0, g.M, g.K, wave, lane);
-  opb.init(B, g.ldb, n0, g.N, g.K, wave, lane);
+  opa.init(A, g.lda, m0, g.M, g.ka, wave, lane);
+  opb.init(B, g.ldb, n0, g.N, g.kb, wave, lane);
   auto issue = [&](int stage, int kst) {
     T* la = lds + stage * C::STAGE;
-    opa.issue(la, kst, KT, wave);
-    opb.issue(la + C::BM * C::BK, kst, KT, wave);
+    opa.issue(la, kst, KT, kt0, wave);
+    opb.issue(la + C::BM * C::BK, kst, KT, kt0, wave);
   };
 
   u32x4 fa[2][C::TM], fb[2][C::TN];
@@ -550,7 +572,9 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
   wait_vmcnt<0>();  // the dummy loads of the tail target LDS: drain them before LDS is reused
   barrier();
 
-  epilogue<T, C>(acc, lds_raw, m0, n0, g, epi);
+  Epi e = epi;
+  apply_split(e, split, nsplit, g.M, 0);
+  epilogue<T, C>(acc, lds_raw, m0, n0, g, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -758,17 +782,24 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
 // AMN / BMN: the operand is stored MN-contiguous (A[k][m], B[k][n]) instead of
 // K-contiguous (A[m][k], B[n][k]); lda / ldb are the leading dimensions of
 // whichever layout is used.
+//
+// ka / kb (0: K): the K extent of A's / B's stored matrix when shorter than K
+// (its k past that read as zero; general kernel only). ksplit: see Shape.
 template <typename T, class C = CfgFor<T>, bool AMN = false, bool BMN = false, class Epi>
 int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb, Epi epi, hipStream_t st,
-           const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1) {
+           const int* lim = nullptr, int lim_off = 0, bool lim_k = false, int ksplit = 1, int ka = 0, int kb = 0) {
   static_assert(sizeof(T) == 2 || (!AMN && !BMN), "fp32 operands must be K-contiguous");
   if (M == 0 || N == 0) return 0;
   if (K <= 0) {
     set_error("gemm: K (%d) must be positive", K);
     return -1;
   }
-  if (ksplit > 1 && (AMN || BMN || K % C::BK != 0 || lim_k)) {
-    set_error("gemm: split-K needs K-contiguous operands and K (%d) a multiple of %d", K, C::BK);
+  if (ka < 0 || kb < 0 || ka > K || kb > K) {
+    set_error("gemm: operand K extents (%d, %d) outside [0, K = %d]", ka, kb, K);
+    return -1;
+  }
+  if (ksplit > 1 && lim_k) {
+    set_error("gemm: split-K with a device-side K bound is not supported");
     return -1;
   }
   auto check = [&](bool mn, int rows, int64_t ld, const char* name) {
@@ -795,17 +826,14 @@ int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb
     return true;
   };
   if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
-  Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0, ksplit < 1 ? 1 : ksplit};
+  Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0, ksplit < 1 ? 1 : ksplit, ka, kb};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN) * g.ksplit;
   if constexpr (!AMN && !BMN && C::STAGES == 2 && C::CPR == 8) {
-    if (K % C::BK == 0) {
+    // (the K-contiguous kernel reads every operand to K: the extents must be K)
+    if (K % C::BK == 0 && (ka == 0 || ka == K) && (kb == 0 || kb == K)) {
       hipLaunchKernelGGL((gemm_kk_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);
       return check_launch("gemm_kk_kernel");
     }
-  }
-  if (g.ksplit > 1) {
-    set_error("gemm: split-K runs on the two-stage K-contiguous kernel only");
-    return -1;
   }
   hipLaunchKernelGGL((gemm_nt_kernel<T, C, AMN, BMN, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g,
                      epi);

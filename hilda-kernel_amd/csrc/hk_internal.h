@@ -79,13 +79,15 @@ size_t grpo_scratch_bytes(int64_t B, int64_t L);
 int grpo_prep_launch(const GrpoInputs& in, void* scratch, hipStream_t st);
 
 // Rows [row0, row0 + nrows) of the B x (L+1) logits rows, `logits` pointing at
-// row row0 (row stride V): per-token results into scratch and, with dlogits
-// (may alias logits), the gradient rows at unit upstream gradient. With rowmap
-// (a compaction, see grpo_compact_launch) row q of the launch is position
-// rowmap[row0 + q], and only q < *n_live - row0 exist.
+// row row0 (row stride ld, 0: the width): per-token results into scratch and,
+// with dlogits (may alias logits), the gradient rows at unit upstream
+// gradient. With rowmap (a compaction, see grpo_compact_launch) row q of the
+// launch is position rowmap[row0 + q], and only q < *n_live - row0 exist.
+// width (0: V): the row elements read, V or more when the columns past V hold
+// -inf (their probability and gradient are then exactly 0).
 int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nrows, const GrpoInputs& in,
                      void* scratch, int dtype, hipStream_t st, const int* rowmap = nullptr,
-                     const int* n_live = nullptr);
+                     const int* n_live = nullptr, int64_t width = 0, int64_t ld = 0);
 
 // Stable compaction of the live positions (l < L, mask != 0) of the B x (L+1)
 // rows: rowmap, inv and *n_live as for ce_compact_launch.

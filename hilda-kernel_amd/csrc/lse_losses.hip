@@ -856,6 +856,7 @@ struct GrpoHot {
   const GrpoTok* tok;
   GrpoOut* out;
   int64_t B, L, V;
+  int64_t W, ld;  // row width the kernel reads (V, or more with -inf padding past V) and row stride
   int64_t row0, nrows;  // the launch covers rows [row0, row0 + nrows) of the (B, L+1) positions
   // optional compaction: launch row q is position rowmap[row0 + q], and only
   // q < *nlim - row0 exist (a device-side bound)
@@ -922,7 +923,7 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
   for (int64_t row = blockIdx.x; row < rows; row += G) {
     GrpoTok tk{};
     if (!live(row, &tk)) {
-      if constexpr (GRAD) fill_row<T, VEC, BLOCK>(dlogits + row * a.V, (int)a.V, 0.f);
+      if constexpr (GRAD) fill_row<T, VEC, BLOCK>(dlogits + row * a.ld, (int)a.W, 0.f);
       const int64_t g = pos(row), b = g / (a.L + 1), l = g - b * (a.L + 1);
       if (l < a.L && threadIdx.x == 0) a.out[b * a.L + l] = GrpoOut{0.f, 0.f, 0.f, 0.f};
     }
@@ -960,15 +961,15 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
     LiveRow cur = next_live(blockIdx.x);
     if (cur.row >= rows) return;
     Regs r;
-    r.load(logits + cur.row * a.V, row_len(a.V));
+    r.load(logits + cur.row * a.ld, row_len(a.W));
     LiveRow next = next_live(cur.row + G);
     int parity = 0;
     for (;;) {
-      const int n = row_len(a.V);  // per iteration (see row_len)
+      const int n = row_len(a.W);  // per iteration (see row_len)
       const int64_t row = cur.row;
       const int id = cur.id;
-      const T* in = logits + row * a.V;
-      const T* src = next.row < rows ? logits + next.row * a.V : in;  // unconditional (see the CE kernel)
+      const T* in = logits + row * a.ld;
+      const T* src = next.row < rows ? logits + next.row * a.ld : in;  // unconditional (see the CE kernel)
       const GrpoTok tk = load_tok(a.tok + cur.tok_i);
       float m, s, xt, M, R, X, rest;
       r.reduce_lane(n, c, id, &m, &s, &xt);
@@ -989,7 +990,7 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
       if constexpr (GRAD) {
         // d loss / d logits_j = -dlogp * (p_j - [j == id]) * dloss / T
         const float g = -dlogp * tk.gs;
-        T* out = dlogits + row * a.V;
+        T* out = dlogits + row * a.ld;
         r.store_prob_grad_then_load(out, n, c, lse2, g, src);
         // the id element: (p_id - 1) * g = -(1 - p_id) * g (see reduce_lane)
         if (Regs::owns_target(id)) out[id] = from_f32<T>(-rest * g);
@@ -1006,9 +1007,9 @@ __global__ __launch_bounds__(BLOCK) void grpo_kernel(T* dlogits, const T* logits
     for (int64_t row = blockIdx.x; row < rows; row += G) {
       GrpoTok tk{};
       if (!live(row, &tk)) continue;
-      T* out = GRAD ? dlogits + row * a.V : nullptr;
-      const T* in = logits + row * a.V;
-      const int n = row_len(a.V);
+      T* out = GRAD ? dlogits + row * a.ld : nullptr;
+      const T* in = logits + row * a.ld;
+      const int n = row_len(a.W);
       // the id logit is read before the reduction's barriers: dlogits may alias
       // logits, and no lane stores before every lane has passed them
       const float xid = tk.id >= 0 ? to_f32<T>(in[tk.id]) : 0.f;
@@ -1367,8 +1368,13 @@ int grpo_prep_launch(const GrpoInputs& in, void* scratch, hipStream_t st) {
 }
 
 int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nrows, const GrpoInputs& in,
-                     void* scratch, int dtype, hipStream_t st, const int* rowmap, const int* n_live) {
+                     void* scratch, int dtype, hipStream_t st, const int* rowmap, const int* n_live, int64_t width,
+                     int64_t ld) {
   if (nrows <= 0) return HK_OK;
+  if (width <= 0) width = in.V;
+  if (ld <= 0) ld = width;
+  HK_REQUIRE(width >= in.V && ld >= width, "GRPO rows: width %lld / stride %lld below V = %lld", (long long)width,
+             (long long)ld, (long long)in.V);
   GrpoHot h{};
   h.rowmap = rowmap;
   h.nlim = n_live;
@@ -1377,6 +1383,8 @@ int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nr
   h.B = in.B;
   h.L = in.L;
   h.V = in.V;
+  h.W = width;
+  h.ld = ld;
   h.row0 = row0;
   h.nrows = nrows;
   h.inv_T = 1.f / in.temperature;
@@ -1385,8 +1393,9 @@ int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nr
   h.eps_hi = in.eps_hi;
   h.has_old = in.old_logp != nullptr;
   const int es = esize(dtype);
-  const bool vec_ok = in.V % (16 / es) == 0 && aligned_to(logits, 16) && (!dlogits || aligned_to(dlogits, 16));
-  const RowCfg cfg = choose_row_cfg(in.V, es, vec_ok);
+  const bool vec_ok = width % (16 / es) == 0 && (ld * es) % 16 == 0 && aligned_to(logits, 16) &&
+                      (!dlogits || aligned_to(dlogits, 16));
+  const RowCfg cfg = choose_row_cfg(width, es, vec_ok);
   return dispatch_t(dtype, [&](auto tt) {
     using T = typename decltype(tt)::type;
     return dispatch_cfg(cfg, [&](auto blk, auto nch) {

@@ -53,9 +53,9 @@ SIGNATURES = {
     "hk_attn_res_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),
     "hk_attn_res_bwd_workspace_size": (_sz, [_i64, _i64]),
     "hk_attn_res_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _sz, _p]),
-    "hk_fused_linear_jsd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
+    "hk_fused_linear_jsd_workspace_size": (_sz, [_i64] * 6 + [_i32, _i32, _i32, _p, _p, _p, _p]),
     "hk_fused_linear_jsd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
-                                   _i64, _p, _sz, _p]),
+                                   _i64, _i64, _p, _sz, _p]),
     "hk_cross_entropy_workspace_size": (_sz, [_i64]),
     "hk_cross_entropy_fwd_grad": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
     "hk_cross_entropy_fwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _sz, _p]),
@@ -63,18 +63,19 @@ SIGNATURES = {
     "hk_selective_log_softmax": (_i32, [_p, _p, _p, _i64, _i64, _p, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
                                         _p]),
     "hk_grpo_workspace_size": (_sz, [_i64, _i64]),
-    "hk_fused_linear_cross_entropy_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32, _i32]),
+    "hk_fused_linear_cross_entropy_workspace_size": (_sz, [_i64] * 5 + [_i32, _i32, _p, _p]),
+    "hk_fused_linear_cross_entropy_plan": (_i32, [_i64] * 5 + [_i32, _i32, _p, _p, _p]),
     "hk_fused_linear_cross_entropy": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32,
-                                             _i64, _p, _sz, _p]),
+                                             _i64, _i64, _p, _sz, _p]),
     "hk_grpo_loss_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _p,
                                 _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _i32, _p, _sz, _p]),
-    "hk_fused_linear_grpo_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
+    "hk_fused_linear_grpo_workspace_size": (_sz, [_i64] * 6 + [_i32, _i32, _p, _p]),
     "hk_fused_linear_grpo": (_i32, [_p] * 7 + [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64,
                                                _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32,
-                                               _i32, _i64, _p, _sz, _p]),
+                                               _i32, _i64, _i64, _p, _sz, _p]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()
@@ -165,3 +166,36 @@ def cu_count(device: torch.device) -> int:
         check(0 if n > 0 else n, "hk_device_cu_count")
         _cu_cache[idx] = n
     return _cu_cache[idx]
+
+
+# Workspace budget of the fused-linear ops (hk_fused_linear_cross_entropy_workspace_size):
+# 0 the default plan (the reference's chunk, fused_linear_cross_entropy.py:112-114),
+# -1 no limit (the fastest plan), > 0 a byte budget.
+BUDGET_ENV = "HILDA_FL_WORKSPACE_BUDGET"
+
+
+def fl_budget(budget) -> int:
+    """A workspace budget argument as the C ABI takes it: None reads $HILDA_FL_WORKSPACE_BUDGET (unset: 0);
+    'default' 0; 'fastest' -1; an int is bytes (0 default, negative no limit)."""
+    if budget is None:
+        budget = os.environ.get(BUDGET_ENV, "0")
+    if isinstance(budget, str):
+        b = budget.strip().lower()
+        if b in ("", "default"):
+            return 0
+        if b in ("fastest", "unlimited", "none"):
+            return -1
+        try:
+            budget = int(float(b))
+        except ValueError:
+            raise ValueError(f"workspace budget {budget!r}: expected bytes, 'default' or 'fastest'") from None
+    budget = int(budget)
+    return -1 if budget < 0 else budget
+
+
+def workspace(nbytes: int, what: str, device: torch.device) -> torch.Tensor:
+    """A device workspace of nbytes (0 from a size query means no plan fits the budget)."""
+    if int(nbytes) == 0:
+        raise RuntimeError(f"{what}: no memory plan fits the workspace budget (or the shape is invalid): "
+                           f"{last_error()}")
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)

@@ -14,6 +14,7 @@ logits: hidden is (B, L+1, H), the states whose lm_head logits GRPOLoss would
 take; weight is the lm_head [V, H]. Returns (loss, kl_mean, clip_ratio); only
 loss is differentiable. All gradient work happens in the forward; the
 backward scales the saved gradients by the upstream gradient on the device.
+Memory follows ``workspace_budget`` as for FusedLinearCrossEntropy; any H and V.
 """
 from __future__ import annotations
 
@@ -23,12 +24,12 @@ from . import _lib
 from .cross_entropy import scale_rows_
 from .grpo_loss import _f32, _ids_arg, _mask_arg
 
-DEFAULT_CHUNK = 8192
+DEFAULT_CHUNK = 0  # no cap: the workspace budget sets the chunk (at most 8192 rows)
 
 
 def fused_linear_grpo_forward(hidden, weight, completion_ids, advantages, old_logp=None, ref_logp=None,
                               completion_mask=None, temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2,
-                              compute_grad=True, chunk=DEFAULT_CHUNK):
+                              compute_grad=True, chunk=DEFAULT_CHUNK, workspace_budget=None):
     """Returns (loss, kl_mean or None, clip_ratio, grad_hidden or None, grad_weight or None, rows), rows being
     the per-token (lse, loss, kl, clipped) [B, L] fp32 tensors."""
     assert hidden.dim() == 3 and weight.dim() == 2 and hidden.shape[2] == weight.shape[1], \
@@ -58,15 +59,17 @@ def fused_linear_grpo_forward(hidden, weight, completion_ids, advantages, old_lo
     grad_hidden = torch.empty_like(hidden) if compute_grad else None
     grad_weight = torch.empty_like(weight) if compute_grad else None
     dt = _lib.dtype_code(hidden)
-    ws_bytes = _lib.load().hk_fused_linear_grpo_workspace_size(B, L, H, V, chunk, dt, int(compute_grad))
-    ws = torch.empty(max(int(ws_bytes), 256), dtype=torch.uint8, device=dev)
+    budget = _lib.fl_budget(workspace_budget)
+    ws_bytes = _lib.load().hk_fused_linear_grpo_workspace_size(B, L, H, V, int(chunk), budget, dt, int(compute_grad),
+                                                               hidden.data_ptr(), weight.data_ptr())
+    ws = _lib.workspace(ws_bytes, "fused linear GRPO", dev)
     _lib.call("hk_fused_linear_grpo", loss.data_ptr(), _lib.ptr(kl_mean), clip_ratio.data_ptr(),
               *(r.data_ptr() for r in rows), _lib.ptr(grad_hidden), _lib.ptr(grad_weight), hidden.data_ptr(),
               weight.data_ptr(), ids.data_ptr(), ids.stride(0), ids.stride(1), adv.data_ptr(),
               _lib.ptr(old), old.stride(0) if old is not None else 0, old.stride(1) if old is not None else 0,
               _lib.ptr(ref), ref.stride(0) if ref is not None else 0, ref.stride(1) if ref is not None else 0,
               _lib.ptr(mask), mcode, msb, msl, B, L, H, V, float(temperature), float(beta), float(eps_low),
-              float(eps_high), dt, int(chunk), ws.data_ptr(), ws.numel(), _lib.stream_of(dev))
+              float(eps_high), dt, int(chunk), budget, ws.data_ptr(), ws.numel(), _lib.stream_of(dev))
     return loss, kl_mean, clip_ratio, grad_hidden, grad_weight, rows
 
 
@@ -75,11 +78,11 @@ class HildaFusedLinearGRPOFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden, weight, completion_ids, advantages, old_logp, ref_logp, completion_mask, temperature,
-                beta, eps_low, eps_high):
+                beta, eps_low, eps_high, workspace_budget=None):
         compute_grad = hidden.requires_grad or weight.requires_grad
         loss, kl_mean, clip_ratio, gh, gw, _ = fused_linear_grpo_forward(
             hidden, weight, completion_ids, advantages, old_logp, ref_logp, completion_mask, temperature, beta,
-            eps_low, eps_high, compute_grad=compute_grad)
+            eps_low, eps_high, compute_grad=compute_grad, workspace_budget=workspace_budget)
         ctx.compute_grad = compute_grad
         ctx.applied = None
         if compute_grad:
@@ -92,7 +95,7 @@ class HildaFusedLinearGRPOFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_loss, grad_kl, grad_clip):
-        nones = (None,) * 9
+        nones = (None,) * 10
         if not ctx.compute_grad or grad_loss is None:
             return (None, None) + nones
         gh, gw = ctx.saved_tensors
@@ -112,24 +115,26 @@ class HildaFusedLinearGRPOFunction(torch.autograd.Function):
 
 
 def hilda_fused_linear_grpo_loss(hidden, weight, completion_ids, advantages, old_logp=None, ref_logp=None,
-                                 completion_mask=None, temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2):
+                                 completion_mask=None, temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2,
+                                 workspace_budget=None):
     """Functional interface: GRPO loss of the lm_head logits hidden @ weight.T, without materialising them."""
     return HildaFusedLinearGRPOFunction.apply(hidden, weight, completion_ids, advantages, old_logp, ref_logp,
-                                              completion_mask, temperature, beta, eps_low, eps_high)
+                                              completion_mask, temperature, beta, eps_low, eps_high, workspace_budget)
 
 
 class FusedLinearGRPOLoss(torch.nn.Module):
     """GRPOLoss (grpo_loss.py:382-397) over hidden states and the lm_head weight."""
 
-    def __init__(self, temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2):
+    def __init__(self, temperature=1.0, beta=0.0, eps_low=0.2, eps_high=0.2, workspace_budget=None):
         super().__init__()
         self.temperature = temperature
         self.beta = beta
         self.eps_low = eps_low
         self.eps_high = eps_high
+        self.workspace_budget = workspace_budget
 
     def forward(self, hidden, weight, completion_ids, advantages, old_logp=None, ref_logp=None,
                 completion_mask=None):
         return hilda_fused_linear_grpo_loss(hidden, weight, completion_ids, advantages, old_logp, ref_logp,
                                             completion_mask, self.temperature, self.beta, self.eps_low,
-                                            self.eps_high)
+                                            self.eps_high, self.workspace_budget)

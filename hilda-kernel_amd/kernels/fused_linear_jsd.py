@@ -11,12 +11,16 @@ scales the saved gradients by the upstream gradient on the device, and a unit
 upstream gradient leaves them untouched (the reference's ``torch.equal`` test
 at :228, without the host synchronisation).
 
+Memory follows ``workspace_budget`` exactly as for FusedLinearCrossEntropy
+(the default: the reference's chunk, its teacher logits chunk beside it).
+
 Differences from the reference, by design:
   * the reference keeps fp32 copies of both logits chunks and of dX
     (:163-188); here the row kernel works from the 16-bit logits in
     registers, in fp32 arithmetic;
-  * grad_weight is summed in fp32 and rounded once (the reference
-    accumulates in the weight dtype, :203);
+  * with room for it (a larger budget), grad_weight is summed in fp32 and
+    rounded once (the reference accumulates in the weight dtype, :203);
+  * any H, Ht and V (padded inside the workspace);
   * rows labelled ignore_index are compacted away on the device before the
     GEMMs, so they cost no FLOPs (the reference computes their logits);
   * the label count stays on the device (the reference reads it, :139);
@@ -32,7 +36,8 @@ from .fused_linear_cross_entropy import DEFAULT_CHUNK
 
 
 def fused_linear_jsd_forward(student_input, student_weight, teacher_input, teacher_weight, labels=None, beta=0.5,
-                             temperature=1.0, ignore_index=-100, compute_grad=True, chunk=DEFAULT_CHUNK):
+                             temperature=1.0, ignore_index=-100, compute_grad=True, chunk=DEFAULT_CHUNK,
+                             workspace_budget=None):
     """Forward (fused_linear_jsd.py:114-205). Returns (loss, grad_input, grad_weight)."""
     si, sw, ti, tw = student_input, student_weight, teacher_input, teacher_weight
     assert si.dim() == 2 and sw.dim() == 2 and si.shape[1] == sw.shape[1], \
@@ -57,11 +62,15 @@ def fused_linear_jsd_forward(student_input, student_weight, teacher_input, teach
     loss = torch.empty((), dtype=torch.float32, device=dev)
     grad_input = torch.empty_like(si) if compute_grad else None
     grad_weight = torch.empty_like(sw) if compute_grad else None
-    ws_bytes = _lib.load().hk_fused_linear_jsd_workspace_size(BT, H, Ht, V, chunk, dt, int(compute_grad))
-    ws = torch.empty(max(int(ws_bytes), 256), dtype=torch.uint8, device=dev)
+    budget = _lib.fl_budget(workspace_budget)
+    ws_bytes = _lib.load().hk_fused_linear_jsd_workspace_size(BT, H, Ht, V, int(chunk), budget, dt,
+                                                              int(compute_grad), int(lab is not None), si.data_ptr(),
+                                                              sw.data_ptr(), ti.data_ptr(), tw.data_ptr())
+    ws = _lib.workspace(ws_bytes, "fused linear JSD", dev)
     _lib.call("hk_fused_linear_jsd", loss.data_ptr(), _lib.ptr(grad_input), _lib.ptr(grad_weight), si.data_ptr(),
               sw.data_ptr(), ti.data_ptr(), tw.data_ptr(), _lib.ptr(lab), BT, H, Ht, V, int(ignore_index),
-              float(beta), float(temperature), dt, int(chunk), ws.data_ptr(), ws.numel(), _lib.stream_of(dev))
+              float(beta), float(temperature), dt, int(chunk), budget, ws.data_ptr(), ws.numel(),
+              _lib.stream_of(dev))
     return loss, grad_input, grad_weight
 
 
@@ -70,10 +79,11 @@ class HildaFusedLinearJSDFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, student_input, student_weight, teacher_input, teacher_weight, labels, beta, temperature,
-                ignore_index):
+                ignore_index, workspace_budget=None):
         compute_grad = student_input.requires_grad or student_weight.requires_grad
         loss, gi, gw = fused_linear_jsd_forward(student_input, student_weight, teacher_input, teacher_weight, labels,
-                                                beta, temperature, ignore_index, compute_grad=compute_grad)
+                                                beta, temperature, ignore_index, compute_grad=compute_grad,
+                                                workspace_budget=workspace_budget)
         ctx.compute_grad = compute_grad
         ctx.applied = None
         if compute_grad:
@@ -82,7 +92,7 @@ class HildaFusedLinearJSDFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        none6 = (None,) * 6
+        none6 = (None,) * 7
         if not ctx.compute_grad:
             return (None, None) + none6
         gi, gw = ctx.saved_tensors
@@ -100,21 +110,24 @@ class HildaFusedLinearJSDFunction(torch.autograd.Function):
 
 
 def hilda_fused_linear_jsd(student_input, student_weight, teacher_input, teacher_weight, labels=None, beta=0.5,
-                           temperature=1.0, ignore_index=-100):
-    """Functional interface: fused linear + JSD loss (fused_linear_jsd.py:244-254)."""
+                           temperature=1.0, ignore_index=-100, workspace_budget=None):
+    """Functional interface: fused linear + JSD loss (fused_linear_jsd.py:244-254).
+    workspace_budget (not in the reference): see the module docstring."""
     return HildaFusedLinearJSDFunction.apply(student_input, student_weight, teacher_input, teacher_weight, labels,
-                                             beta, temperature, ignore_index)
+                                             beta, temperature, ignore_index, workspace_budget)
 
 
 class FusedLinearJSDLoss(torch.nn.Module):
-    """Fused linear projection + JSD loss for distillation (fused_linear_jsd.py:261-275)."""
+    """Fused linear projection + JSD loss for distillation (fused_linear_jsd.py:261-275).
+    workspace_budget (not in the reference): see the module docstring."""
 
-    def __init__(self, beta=0.5, temperature=1.0, ignore_index=-100):
+    def __init__(self, beta=0.5, temperature=1.0, ignore_index=-100, workspace_budget=None):
         super().__init__()
         self.beta = beta
         self.temperature = temperature
         self.ignore_index = ignore_index
+        self.workspace_budget = workspace_budget
 
     def forward(self, student_input, student_weight, teacher_input, teacher_weight, labels=None):
         return hilda_fused_linear_jsd(student_input, student_weight, teacher_input, teacher_weight, labels,
-                                      self.beta, self.temperature, self.ignore_index)
+                                      self.beta, self.temperature, self.ignore_index, self.workspace_budget)

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define HK_ABI_VERSION 1
+#define HK_ABI_VERSION 2
 
 #define HK_F32 0
 #define HK_F16 1
@@ -191,24 +191,31 @@ int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const
                int64_t ignore_index, float beta, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ld_dx,
                int dtype, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
-/* Bytes of device workspace hk_fused_linear_jsd needs (chunk <= 0: 8192); Ht: the teacher's hidden size. */
-size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int dtype,
-                                          int with_grad);
+/* Bytes of device workspace hk_fused_linear_jsd needs for a call with the same
+ * shape, chunk, budget, dtype, gradient and label choice and the same input
+ * pointers (nullable: taken as 16-byte aligned); Ht: the teacher's hidden
+ * size. 0 for an invalid shape or a budget no plan fits (see
+ * hk_fused_linear_cross_entropy_workspace_size for chunk and budget). */
+size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk,
+                                          int64_t workspace_budget, int dtype, int with_grad, int with_labels,
+                                          const void* s_input, const void* s_weight, const void* t_input,
+                                          const void* t_weight);
 
-/* Replaces fused_linear_jsd_forward (fused_linear_jsd.py:114-205): per chunk of
- * `chunk` rows, student logits s_input[BT,H] * s_weight[V,H]^T and teacher
- * logits t_input[BT,Ht] * t_weight[V,Ht]^T on MFMA (fp32, bf16 or fp16), both
+/* Replaces fused_linear_jsd_forward (fused_linear_jsd.py:114-205): per chunk,
+ * student logits s_input[BT,H] * s_weight[V,H]^T and teacher logits
+ * t_input[BT,Ht] * t_weight[V,Ht]^T on MFMA (fp32, bf16 or fp16), both
  * temperature log-softmaxes, JSD(beta) per row divided by
  * max(#labels != ignore_index, 1) (BT without labels), and (dinput, dweight
  * non-null) the student dlogits contracted into dinput [BT,H] and dweight
- * [V,H] (summed in fp32, rounded once). Rows labelled ignore_index are
- * compacted away on the device before the GEMMs. The teacher gets no
- * gradient. *loss_out = the summed loss. Rows are contiguous, H, Ht and V
- * multiples of 8, pointers 16-byte aligned. */
+ * [V,H]. Rows labelled ignore_index are compacted away on the device before
+ * the GEMMs. The teacher gets no gradient. *loss_out = the summed loss. Rows
+ * are contiguous; any H, Ht and V. The chunk engine and its memory plans are
+ * hk_fused_linear_cross_entropy's. */
 int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
                         const void* t_input, const void* t_weight, const int64_t* labels, int64_t BT, int64_t H,
                         int64_t Ht, int64_t V, int64_t ignore_index, float beta, float temperature, int dtype,
-                        int64_t chunk, void* workspace, size_t workspace_bytes, hk_stream_t stream);
+                        int64_t chunk, int64_t workspace_budget, void* workspace, size_t workspace_bytes,
+                        hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
 /* FusedLinear-GRPO                                                        */
@@ -216,16 +223,18 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
 /* No counterpart in the reference: its GRPO op takes materialised logits
  * (grpo_loss.py:241-330). This is that op behind the lm_head, chunked like
  * fused_linear_cross_entropy_forward (fused_linear_cross_entropy.py:103-171),
- * so the (B, L+1, V) logits never exist. Bytes of workspace it needs (0 for an
- * unsupported dtype); chunk <= 0 selects the default (8192 rows). */
-size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int dtype,
-                                           int with_grad);
+ * so the (B, L+1, V) logits never exist. Bytes of workspace it needs for a
+ * call with the same arguments (0 for an invalid shape or a budget no plan
+ * fits; chunk and budget as for hk_fused_linear_cross_entropy_workspace_size). */
+size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk,
+                                           int64_t workspace_budget, int dtype, int with_grad, const void* hidden,
+                                           const void* weight);
 
-/* hidden (B, L+1, H) and weight [V, H] (fp32, bf16 or fp16, contiguous): logits =
+/* hidden (B, L+1, H) and weight [V, H] (fp32, bf16 or fp16, contiguous, any H and V): logits =
  * hidden weight^T, then exactly hk_grpo_loss_fwd's loss, kl_mean, clip_ratio
  * and per-token rows, and with dhidden (B, L+1, H) / dweight [V, H] (both or
  * neither) the gradients of the loss at unit upstream gradient (zero rows of
- * dhidden at masked tokens and at position L; dW accumulated in fp32). */
+ * dhidden at masked tokens and at position L). */
 int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float* lse_rows, float* loss_rows,
                          float* kl_rows, float* clip_rows, void* dhidden, void* dweight, const void* hidden,
                          const void* weight, const int64_t* ids, int64_t ids_sB, int64_t ids_sL,
@@ -233,7 +242,7 @@ int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float*
                          const float* ref_logp, int64_t ref_sB, int64_t ref_sL, const void* mask, int mask_dtype,
                          int64_t mask_sB, int64_t mask_sL, int64_t B, int64_t L, int64_t H, int64_t V,
                          float temperature, float beta, float eps_low, float eps_high, int dtype, int64_t chunk,
-                         void* workspace, size_t workspace_bytes, hk_stream_t stream);
+                         int64_t workspace_budget, void* workspace, size_t workspace_bytes, hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
 /* AttnRes (attention residuals over depth)                                */
@@ -327,25 +336,48 @@ int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_
 /* ----------------------------------------------------------------------- */
 /* FusedLinearCrossEntropy                                                 */
 /* ----------------------------------------------------------------------- */
-/* Bytes of device workspace hk_fused_linear_cross_entropy needs (0 for an
- * unsupported dtype). chunk <= 0 selects the default (8192 rows). */
-size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk, int dtype,
-                                                    int with_grad);
+/* Bytes of device workspace hk_fused_linear_cross_entropy needs for a call
+ * with the same shape, chunk, budget, dtype and gradient choice and the same
+ * hidden/weight pointers (nullable: taken as 16-byte aligned); 0 for an
+ * invalid shape or a budget no plan fits.
+ *   chunk: most rows per chunk (<= 0: 8192).
+ *   workspace_budget: 0 selects the default plan, whose workspace is what the
+ *     reference's chunk costs (fused_linear_cross_entropy.py:112-114: chunk
+ *     logits about the size of the hidden states, at least 64 rows) plus a
+ *     quarter of that for split partial sums; < 0 no limit (the fastest plan);
+ *     > 0 at most that many bytes. Within the budget the plan with the least
+ *     modelled time is taken (hk_fused_linear_cross_entropy_plan reports it). */
+size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk,
+                                                    int64_t workspace_budget, int dtype, int with_grad,
+                                                    const void* hidden, const void* weight);
+
+/* No counterpart in the reference: the plan the call above sizes, for
+ * benchmarks and tests. info[8] = rows per chunk, chunks, dW mode (0: every
+ * chunk's D^T kept and one dW GEMM after the loop; 1: an fp32 [V,H]
+ * accumulator; 2: accumulated in the output, rounded per chunk for 16-bit
+ * inputs), W^T materialised (else W read MN-contiguous), D^T materialised
+ * (else D read MN-contiguous), dX split cap, workspace bytes, modelled ns. */
+int hk_fused_linear_cross_entropy_plan(int64_t BT, int64_t H, int64_t V, int64_t chunk, int64_t workspace_budget,
+                                       int dtype, int with_grad, const void* hidden, const void* weight,
+                                       int64_t* info);
 
 /* Replaces fused_linear_cross_entropy_forward (fused_linear_cross_entropy.py:103-171)
  * and its backward scaling (:192-210). hidden [BT,H], weight [V,H] (fp32, bf16
- * or fp16, contiguous); targets [BT] int64; rows equal to ignore_index are ignored.
- * loss_rows[r] = CE of row r (scaled by 1/max(n_valid,1) when gradients are
- * computed with reduction mean); loss_out (nullable) = sum, or mean over valid
- * rows. With dhidden/dweight (both or neither): the gradients of the reduced
- * loss at unit upstream gradient, each row's gradient further multiplied by
- * row_scale[r] when row_scale is given (reduction 'none' backward). Logits are
- * produced `chunk` rows at a time on MFMA (fp32 inputs on the fp32 MFMA), for the rows whose target
- * is not ignore_index only (compacted on the device); dW is summed in fp32. */
+ * or fp16, contiguous, any H and V); targets [BT] int64; rows equal to
+ * ignore_index are ignored. loss_rows[r] = CE of row r (scaled by
+ * 1/max(n_valid,1) when gradients are computed with reduction mean);
+ * loss_out (nullable) = sum, or mean over valid rows. With dhidden/dweight
+ * (both or neither): the gradients of the reduced loss at unit upstream
+ * gradient, each row's gradient further multiplied by row_scale[r] when
+ * row_scale is given (reduction 'none' backward). Logits are produced a chunk
+ * of rows at a time on MFMA (fp32 inputs on the fp32 MFMA), for the rows whose
+ * target is not ignore_index only (compacted on the device), in the memory
+ * plan workspace_budget selects (see the size query above). */
 int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidden, void* dweight, const void* hidden,
                                   const void* weight, const int64_t* targets, const float* row_scale, int64_t BT,
                                   int64_t H, int64_t V, int64_t ignore_index, int reduction, int dtype, int64_t chunk,
-                                  void* workspace, size_t workspace_bytes, hk_stream_t stream);
+                                  int64_t workspace_budget, void* workspace, size_t workspace_bytes,
+                                  hk_stream_t stream);
 
 /* ----------------------------------------------------------------------- */
 /* Streaming copies (measurement references)                               */

@@ -81,30 +81,39 @@ def test_argument_validation_losses_without_gpu():
     _expect_einval(lib.hk_kl_div_fwd(p, p, p, p, 4, 8, 4, 8, 0, 1e-10, 1, 2, None), "shape")
     _expect_einval(lib.hk_jsd_fwd(p, p, p, p, p, None, -100, 1.5, 4, 8, 8, 8, 8, 2, ws, 1 << 20, None), "beta")
     _expect_einval(lib.hk_geglu_fwd(p, p, p, -1, 2, None), "element count")
-    # FusedLinearCE: hidden [BT, H], weight [V, H]
+    # FusedLinearCE: hidden [BT, H], weight [V, H] (any H and V); chunk, budget, workspace
     flce = [p, p, p, p, p, p, p, None]
-    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 5, 0, ws, 1 << 20, None),
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 5, 0, 0, ws, 1 << 20, None),
                    "fp32, bf16 and fp16")
-    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 60, 128, -100, 1, 2, 0, ws, 1 << 20, None),
-                   "multiples of 8")
-    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 5, 2, 0, ws, 1 << 20, None),
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 0, 128, -100, 1, 2, 0, 0, ws, 1 << 20, None),
+                   "invalid shape")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 5, 2, 0, 0, ws, 1 << 20, None),
                    "reduction")
-    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 2, 0, ws, 64, None),
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 2, 0, 0, ws, 64, None),
                    "workspace too small")
-    _expect_einval(lib.hk_fused_linear_cross_entropy(p, p, p, None, p, p, p, None, 64, 64, 128, -100, 1, 2, 0, ws,
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce, 64, 64, 128, -100, 1, 2, 0, 4096, ws, 1 << 20, None),
+                   "below the smallest plan")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(p, p, p, None, p, p, p, None, 64, 64, 128, -100, 1, 2, 0, 0, ws,
                                                      1 << 20, None), "computed together")
+    _expect_einval(lib.hk_fused_linear_cross_entropy(*flce[:4], ctypes.c_void_p(257), *flce[5:], 64, 64, 128, -100,
+                                                     1, 2, 0, 0, ws, 1 << 20, None), "element size")
     # FusedLinear-GRPO: hidden (B, L+1, H), weight [V, H]
     head = [p, p, p, p, p, p, p, p, p, p, p, p, 8, 1, p, None, 0, 0, None, 0, 0, None, 0, 0, 0, 2, 7]
-    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 3, 0, ws, 1 << 30, None),
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 3, 0, 0, ws, 1 << 30, None),
                    "fp32, bf16 and fp16")
-    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 100, 1.0, 0.0, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
-                   "multiples of 8")
-    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.1, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 0, 128, 1.0, 0.0, 0.2, 0.2, 2, 0, 0, ws, 1 << 30, None),
+                   "invalid shape")
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.1, 0.2, 0.2, 2, 0, 0, ws, 1 << 30, None),
                    "ref_logp")
-    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, -1.0, 0.0, 0.2, 0.2, 2, 0, ws, 1 << 30, None),
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, -1.0, 0.0, 0.2, 0.2, 2, 0, 0, ws, 1 << 30, None),
                    "temperature")
-    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 2, 0, ws, 64, None),
+    _expect_einval(lib.hk_fused_linear_grpo(*head, 64, 128, 1.0, 0.0, 0.2, 0.2, 2, 0, 0, ws, 64, None),
                    "workspace too small")
+    # FusedLinearJSD
+    jsd = [p, p, p, p, p, p, p, None]
+    _expect_einval(lib.hk_fused_linear_jsd(*jsd, 64, 64, 64, 128, -100, 1.5, 1.0, 2, 0, 0, ws, 1 << 30, None), "beta")
+    _expect_einval(lib.hk_fused_linear_jsd(*jsd, 64, 64, 0, 128, -100, 0.5, 1.0, 2, 0, 0, ws, 1 << 30, None),
+                   "teacher hidden size")
     # AttnRes
     _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 33, 16, 64, 1e-6, 2, None), "1..32 blocks")
     _expect_einval(lib.hk_attn_res_fwd(p, p, p, p, p, p, 4, 16, 12, 1e-6, 2, None), "multiple of 8")
@@ -121,21 +130,65 @@ def test_argument_validation_losses_without_gpu():
     _expect_einval(lib.hk_stream_mix(p, p, 64, 72, 2, 1, None), "stride")
 
 
+def _flce_ws(BT, H, V, budget=0, dtype=2, grad=1, chunk=0):
+    return _lib.load().hk_fused_linear_cross_entropy_workspace_size(BT, H, V, chunk, budget, dtype, grad, None, None)
+
+
+def _flce_plan(BT, H, V, budget=0, dtype=2, grad=1, chunk=0):
+    info = (ctypes.c_int64 * 8)()
+    _lib.check(_lib.load().hk_fused_linear_cross_entropy_plan(BT, H, V, chunk, budget, dtype, grad, None, None, info),
+               "plan")
+    return list(info)
+
+
 @needs_lib
 def test_fused_linear_workspace_queries():
     lib = _lib.load()
-    # fp32, bf16 and fp16 (fp32 operands take twice the bytes); an unknown dtype needs no workspace; a gradient
-    # call needs more (transposed operands, D^T) than a loss-only call
-    assert lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 5, 1) == 0
-    assert lib.hk_fused_linear_cross_entropy_workspace_size(256, 4096, 32000, 0, 0, 1) > \
-        lib.hk_fused_linear_cross_entropy_workspace_size(256, 4096, 32000, 0, 2, 1)
-    fwd = lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 2, 0)
-    bwd = lib.hk_fused_linear_cross_entropy_workspace_size(16384, 4096, 128256, 0, 2, 1)
-    assert 0 < fwd < bwd
-    # C5 keeps every chunk's D^T (4.2 GB) instead of one chunk's plus the 2.1 GB fp32 accumulator: no more memory
-    assert bwd < 12 * 2**30
-    assert lib.hk_fused_linear_grpo_workspace_size(16, 1023, 4096, 151936, 0, 2, 1) > 0
-    assert lib.hk_fused_linear_grpo_workspace_size(0, 1023, 4096, 151936, 0, 2, 1) == 0
+    MiB = 2**20
+    # an unknown dtype needs no workspace; a gradient call needs more than a loss-only call
+    assert _flce_ws(16384, 4096, 128256, dtype=5) == 0
+    assert 0 < _flce_ws(16384, 4096, 128256, grad=0) < _flce_ws(16384, 4096, 128256)
+    # the default plan costs what the reference's chunk costs (fused_linear_cross_entropy.py:112-114):
+    # chunk logits about the size of the hidden states, plus the gathered rows, their transpose and a quarter
+    # of the chunk for split partials; nothing grows with BT x V
+    for BT, H, V, rows in ((4096, 4096, 128256, 128), (8192, 4096, 128256, 256), (8192, 4096, 32000, 1024),
+                           (16384, 4096, 128256, 512)):
+        chunk_bytes = rows * ((V + 63) // 64 * 64) * 2
+        ws = _flce_ws(BT, H, V)
+        assert 0 < ws <= 1.25 * chunk_bytes + 2 * rows * H * 2 + 16 * BT + MiB, (BT, H, V, ws)
+        C, nch, dw, wt, dt, _, total, _ = _flce_plan(BT, H, V)
+        assert total == ws and C * nch >= BT and dw == 2 and not wt and not dt  # the leanest form
+    # 47.7% below the unfused path's peak at the reference's tightest memory config (N 4096, V 128256,
+    # fp16): h + w + logits + log-softmax + their two gradients at most, against h, w, both gradients and
+    # the workspace here
+    BT, H, V = 4096, 4096, 128256
+    unfused = 2 * (BT * H + V * H + 3 * BT * V)
+    ours = 2 * 2 * (BT * H + V * H) + _flce_ws(BT, H, V, dtype=1)
+    assert ours <= (1 - 0.477) * unfused
+    # no limit: C5 takes the fastest plan, every chunk's D^T kept and one dW GEMM (GBs of workspace)
+    C, nch, dw, wt, dt, _, total, model = _flce_plan(16384, 4096, 128256, budget=-1)
+    assert (C, nch, dw, wt, dt) == (8192, 2, 0, 1, 1) and total > 4 * 2**30
+    # a larger budget never gives a slower modelled plan; each plan fits its budget
+    prev = None
+    for b in (64 * MiB, 256 * MiB, 1 << 30, 4 << 30, 16 << 30):
+        C, nch, dw, wt, dt, _, total, model = _flce_plan(16384, 4096, 128256, budget=b)
+        assert total <= b
+        assert prev is None or model <= prev
+        prev = model
+    # a budget below the smallest plan: no workspace size (and the op rejects the call)
+    assert _flce_ws(64, 64, 128, budget=4096) == 0
+    # fp32 has no MN-contiguous operand form: W^T and D^T are always materialised
+    _, _, _, wt, dt, _, _, _ = _flce_plan(256, 4096, 32000, dtype=0)
+    assert wt and dt
+    # any H and V: an odd hidden size pads the weight into a copy (weight-sized workspace)
+    assert _flce_ws(512, 4099, 32001) > 32001 * 4104 * 2
+    # a misaligned weight is copied too
+    assert (lib.hk_fused_linear_cross_entropy_workspace_size(512, 4096, 32000, 0, 0, 2, 1, None, ctypes.c_void_p(18))
+            > 32000 * 4096 * 2)
+    assert lib.hk_fused_linear_grpo_workspace_size(16, 1023, 4096, 151936, 0, 0, 2, 1, None, None) > 0
+    assert lib.hk_fused_linear_grpo_workspace_size(0, 1023, 4096, 151936, 0, 0, 2, 1, None, None) == 0
+    assert lib.hk_fused_linear_jsd_workspace_size(8192, 4096, 4096, 128256, 0, 0, 2, 1, 1, None, None, None,
+                                                  None) > 0
     assert lib.hk_attn_res_bwd_workspace_size(8192, 4096) % (2 * 4096 * 4) == 0
 
 

@@ -129,15 +129,20 @@ def test_flce_all_ignored_and_no_grad():
     assert_close(l_ng, l_ref, name="no-grad loss", rtol=2e-3, atol=2e-3)
 
 
-def test_flce_c5_config():
-    """C5: hidden [16384, 4096], weight [128256, 4096] bf16, 5% ignored, mean; on the GPU."""
+@pytest.mark.parametrize("budget", ["fastest", None])
+def test_flce_c5_config(budget):
+    """C5: hidden [16384, 4096], weight [128256, 4096] bf16, 5% ignored, mean; on the GPU, in the unlimited
+    plan (two 8192-row chunks, one dW GEMM over every row) and the default one (the reference's chunk: 43
+    chunks, dW accumulated in bf16 in the output as the reference's addmm does, fused_linear_cross_entropy.py:161)."""
     dev = gpu()
     c = workloads.c5_fused_linear_ce(device=dev)
     h, w, t = c["hidden"], c["weight"], c["targets"]
-    loss_rows, _, _, _ = fl.fused_linear_cross_entropy_forward(h, w, t, -100, "none", compute_grad=False)
+    print(f"C5 budget={budget}", flush=True)
+    loss_rows, _, _, _ = fl.fused_linear_cross_entropy_forward(h, w, t, -100, "none", compute_grad=False,
+                                                               workspace_budget=budget)
     hg = h.requires_grad_(True)
     wg = w.requires_grad_(True)
-    loss = hilda_fused_linear_cross_entropy(hg, wg, t)
+    loss = hilda_fused_linear_cross_entropy(hg, wg, t, workspace_budget=budget)
     loss.backward()
     valid = t != -100
     n_valid = int(valid.sum())
@@ -161,10 +166,15 @@ def test_flce_c5_config():
     assert_close(hg.grad[idx].float() * n_valid, dh_ref, name="dhidden rows * n_valid", **tol(torch.bfloat16))
     assert rel_fro(hg.grad[idx].float() * n_valid, dh_ref) < 1e-2
     # <X, dX> = <W, dW>: both equal sum_{r,v} D_rv Z_rv (Z = X W^T, D the logits gradient), so a
-    # dropped chunk, a wrong scale or mispaired rows in either GEMM breaks the equality
+    # dropped chunk, a wrong scale or mispaired rows in either GEMM breaks the equality. With dW summed in
+    # bf16 over 43 chunks, a vocabulary row that is some row's target holds a term ~1/n_valid, and the later
+    # chunks' softmax terms (~1e-4 of it) round away: the 11% of rows that are targets lose about half
+    # their softmax mass, which is sum_v p_v z_v = E_p[z], about 1.6 of the 1.65 here (measured 4.5% low).
+    # 1% (fp32 sums) catches a dropped chunk of two; 10% (bf16 sums) a wrong scale or mispaired GEMM rows,
+    # while a dropped chunk of 43 shows in the sampled dhidden rows above (one or two in every chunk).
     ip_x = (h.detach().double() * hg.grad.double()).sum().item()
     ip_w = (w.detach().double() * wg.grad.double()).sum().item()
-    assert math.isclose(ip_x, ip_w, rel_tol=1e-2), (ip_x, ip_w)
+    assert math.isclose(ip_x, ip_w, rel_tol=1e-2 if budget == "fastest" else 0.1), (ip_x, ip_w)
     # sampled vocabulary rows of dW against the oracle summed over all 16384 rows: each live row's
     # log-sum-exp from CPU fp32 logits (bf16 products summed in fp32, rounded to bf16 as the GEMM
     # returns them), then D[:, v] and dW[v] = D[:, v]^T X in fp64
@@ -274,3 +284,179 @@ def test_flce_wide_logits(dtype, BT, V):
     _rows_check("dweight", gw, dw_ref, 2.0 ** -24 * math.sqrt(BT * H) if dtype == torch.float16 else 0.0)
     _rows_check("dhidden", gi, dh_ref, slack)
     assert torch.count_nonzero(gi[(t == -100).to(dev)]).item() == 0
+
+
+# Every memory plan of the chunk engine: the dW form (every chunk's D^T kept and one GEMM after the loop; an fp32
+# accumulator; accumulated in the output), W^T or W read MN-contiguous by the dX GEMM, D^T or D read
+# MN-contiguous by the dW GEMM (HILDA_FL_FORM forces one; the budget is unlimited).
+FORMS = ["defer,wt,dt", "defer,wmn,dt", "acc,wt,dt", "acc,wt,dmn", "acc,wmn,dt", "acc,wmn,dmn",
+         "out,wt,dt", "out,wt,dmn", "out,wmn,dt", "out,wmn,dmn"]
+DW_NAME = {"defer": "deferred", "acc": "fp32 accumulator", "out": "in output"}
+
+
+@pytest.mark.parametrize("form", FORMS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_flce_plan_forms(form, dtype, monkeypatch):
+    """V = 2000 and H = 264 (neither a multiple of 64), five chunks of 128 rows, a wholly ignored chunk and live
+    rows ending mid-chunk: each form against the fp64 oracle, exact zeros on ignored rows."""
+    BT, H, V = 600, 264, 2000
+    h, w, t = _case(BT, H, V, dtype, 7)
+    t[200:330] = -100
+    monkeypatch.setenv("HILDA_FL_FORM", form)
+    dw, wf, df = form.split(",")
+    plan = fl.fused_linear_cross_entropy_plan(BT, H, V, dtype, chunk=128, workspace_budget=-1)
+    assert (plan["dw"], plan["w_transposed"], plan["d_transposed"]) == (DW_NAME[dw], wf == "wt", df == "dt")
+    assert plan["chunks"] == 5
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, "sum")
+    dev = gpu()
+    print(f"FLCE form {form} {dtype}", flush=True)
+    loss, gi, gw, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "sum",
+                                                            compute_grad=True, chunk=128, workspace_budget=-1)
+    assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
+    tt = tol(dtype)
+    assert_close(gi, dh_ref, name="dhidden", **tt)
+    assert rel_fro(gi, dh_ref) < 1e-2
+    assert torch.count_nonzero(gi[(t == -100).to(dev)]).item() == 0
+    if dw != "out":
+        # dW summed in fp32 and rounded once
+        assert_close(gw, dw_ref, name="dweight", **tt)
+        assert rel_fro(gw, dw_ref) < 1e-2
+        return
+    # dW accumulated in the 16-bit output, chunk by chunk (the reference's addmm into its bf16 grad_weight,
+    # fused_linear_cross_entropy.py:161): emulate that in fp64 over the same chunks of live rows (each chunk's
+    # partial added to the running 16-bit sum and rounded). The kernel's error against the exact dW is that
+    # arithmetic's (its D entries may sit one rounding step from the emulation's, so compare norms): no
+    # larger than the emulation's own error plus a margin, and close to the emulation itself.
+    emu = _chunked_dw(h, w, t, 128, dtype)
+    e_ours, e_emu = rel_fro(gw, dw_ref), rel_fro(emu, dw_ref)
+    print(f"in-output dW: rel error {e_ours:.3e}, emulated reference arithmetic {e_emu:.3e}", flush=True)
+    assert e_ours <= 1.5 * e_emu + 1e-3
+    assert rel_fro(gw, emu) < 1e-2
+
+
+def _chunked_dw(h, w, t, C, dtype):
+    """dW of the sum-reduced CE accumulated chunk by chunk in `dtype` (live rows compacted in order, C a chunk)."""
+    live = (t != -100).nonzero().squeeze(1)
+    hd, wd = h.double(), w.double()
+    z = (hd[live] @ wd.T).to(dtype).double()
+    d = torch.softmax(z, -1)
+    d[torch.arange(live.numel()), t[live]] -= 1.0
+    d = d.to(dtype).double()  # the gradient stored over the 16-bit logits
+    acc = None
+    for c0 in range(0, live.numel(), C):
+        part = d[c0:c0 + C].T @ hd[live[c0:c0 + C]]
+        acc = part.to(dtype).double() if acc is None else (acc + part).to(dtype).double()
+    return acc
+
+
+@pytest.mark.parametrize("form", ["defer,wt,dt", "out,wt,dt"])
+def test_flce_plan_forms_fp32(form, monkeypatch):
+    """fp32 takes the materialised forms only; accumulating dW in the fp32 output is an fp32 sum, so both
+    forms meet the fp32 tolerance (rtol/atol 1e-5) against the fp64 oracle."""
+    BT, H, V = 300, 136, 1000
+    h, w, t = _case(BT, H, V, torch.float32, 8)
+    monkeypatch.setenv("HILDA_FL_FORM", form)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, "mean")
+    dev = gpu()
+    loss, gi, gw, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "mean",
+                                                            compute_grad=True, chunk=64, workspace_budget=-1)
+    n = int((t != -100).sum())
+    tt = tol(torch.float32)
+    assert_close(loss, l_ref, name="loss", **tt)
+    assert_close(gi * n, dh_ref * n, name="dhidden*n", **tt)
+    assert_close(gw * n, dw_ref * n, name="dweight*n", **tt)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("BT,H,V", [(64, 256, 32001), (48, 128, 50257), (96, 257, 1003), (40, 1027, 600)])
+@pytest.mark.parametrize("budget", [None, -1])
+def test_flce_any_shape(dtype, BT, H, V, budget):
+    """Vocabulary and hidden sizes that are not multiples of 8 (GPT-2's 50257, 32001) against the oracle, in
+    the default (reference-sized) plan and the unlimited one: the chunk buffer's stride is padded, its columns
+    past V are -inf logits and zero gradients, an odd H is padded in the gathered rows and a weight copy."""
+    h, w, t = _case(BT, H, V, dtype, BT + H + V)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(h, w, t, "mean")
+    dev = gpu()
+    print(f"FLCE any shape BT={BT} H={H} V={V} {dtype} budget={budget}", flush=True)
+    hg = h.to(dev).requires_grad_(True)
+    wg = w.to(dev).requires_grad_(True)
+    loss = hilda_fused_linear_cross_entropy(hg, wg, t.to(dev), workspace_budget=budget)
+    loss.backward()
+    n = int((t != -100).sum())
+    tt = tol(dtype)
+    lt = tt if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
+    assert_close(loss, l_ref, name="loss", **lt)
+    assert_close(hg.grad.float() * n, dh_ref * n, name="dhidden*n", **tt)
+    assert_close(wg.grad.float() * n, dw_ref * n, name="dweight*n", **tt)
+    if dtype != torch.float32:
+        assert rel_fro(hg.grad, dh_ref) < 1e-2 and rel_fro(wg.grad, dw_ref) < 1e-2
+    assert torch.count_nonzero(hg.grad[(t == -100).to(dev)]).item() == 0
+
+
+@pytest.mark.parametrize("budget", [None, -1])
+def test_flce_misaligned_inputs(budget):
+    """hidden and weight views that start 2 bytes into their storage (not 16-byte aligned): read element by
+    element into the gathered rows and a weight copy, with the same results as aligned copies."""
+    BT, H, V = 200, 256, 3000
+    dtype = torch.bfloat16
+    h, w, t = _case(BT, H, V, dtype, 3)
+    dev = gpu()
+    hs = torch.empty(BT * H + 1, dtype=dtype, device=dev)
+    ws = torch.empty(V * H + 1, dtype=dtype, device=dev)
+    hv, wv = hs[1:].view(BT, H), ws[1:].view(V, H)
+    hv.copy_(h.to(dev))
+    wv.copy_(w.to(dev))
+    assert hv.data_ptr() % 16 != 0 and wv.data_ptr() % 16 != 0
+    la, gia, gwa, _ = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "none",
+                                                            compute_grad=True, workspace_budget=budget)
+    lm, gim, gwm, _ = fl.fused_linear_cross_entropy_forward(hv, wv, t.to(dev), -100, "none", compute_grad=True,
+                                                            workspace_budget=budget)
+    assert torch.equal(la, lm) and torch.equal(gia, gim) and torch.equal(gwa, gwm)
+
+
+def test_flce_default_and_fastest_plans_agree():
+    """The logits GEMM and the CE rows are the same code in every plan, so the per-row losses are bitwise
+    equal between the default plan and the unlimited one; the gradients agree to bf16 rounding."""
+    BT, H, V = 1024, 512, 20000
+    h, w, t = _case(BT, H, V, torch.bfloat16, 12)
+    dev = gpu()
+    fast = fl.fused_linear_cross_entropy_plan(BT, H, V, torch.bfloat16, workspace_budget=-1)
+    lean = fl.fused_linear_cross_entropy_plan(BT, H, V, torch.bfloat16)
+    assert lean["workspace_bytes"] < fast["workspace_bytes"] and lean["chunks"] > fast["chunks"]
+    out = {}
+    for name, b in (("lean", None), ("fast", -1)):
+        out[name] = fl.fused_linear_cross_entropy_forward(h.to(dev), w.to(dev), t.to(dev), -100, "none",
+                                                          compute_grad=True, workspace_budget=b)
+    assert torch.equal(out["lean"][0], out["fast"][0])
+    assert rel_fro(out["lean"][1], out["fast"][1]) < 1e-2 and rel_fro(out["lean"][2], out["fast"][2]) < 1e-2
+
+
+def test_flce_peak_memory_below_unfused():
+    """Peak memory of fwd+bwd, measured as the reference's benchmark does (bench_fused_linear_ce.py:171-178,
+    leaves allocated inside the measured function): the default plan stays at least 47.7% below torch's
+    unfused hidden @ W.T + cross_entropy (the low end of the reference's claim, README.md:42)."""
+    BT, H, V = 2048, 1024, 50257
+    dtype = torch.float16
+    dev = gpu()
+    t = torch.randint(0, V, (BT,), device=dev)
+
+    def peak(fn):
+        fn()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        fn()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated(dev) - base
+
+    def run(f):
+        def fn():
+            h = torch.randn(BT, H, device=dev, dtype=dtype, requires_grad=True)
+            w = torch.randn(V, H, device=dev, dtype=dtype, requires_grad=True)
+            f(h, w).backward()
+        return fn
+
+    unfused = peak(run(lambda h, w: torch.nn.functional.cross_entropy(h @ w.T, t)))
+    ours = peak(run(lambda h, w: hilda_fused_linear_cross_entropy(h, w, t)))
+    print(f"peak MiB: unfused {unfused / 2**20:.1f}, default plan {ours / 2**20:.1f}", flush=True)
+    assert ours <= (1 - 0.477) * unfused

@@ -163,8 +163,8 @@ def test_fused_linear_grpo_rejects():
     adv = torch.zeros(2, device=dev)
     with pytest.raises(TypeError):
         hilda_fused_linear_grpo_loss(h.double(), w.double(), ids, adv)
-    with pytest.raises(RuntimeError, match="multiples of 8"):
-        hilda_fused_linear_grpo_loss(h, w[:99], ids, adv)
+    with pytest.raises(RuntimeError, match="workspace budget"):  # below the smallest plan
+        hilda_fused_linear_grpo_loss(h, w[:99], ids, adv, workspace_budget=1024)
     with pytest.raises(ValueError):
         hilda_fused_linear_grpo_loss(h, w[:96], ids, adv, beta=0.1)
 
@@ -237,3 +237,42 @@ def test_fused_linear_grpo_masked_sequences(chunk):
     live[:, :L] = mask.bool()
     assert torch.count_nonzero(gh.cpu()[~live]).item() == 0
     assert torch.count_nonzero(rows[1].cpu()[~mask.bool()]).item() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("budget", [None, -1])
+def test_fused_linear_grpo_any_shape(dtype, budget):
+    """H = 133 and V = 1001 (not multiples of 8): the GRPO row kernel reads rows padded with -inf logits to the
+    next 16-byte multiple (probability and gradient 0 there); default and unlimited plans against the oracle."""
+    B, L, H, V = 3, 20, 133, 1001
+    beta, T, el, eh = 0.1, 1.0, 0.2, 0.2
+    h, w, ids, adv, old, ref, mask = _case(B, L, H, V, dtype, 123)
+    outs, (dh_ref, dw_ref) = _oracle(h, w, ids, adv, old, ref, mask, T, beta, el, eh)
+    dev = gpu()
+    print(f"FL-GRPO any shape {dtype} budget={budget}", flush=True)
+    args = (ids.to(dev), adv.to(dev), _dev(old), _dev(ref), _dev(mask), T, beta, el, eh)
+    loss, kl, clip, gh, gw, _ = flg.fused_linear_grpo_forward(h.to(dev), w.to(dev), *args, chunk=16,
+                                                              workspace_budget=budget)
+    lt = tol(dtype) if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
+    assert_close(loss, outs[0], name="loss", **lt)
+    assert_close(kl, outs[1], name="kl_mean", **lt)
+    scale = B * L
+    assert_close(gh.float() * scale, dh_ref * scale, name="dhidden*B*L", **tol(dtype))
+    assert_close(gw.float() * scale, dw_ref * scale, name="dweight*B*L", **tol(dtype))
+    assert torch.count_nonzero(gh[:, -1]).item() == 0
+
+
+@pytest.mark.parametrize("form", ["out,wmn,dmn", "acc,wmn,dt", "defer,wt,dt"])
+def test_fused_linear_grpo_plan_forms(form, monkeypatch):
+    B, L, H, V = 4, 30, 64, 1500
+    dtype = torch.bfloat16
+    h, w, ids, adv, old, ref, mask = _case(B, L, H, V, dtype, 321)
+    outs, (dh_ref, dw_ref) = _oracle(h, w, ids, adv, old, ref, mask, 1.0, 0.1, 0.2, 0.2)
+    monkeypatch.setenv("HILDA_FL_FORM", form)
+    dev = gpu()
+    args = (ids.to(dev), adv.to(dev), old.to(dev), ref.to(dev), mask.to(dev), 1.0, 0.1, 0.2, 0.2)
+    loss, kl, clip, gh, gw, _ = flg.fused_linear_grpo_forward(h.to(dev), w.to(dev), *args, chunk=24,
+                                                              workspace_budget=-1)
+    assert_close(loss, outs[0], name="loss", rtol=2e-3, atol=2e-3)
+    assert rel_fro(gh, dh_ref) < 1e-2 and rel_fro(gw, dw_ref) < 1e-2
+    assert_close(gw.float() * B * L, dw_ref * B * L, name="dweight*B*L", **tol(dtype))

@@ -172,3 +172,41 @@ def test_fused_linear_jsd_compaction_and_chunks(labels_kind, BT, chunk):
     assert rel_fro(gi, dh_ref.to(dtype)) < 1e-2 and rel_fro(gw, dw_ref.to(dtype)) < 1e-2
     if labels is not None:
         assert torch.count_nonzero(gi[(labels == -100).to(dev)]).item() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("labels_on", [True, False])
+@pytest.mark.parametrize("budget", [None, -1])
+def test_fused_linear_jsd_any_shape(dtype, labels_on, budget):
+    """Student H, teacher Ht and V that are not multiples of 8: padded rows, weight copies and a padded chunk
+    stride (zeros past V in both logits chunks), in the default and the unlimited plan, against the oracle."""
+    BT, H, Ht, V = 96, 257, 131, 1003
+    si, sw, ti, tw, labels = _case(BT, H, Ht, V, dtype, 5, with_labels=labels_on)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(si, sw, ti, tw, labels, 0.5, 1.0)
+    dev = gpu()
+    print(f"FLJSD any shape {dtype} labels={labels_on} budget={budget}", flush=True)
+    loss, gi, gw = fj.fused_linear_jsd_forward(si.to(dev), sw.to(dev), ti.to(dev), tw.to(dev),
+                                               None if labels is None else labels.to(dev), 0.5, 1.0, -100,
+                                               compute_grad=True, chunk=32, workspace_budget=budget)
+    n = BT if labels is None else max(int((labels != -100).sum()), 1)
+    lt = tol(dtype) if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
+    assert_close(loss, l_ref, name="loss", **lt)
+    tt = tol(dtype)
+    assert_close(gi.float() * n, dh_ref * n, name="dinput*n", **tt)
+    assert_close(gw.float() * n, dw_ref * n, name="dweight*n", **tt)
+
+
+@pytest.mark.parametrize("form", ["out,wmn,dmn", "acc,wt,dmn", "defer,wmn,dt"])
+def test_fused_linear_jsd_plan_forms(form, monkeypatch):
+    BT, H, Ht, V = 300, 128, 64, 2000
+    dtype = torch.bfloat16
+    si, sw, ti, tw, labels = _case(BT, H, Ht, V, dtype, 6)
+    monkeypatch.setenv("HILDA_FL_FORM", form)
+    (l_ref,), (dh_ref, dw_ref) = _oracle(si, sw, ti, tw, labels, 0.5, 1.0)
+    dev = gpu()
+    loss, gi, gw = fj.fused_linear_jsd_forward(si.to(dev), sw.to(dev), ti.to(dev), tw.to(dev), labels.to(dev), 0.5,
+                                               1.0, -100, compute_grad=True, chunk=64, workspace_budget=-1)
+    n = max(int((labels != -100).sum()), 1)
+    assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
+    assert rel_fro(gi, dh_ref.to(dtype)) < 1e-2 and rel_fro(gw, dw_ref.to(dtype)) < 1e-2
+    assert_close(gw.float() * n, dw_ref * n, name="dweight*n", **tol(dtype))

@@ -403,6 +403,176 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(T* __restrict__ C, int6
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Vocabulary-tiled CrossEntropy row passes. The logits tile holds every row's
+// columns [v0, v0 + w) (row stride ld); logits are scaled by log2(e) into
+// base 2. VtRow is a row's state across the tiles: the running maximum m,
+// the sum sx of 2^(z - m) over the columns seen that are not the target, and
+// the target logit zt (-inf until its tile). After vt_finalize_kernel: m holds
+// the base-2 log-sum-exp and sx 1 - p_target (formed from the other columns'
+// mass, so a peaked row keeps its small target gradient exact).
+// ---------------------------------------------------------------------------
+struct VtRow {
+  float m, sx, zt, pad;
+};
+
+constexpr int kVtLanes = 256;
+constexpr int kVtVec = 4;  // 16-byte vectors a lane holds: rows of up to 256 x 4 x 16 bytes
+
+template <typename T>
+__device__ __forceinline__ void vt_load(const T* row, int64_t w, float (&x)[kVtVec][16 / sizeof(T)]) {
+  constexpr int E = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int k = 0; k < kVtVec; ++k) {
+    const int64_t j0 = ((int64_t)k * kVtLanes + threadIdx.x) * E;
+    if (j0 + E <= w) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(row + j0);
+      const T* e = reinterpret_cast<const T*>(&v);
+#pragma unroll
+      for (int i = 0; i < E; ++i) x[k][i] = to_f32<T>(e[i]) * kLog2e;
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) x[k][i] = j0 + i < w ? to_f32<T>(row[j0 + i]) * kLog2e : -__builtin_huge_valf();
+    }
+  }
+}
+
+// One block a row (grid-stride): the tile's max and non-target sum, merged into the row state.
+template <typename T>
+__global__ __launch_bounds__(kVtLanes) void vt_lse_kernel(const T* __restrict__ L, int64_t ld, int64_t w, int64_t v0,
+                                                        const int64_t* __restrict__ targets, int64_t ignore_index,
+                                                        VtRow* __restrict__ state, int64_t rows, int first) {
+  constexpr int E = 16 / (int)sizeof(T);
+  __shared__ float red[kVtLanes / kWave];
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const int64_t t = targets[r];
+    if (t == ignore_index) continue;  // uniform in the block
+    const int64_t tl = t - v0;         // the target's column in this tile, if it is here
+    float x[kVtVec][E];
+    vt_load<T>(L + r * ld, w, x);
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int k = 0; k < kVtVec; ++k)
+#pragma unroll
+      for (int i = 0; i < E; ++i) m = fmaxf(m, x[k][i]);
+    m = block_max<kVtLanes / kWave>(m, red);
+    float sx = 0.f, zt = -__builtin_huge_valf();
+#pragma unroll
+    for (int k = 0; k < kVtVec; ++k)
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int64_t j = ((int64_t)k * kVtLanes + threadIdx.x) * E + i;
+        if (j == tl) zt = x[k][i];
+        else sx += exp2_fast(x[k][i] - m);  // (-inf columns add 0)
+      }
+    sx = block_sum<kVtLanes / kWave>(sx, red);
+    zt = block_max<kVtLanes / kWave>(zt, red);
+    if (threadIdx.x == 0) {
+      VtRow q = first ? VtRow{-__builtin_huge_valf(), 0.f, -__builtin_huge_valf(), 0.f} : state[r];
+      const float M = fmaxf(q.m, m);
+      q.sx = (q.sx > 0.f ? q.sx * exp2_fast(q.m - M) : 0.f) + (sx > 0.f ? sx * exp2_fast(m - M) : 0.f);
+      q.m = M;
+      if (tl >= 0 && tl < w) q.zt = zt;
+      state[r] = q;
+    }
+  }
+}
+
+// Per row after the last tile: loss (times s when scale), and the state turned
+// into (base-2 log-sum-exp, 1 - p_target).
+__global__ __launch_bounds__(256) void vt_finalize_kernel(VtRow* __restrict__ state, float* __restrict__ loss_rows,
+                                                          const int64_t* __restrict__ targets, int64_t ignore_index,
+                                                          const int* __restrict__ n_valid, int scale, int64_t rows) {
+  const float s = scale ? 1.f / (float)max(*n_valid, 1) : 1.f;
+  for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < rows; r += (int64_t)gridDim.x * 256) {
+    if (targets[r] == ignore_index) {
+      loss_rows[r] = 0.f;
+      continue;
+    }
+    VtRow q = state[r];
+    const float et = exp2_fast(q.zt - q.m);
+    const float tot = q.sx + et;
+    const float lse2 = q.m + log2_fast(tot);
+    loss_rows[r] = (lse2 - q.zt) * kLn2 * s;
+    state[r] = VtRow{lse2, q.sx / tot, q.zt, 0.f};
+  }
+}
+
+// The gradient tile in place: D = (p - onehot) * g with g = s * row_scale[r]
+// (s = 1 / max(n_valid, 1) when scale), the target entry -(1 - p_t) * g;
+// columns [w, wz) and ignored rows are zero.
+template <typename T>
+__global__ __launch_bounds__(kVtLanes) void vt_grad_kernel(T* __restrict__ L, int64_t ld, int64_t w, int64_t wz,
+                                                         int64_t v0, const int64_t* __restrict__ targets,
+                                                         int64_t ignore_index, const VtRow* __restrict__ state,
+                                                         const int* __restrict__ n_valid, int scale,
+                                                         const float* __restrict__ row_scale, int64_t rows) {
+  constexpr int E = 16 / (int)sizeof(T);
+  const float s = scale ? 1.f / (float)max(*n_valid, 1) : 1.f;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    T* row = L + r * ld;
+    const int64_t t = targets[r];
+    const bool dead = t == ignore_index;
+    const VtRow q = dead ? VtRow{0.f, 0.f, 0.f, 0.f} : state[r];
+    const float g = dead ? 0.f : s * (row_scale ? row_scale[r] : 1.f);
+    const int64_t tl = t - v0;
+    float x[kVtVec][E];
+    if (!dead) vt_load<T>(row, w, x);
+#pragma unroll
+    for (int k = 0; k < kVtVec; ++k) {
+      const int64_t j0 = ((int64_t)k * kVtLanes + threadIdx.x) * E;
+      if (j0 >= wz) continue;
+      T out[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int64_t j = j0 + i;
+        float d = 0.f;
+        if (!dead && j < w) d = j == tl ? -q.sx * g : exp2_fast(x[k][i] - q.m) * g;
+        out[i] = from_f32<T>(d);
+      }
+      if (j0 + E <= wz) {
+        *reinterpret_cast<u32x4*>(row + j0) = *reinterpret_cast<const u32x4*>(out);
+      } else {
+        for (int i = 0; i < E && j0 + i < wz; ++i) row[j0 + i] = out[i];
+      }
+    }
+  }
+}
+
+
+// The tile's target entries set to zero (after the tile's dW GEMM has read them):
+// dX is then summed across the tiles from softmax terms alone, of like size, and
+// vt_target_dx_kernel adds each row's target term once at the end.
+template <typename T>
+__global__ __launch_bounds__(256) void vt_drop_targets_kernel(T* __restrict__ L, int64_t ld, int64_t w, int64_t v0,
+                                                              const int64_t* __restrict__ targets,
+                                                              int64_t ignore_index, int64_t rows) {
+  for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < rows; r += (int64_t)gridDim.x * 256) {
+    const int64_t t = targets[r];
+    if (t != ignore_index && t >= v0 && t < v0 + w) L[r * ld + (t - v0)] = from_f32<T>(0.f);
+  }
+}
+
+// dX[r] += -(1 - p_target) * g * W[target] for every live row, in fp32, rounded once (one block a row).
+template <typename T>
+__global__ __launch_bounds__(256) void vt_target_dx_kernel(T* __restrict__ dX, int64_t H, const T* __restrict__ W,
+                                                           int64_t ldw, const int64_t* __restrict__ targets,
+                                                           int64_t ignore_index, int64_t V,
+                                                           const VtRow* __restrict__ state,
+                                                           const int* __restrict__ n_valid, int scale,
+                                                           const float* __restrict__ row_scale, int64_t rows) {
+  const float s = scale ? 1.f / (float)max(*n_valid, 1) : 1.f;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const int64_t t = targets[r];
+    if (t == ignore_index || t < 0 || t >= V) continue;
+    const float c = -state[r].sx * s * (row_scale ? row_scale[r] : 1.f);
+    const T* wr = W + t * ldw;
+    T* o = dX + r * H;
+    for (int64_t j = threadIdx.x; j < H; j += 256) o[j] = from_f32<T>(to_f32<T>(o[j]) + c * to_f32<T>(wr[j]));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -526,6 +696,7 @@ struct FlShape {
   size_t fixed_extra;  // the row step's own scratch, bytes
   size_t row_extra;    // and per chunk row
   int64_t chunk_cap;   // rows per chunk at most (<= 0: no cap below 8192)
+  bool vt_ok = false;  // the vocabulary-tiled plan applies (CrossEntropy on 16-bit inputs)
 };
 
 struct FlPlan {
@@ -540,6 +711,13 @@ struct FlPlan {
   size_t nvalid = 0, nlive = 0, rowmap = 0, inv = 0, tc = 0, sc = 0, lc = 0;
   size_t xg = 0, xt = 0, lg = 0, wtp = 0, wp = 0, dtp = 0, acc = 0, part = 0, extra = 0, total = 0;
   double cost = 0;
+  // the vocabulary-tiled plan: tiles of Vt vocabulary columns over every row
+  // (the logits tile [BT, Vt] at lg), per-row state at vst, the hidden rows
+  // padded at xg when they cannot be read in place; dw = kDwAcc sums dX in an
+  // fp32 [BT, Hp] buffer at acc, kDwOut in the output
+  bool vtile = false;
+  int64_t Vt = 0, ntiles = 0;
+  size_t vst = 0;
 };
 
 int dx_bk(int es) { return es == 4 ? gemm::F32Cfg::BK : gemm::DefaultCfg::BK; }
@@ -607,6 +785,64 @@ FlPlan fl_layout(const FlShape& s, int64_t C, bool wt, bool dt, int dw, int smax
   return p;
 }
 
+// The vocabulary-tiled candidate: tiles of Vt columns (a multiple of 256) over
+// all BT rows; dX summed in fp32 (dw = kDwAcc) or in the output (kDwOut).
+FlPlan vt_layout(const FlShape& s, int64_t Vt, int dw) {
+  FlPlan p;
+  p.vtile = true;
+  p.Vt = Vt;
+  p.ntiles = cdiv(s.V, Vt);
+  p.C = Vt;
+  p.nch = p.ntiles;
+  p.Hp = pad8(s.H);
+  p.V8 = pad8(s.V);
+  p.Vr = (s.V + 16 / s.es - 1) / (16 / s.es) * (16 / s.es);
+  p.ldl = Vt;
+  p.gather = !s.x_ok;
+  p.wpad = !s.w_ok;
+  p.dw = dw;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t es = (size_t)s.es, bt = (size_t)std::max<int64_t>(s.BT, 1);
+  p.nvalid = take(256);
+  p.nlive = take(256);
+  p.vst = take(bt * 16);
+  p.lg = take(bt * (size_t)Vt * es);
+  if (p.gather) p.xg = take(bt * (size_t)p.Hp * es);
+  if (p.wpad) p.wp = take((size_t)s.V * p.Hp * es);
+  if (s.grad && dw == kDwAcc && p.ntiles > 1) p.acc = take(bt * (size_t)p.Hp * 4);
+  p.total = off;
+  return p;
+}
+
+// Modelled time of a vocabulary-tiled candidate: the logits GEMM twice (the
+// log-sum-exp pass, then the gradient pass), the dW GEMM with both operands
+// MN-contiguous, the dX GEMM with W MN-contiguous, idle CUs when a GEMM has
+// fewer than 256 tiles, the row passes' HBM bytes and dX's read-modify-writes.
+double vt_cost(const FlShape& s, const FlPlan& p) {
+  const double Rg = 1.25e15, Rm = 5.0e12, pen = 1.15, launch = 5e-6;
+  const double es = s.es, BT = (double)s.BT, Hp = (double)p.Hp, V = (double)s.V;
+  const double F = 2.0 * BT * Hp * V;
+  auto fill = [](int64_t tiles) { return tiles >= 256 ? 1.0 : 256.0 / (double)std::max<int64_t>(tiles, 1); };
+  const int64_t tb = cdiv(s.BT, 256), tv = cdiv(p.Vt, 256), th = cdiv(p.Hp, 256);
+  double t = F / Rg * fill(tb * tv) + BT * V * es / Rm + p.ntiles * 3 * launch;
+  if (p.gather) t += 2.0 * es * BT * Hp / Rm;
+  if (p.wpad) t += 2.0 * es * V * Hp / Rm;
+  if (s.grad) {
+    t += F / Rg * fill(tb * tv) + 2.0 * BT * V * es / Rm;
+    t += F / Rg * fill(tv * th) * pen * pen;
+    t += F / Rg * fill(tb * th) * pen;
+    const double nt = (double)p.ntiles;
+    t += (p.dw == kDwAcc ? 8.0 * BT * Hp * (nt - 1) : 2.0 * es * BT * Hp * (nt - 1)) / Rm;
+    t += p.ntiles * 4 * launch;
+  }
+  return t;
+}
+
 // Modelled time (seconds) of a candidate: GEMMs at a kk-kernel rate, 15% more
 // for a GEMM with an MN-contiguous operand, tile waste of a short chunk, a dX
 // GEMM that leaves CUs idle, and the HBM bytes of the transposes, the dW
@@ -669,11 +905,14 @@ void fl_forms(const FlShape& s, int64_t nch, F&& f) {
 
 // A debugging override of the form (like MIOpen's MIOPEN_DEBUG_* variables):
 // HILDA_FL_FORM="<dw>,<w>,<d>" with dw one of defer / acc / out, w one of wt /
-// wmn, d one of dt / dmn restricts the plan to that form (the chunk still from
-// the budget). Returns false when unset; *bad when it does not parse.
-bool forced_form(int* dw, bool* wt, bool* dt, bool* bad) {
+// wmn, d one of dt / dmn restricts the plan to that row-chunked form (the chunk
+// still from the budget); "vtile,<acc|out>,<columns>" to the vocabulary-tiled
+// plan with that dX sum and tile width (a multiple of 256). Returns false when
+// unset; *bad when it does not parse. *vt: the tile width (0: row chunks).
+bool forced_form(int* dw, bool* wt, bool* dt, int64_t* vt, bool* bad) {
   const char* e = std::getenv("HILDA_FL_FORM");
   *bad = false;
+  *vt = 0;
   if (!e || !*e) return false;
   char a[16] = {0}, b[16] = {0}, c[16] = {0};
   if (std::sscanf(e, "%15[^,],%15[^,],%15s", a, b, c) != 3) {
@@ -681,6 +920,12 @@ bool forced_form(int* dw, bool* wt, bool* dt, bool* bad) {
     return true;
   }
   const std::string sa(a), sb(b), sc(c);
+  if (sa == "vtile") {
+    *dw = sb == "acc" ? kDwAcc : sb == "out" ? kDwOut : -1;
+    *vt = std::atoll(c);
+    *bad = *dw < 0 || *vt <= 0 || *vt % 256 != 0 || *vt > 8192;
+    return true;
+  }
   *dw = sa == "defer" ? kDwDefer : sa == "acc" ? kDwAcc : sa == "out" ? kDwOut : -1;
   *wt = sb == "wt";
   *dt = sc == "dt";
@@ -698,6 +943,7 @@ constexpr size_t kSmallWorkspace = (size_t)40 << 20;
 // dW summed in fp32 (or computed whole): every form but accumulation in a
 // 16-bit output over several chunks.
 bool exact_dw(const FlShape& s, const FlPlan& p) { return !s.grad || p.dw != kDwOut || p.nch <= 1 || s.es == 4; }
+// (a vocabulary-tiled plan writes dW once; its dX is summed across the tiles in the same ways)
 
 // The plan for a byte budget: budget == 0 the default (at most the larger of
 // kSmallWorkspace and what the reference's chunk costs in the leanest form),
@@ -708,9 +954,10 @@ bool exact_dw(const FlShape& s, const FlPlan& p) { return !s.grad || p.dw != kDw
 // nothing fits.
 int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
   int f_dw = 0;
+  int64_t f_vt = 0;
   bool f_wt = false, f_dt = false, f_bad = false;
-  const bool forced = s.grad && forced_form(&f_dw, &f_wt, &f_dt, &f_bad);
-  HK_REQUIRE(!f_bad, "HILDA_FL_FORM: expected <defer|acc|out>,<wt|wmn>,<dt|dmn>");
+  const bool forced = forced_form(&f_dw, &f_wt, &f_dt, &f_vt, &f_bad) && (s.grad || f_vt > 0);
+  HK_REQUIRE(!f_bad, "HILDA_FL_FORM: expected <defer|acc|out>,<wt|wmn>,<dt|dmn> or vtile,<acc|out>,<columns>");
   const int64_t cmax_rows = std::min<int64_t>(8192, s.chunk_cap > 0 ? s.chunk_cap : 8192);
   const int64_t cmax = std::max<int64_t>(8, std::min<int64_t>(cmax_rows & ~(int64_t)7, pad8(std::max<int64_t>(s.BT, 1))));
   const int smax_full = s.grad ? (int)std::max<int64_t>(1, std::min<int64_t>(8, pad64(s.V) / dx_bk(s.es) / 16)) : 1;
@@ -738,7 +985,7 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
   for (int64_t C : cs) {
     const int64_t nch = s.BT > 0 ? cdiv(s.BT, C) : 0;
     fl_forms(s, nch, [&](bool wt, bool dt, int dw) {
-      if (forced && (dw != f_dw || wt != f_wt || dt != f_dt)) return;
+      if (forced && (f_vt > 0 || dw != f_dw || wt != f_wt || dt != f_dt)) return;
       for (int sm = smax_full; sm >= 1; sm = sm > 1 ? sm / 2 : 0) {
         FlPlan p = fl_layout(s, C, wt, dt, dw, sm);
         if (p.total > cap) continue;
@@ -753,6 +1000,22 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
         break;  // fewer splits only if more do not fit
       }
     });
+  }
+  if (s.vt_ok && s.BT > 0 && (forced ? f_vt > 0 : s.chunk_cap <= 0)) {
+    const int64_t vmax = std::min<int64_t>(8192, (s.V + 255) / 256 * 256);
+    for (int64_t Vt = vmax; Vt >= 256; Vt -= 256)
+      for (int dw : {kDwAcc, kDwOut}) {
+        if (forced && (Vt != f_vt || dw != f_dw)) continue;
+        FlPlan p = vt_layout(s, Vt, dw);
+        if (p.total > cap) continue;
+        p.cost = vt_cost(s, p);
+        const bool ex = exact_dw(s, p), bex = found && exact_dw(s, best);
+        if (!found || (ex && !bex) ||
+            (ex == bex && (p.cost < best.cost || (p.cost == best.cost && p.total < best.total)))) {
+          best = p;
+          found = true;
+        }
+      }
   }
   if (!found && forced) {
     set_error("HILDA_FL_FORM: the forced form does not apply to this call (dtype, chunk count or budget)");
@@ -903,6 +1166,105 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
   return rc;
 }
 
+
+// The vocabulary-tiled plan for CrossEntropy (p.vtile). Pass 1, per tile of
+// Vt vocabulary columns: the logits of every row for those columns (the same
+// GEMM as the row-chunked plans, so the same logits bit for bit), folded into
+// each row's running log-sum-exp. Then the losses. Pass 2, per tile: the
+// logits again, the gradient tile D in place, dW of the tile's vocabulary rows
+// as one GEMM over all BT rows (written once, summed in fp32), and dX += D W_t,
+// summed across the tiles in an fp32 buffer or in the output. No rows are
+// compacted: ignored rows have zero gradient rows. n_valid is counted already.
+template <typename T>
+int vtiled_ce(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, char* ws, const FlPlan& p, bool grad, T* dX,
+              T* dWo, const int64_t* targets, int64_t ignore_index, const int* n_valid, bool mean,
+              const float* row_scale, float* loss_rows, hipStream_t st) {
+  const int64_t Hp = p.Hp, Vt = p.Vt;
+  T* Lt = (T*)(ws + p.lg);
+  VtRow* state = (VtRow*)(ws + p.vst);
+  float* acc = (grad && p.dw == kDwAcc && p.ntiles > 1) ? (float*)(ws + p.acc) : nullptr;
+  int rc = HK_OK;
+  const T* Xk = X;
+  int64_t ldx = H;
+  if (p.gather) {  // hidden rows at a 16-byte multiple, zero filled past H
+    rc = gather_rows<T>((T*)(ws + p.xg), Hp, Hp, X, H, H, nullptr, nullptr, BT, 0, BT, st);
+    if (rc) return rc;
+    Xk = (const T*)(ws + p.xg);
+    ldx = Hp;
+  }
+  const T* Wk = W;
+  int64_t ldw = H;
+  if (p.wpad) {
+    rc = gather_rows<T>((T*)(ws + p.wp), Hp, Hp, W, H, H, nullptr, nullptr, V, 0, V, st);
+    if (rc) return rc;
+    Wk = (const T*)(ws + p.wp);
+    ldw = Hp;
+  }
+  const int dev = current_device();
+  const int cu = dev >= 0 ? cu_count(dev) : 256;
+  const dim3 rgrid((unsigned)std::min<int64_t>(BT, (int64_t)(cu > 0 ? cu : 256) * 8));
+  auto logits = [&](int64_t v0, int64_t w) {
+    return launch_gemm<T>(Xk, Wk + v0 * ldw, (int)BT, (int)w, (int)Hp, ldx, ldw,
+                          EpiLogits<T>{Lt, Vt, -__builtin_huge_valf()}, st);
+  };
+  for (int64_t ti = 0; ti < p.ntiles; ++ti) {
+    const int64_t v0 = ti * Vt, w = std::min<int64_t>(Vt, V - v0);
+    rc = logits(v0, w);
+    if (rc) return rc;
+    hipLaunchKernelGGL((vt_lse_kernel<T>), rgrid, dim3(kVtLanes), 0, st, Lt, Vt, w, v0, targets, ignore_index, state,
+                       BT, ti == 0 ? 1 : 0);
+    rc = check_launch("vt_lse_kernel");
+    if (rc) return rc;
+  }
+  const bool scale = grad && mean;
+  hipLaunchKernelGGL(vt_finalize_kernel, dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 4096)), dim3(256), 0, st,
+                     state, loss_rows, targets, ignore_index, n_valid, scale ? 1 : 0, BT);
+  rc = check_launch("vt_finalize_kernel");
+  if (rc || !grad) return rc;
+  const bool dvec = H % 4 == 0 && aligned_to(dX, 16);
+  const bool wvec = H % 4 == 0 && aligned_to(dWo, 16);
+  for (int64_t ti = 0; ti < p.ntiles; ++ti) {
+    const int64_t v0 = ti * Vt, w = std::min<int64_t>(Vt, V - v0), w8 = pad8(w);
+    rc = logits(v0, w);
+    if (rc) return rc;
+    hipLaunchKernelGGL((vt_grad_kernel<T>), rgrid, dim3(kVtLanes), 0, st, Lt, Vt, w, w8, v0, targets, ignore_index,
+                       state, n_valid, scale ? 1 : 0, row_scale, BT);
+    rc = check_launch("vt_grad_kernel");
+    if (rc) return rc;
+    // dW of the tile's rows: D [BT, w8] (k = the row, m = the tile column) and X [BT, Hp] (k = the row,
+    // n = the hidden column), both read MN-contiguous; K = BT
+    rc = launch_gemm_mn<T, true, true>(Lt, Xk, (int)w8, (int)Hp, (int)BT, Vt, ldx,
+                                       EpiDw<T, 0>{dWo + v0 * H, H, nullptr, Hp, (int)w, (int)H, wvec}, st);
+    if (rc) return rc;
+    if (p.ntiles > 1 && !acc) {
+      // summed in the 16-bit output: the softmax terms only (see vt_drop_targets_kernel)
+      hipLaunchKernelGGL((vt_drop_targets_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 4096)),
+                         dim3(256), 0, st, Lt, Vt, w, v0, targets, ignore_index, BT);
+      rc = check_launch("vt_drop_targets_kernel");
+      if (rc) return rc;
+    }
+    // dX (+)= D W_t: D K-contiguous (K = w8, zero past w), W_t's rows read MN-contiguous (k past w zero)
+    auto dx_gemm = [&](auto epi) {
+      return launch_gemm_mn<T, false, true>(Lt, Wk + v0 * ldw, (int)BT, (int)Hp, (int)w8, Vt, ldw, epi, st, nullptr,
+                                            0, false, 1, (int)w);
+    };
+    const int bl = (int)BT, hl = (int)H;
+    if (p.ntiles == 1) rc = dx_gemm(EpiDw<T, 0>{dX, H, nullptr, Hp, bl, hl, dvec});
+    else if (!acc) rc = ti == 0 ? dx_gemm(EpiDw<T, 0>{dX, H, nullptr, Hp, bl, hl, dvec})
+                                : dx_gemm(EpiDw<T, 1>{dX, H, nullptr, Hp, bl, hl, dvec});
+    else if (ti == 0) rc = dx_gemm(EpiDw<T, 2>{dX, H, acc, Hp, bl, hl, dvec});
+    else if (ti + 1 < p.ntiles) rc = dx_gemm(EpiDw<T, 3>{dX, H, acc, Hp, bl, hl, dvec});
+    else rc = dx_gemm(EpiDw<T, 4>{dX, H, acc, Hp, bl, hl, dvec});
+    if (rc) return rc;
+  }
+  if (p.ntiles > 1 && !acc) {
+    hipLaunchKernelGGL((vt_target_dx_kernel<T>), rgrid, dim3(256), 0, st, dX, H, Wk, ldw, targets, ignore_index, V,
+                       state, n_valid, scale ? 1 : 0, row_scale, BT);
+    rc = check_launch("vt_target_dx_kernel");
+  }
+  return rc;
+}
+
 // Shape checks shared by the fused-linear entry points.
 int fl_check_dims(int64_t BT, int64_t H, int64_t V) {
   HK_REQUIRE(BT >= 0 && H > 0 && V > 0, "invalid shape BT=%lld H=%lld V=%lld", (long long)BT, (long long)H,
@@ -925,9 +1287,66 @@ FlShape flce_shape(int64_t BT, int64_t H, int64_t V, int dtype, bool grad, int64
   s.w_ok = H % 8 == 0 && (!weight || aligned_to(weight, 16));
   s.ce = true;
   s.chunk_cap = chunk;
+  s.vt_ok = s.es == 2;  // (the tiled dW GEMM reads both operands MN-contiguous: 16-bit only)
   return s;
 }
 
+}  // namespace
+}  // namespace hk
+
+namespace hk {
+namespace {
+struct JsdExtra {
+  size_t lc, labc, lt, xtc, wtp, total;
+};
+JsdExtra jsd_extra(int64_t BT, int64_t Ht, int64_t V, int64_t C, int es, bool t_gather, bool t_wpad) {
+  JsdExtra e{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
+  e.lc = take(bt * 4);
+  e.labc = take(bt * 8);
+  e.lt = take((size_t)C * pad64(V) * es);
+  e.xtc = t_gather ? take((size_t)C * pad8(Ht) * es) : 0;
+  e.wtp = t_wpad ? take((size_t)V * pad8(Ht) * es) : 0;
+  e.total = off;
+  return e;
+}
+
+FlShape fljsd_shape(int64_t BT, int64_t H, int64_t Ht, int64_t V, int dtype, bool grad, int64_t chunk, bool labels,
+                    const void* s_in, const void* s_w, const void* t_in, const void* t_w, bool* t_gather,
+                    bool* t_wpad) {
+  FlShape s{};
+  s.BT = BT;
+  s.H = H;
+  s.V = V;
+  s.es = fl_esize(dtype);
+  s.grad = grad;
+  s.compact = labels;
+  s.x_ok = H % 8 == 0 && (!s_in || aligned_to(s_in, 16));
+  s.w_ok = H % 8 == 0 && (!s_w || aligned_to(s_w, 16));
+  *t_gather = labels || Ht % 8 != 0 || (t_in && !aligned_to(t_in, 16));
+  *t_wpad = Ht % 8 != 0 || (t_w && !aligned_to(t_w, 16));
+  const JsdExtra e0 = jsd_extra(BT, Ht, V, 0, s.es, *t_gather, *t_wpad);
+  s.fixed_extra = e0.total + 4 * 256;
+  s.row_extra = (size_t)pad64(V) * s.es + (*t_gather ? (size_t)pad8(Ht) * s.es : 0);
+  s.chunk_cap = chunk;
+  return s;
+}
+}  // namespace
+namespace {
+FlShape flgrpo_shape(int64_t B, int64_t L, int64_t H, int64_t V, int dtype, bool grad, int64_t chunk,
+                     const void* hidden, const void* weight) {
+  FlShape s = flce_shape(B * (L + 1), H, V, dtype, grad, chunk, hidden, weight);
+  s.ce = false;
+  s.vt_ok = false;
+  s.fixed_extra = grpo_scratch_bytes(B, L);
+  return s;
+}
 }  // namespace
 }  // namespace hk
 
@@ -957,7 +1376,7 @@ int hk_fused_linear_cross_entropy_plan(int64_t BT, int64_t H, int64_t V, int64_t
     return rc;
   info[0] = p.C;
   info[1] = p.nch;
-  info[2] = p.dw;
+  info[2] = p.vtile ? 3 + (p.dw == kDwAcc ? 0 : 1) : p.dw;
   info[3] = p.wt ? 1 : 0;
   info[4] = p.dt ? 1 : 0;
   info[5] = p.ksplit;
@@ -1003,6 +1422,16 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
   auto run = [&](auto tag) -> int {
     using T = typename decltype(tag)::type;
     int rc = HK_OK;
+    if (lay.vtile) {
+      rc = count_valid_launch(n_valid, targets, BT, ignore_index, has_ignore, st);
+      if (rc) return rc;
+      rc = vtiled_ce<T>((const T*)hidden, (const T*)weight, BT, H, V, ws, lay, grad, (T*)dhidden, (T*)dweight,
+                        targets, ignore_index, n_valid, reduction == HK_REDUCTION_MEAN, row_scale, loss_rows, st);
+      if (rc) return rc;
+      if (!loss_out) return HK_OK;
+      const bool divide = !grad && reduction == HK_REDUCTION_MEAN;
+      return sum_rows_launch(loss_out, loss_rows, BT, divide ? n_valid : nullptr, divide, st);
+    }
     if (BT > 0) {
       rc = count_valid_launch(n_valid, targets, BT, ignore_index, has_ignore, st);
       if (rc) return rc;
@@ -1045,49 +1474,6 @@ int hk_fused_linear_cross_entropy(float* loss_out, float* loss_rows, void* dhidd
 // logits chunk and gathered teacher rows (per chunk row) and a padded copy of
 // the teacher weight when its rows are not 16-byte multiples.
 // ---------------------------------------------------------------------------
-namespace {
-struct JsdExtra {
-  size_t lc, labc, lt, xtc, wtp, total;
-};
-JsdExtra jsd_extra(int64_t BT, int64_t Ht, int64_t V, int64_t C, int es, bool t_gather, bool t_wpad) {
-  JsdExtra e{};
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off += align256(bytes);
-    return o;
-  };
-  const size_t bt = (size_t)std::max<int64_t>(BT, 1);
-  e.lc = take(bt * 4);
-  e.labc = take(bt * 8);
-  e.lt = take((size_t)C * pad64(V) * es);
-  e.xtc = t_gather ? take((size_t)C * pad8(Ht) * es) : 0;
-  e.wtp = t_wpad ? take((size_t)V * pad8(Ht) * es) : 0;
-  e.total = off;
-  return e;
-}
-
-FlShape fljsd_shape(int64_t BT, int64_t H, int64_t Ht, int64_t V, int dtype, bool grad, int64_t chunk, bool labels,
-                    const void* s_in, const void* s_w, const void* t_in, const void* t_w, bool* t_gather,
-                    bool* t_wpad) {
-  FlShape s{};
-  s.BT = BT;
-  s.H = H;
-  s.V = V;
-  s.es = fl_esize(dtype);
-  s.grad = grad;
-  s.compact = labels;
-  s.x_ok = H % 8 == 0 && (!s_in || aligned_to(s_in, 16));
-  s.w_ok = H % 8 == 0 && (!s_w || aligned_to(s_w, 16));
-  *t_gather = labels || Ht % 8 != 0 || (t_in && !aligned_to(t_in, 16));
-  *t_wpad = Ht % 8 != 0 || (t_w && !aligned_to(t_w, 16));
-  const JsdExtra e0 = jsd_extra(BT, Ht, V, 0, s.es, *t_gather, *t_wpad);
-  s.fixed_extra = e0.total + 4 * 256;
-  s.row_extra = (size_t)pad64(V) * s.es + (*t_gather ? (size_t)pad8(Ht) * s.es : 0);
-  s.chunk_cap = chunk;
-  return s;
-}
-}  // namespace
 
 size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk,
                                           int64_t workspace_budget, int dtype, int with_grad, int with_labels,
@@ -1208,15 +1594,6 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
 // ---------------------------------------------------------------------------
 // FusedLinear-GRPO
 // ---------------------------------------------------------------------------
-namespace {
-FlShape flgrpo_shape(int64_t B, int64_t L, int64_t H, int64_t V, int dtype, bool grad, int64_t chunk,
-                     const void* hidden, const void* weight) {
-  FlShape s = flce_shape(B * (L + 1), H, V, dtype, grad, chunk, hidden, weight);
-  s.ce = false;
-  s.fixed_extra = grpo_scratch_bytes(B, L);
-  return s;
-}
-}  // namespace
 
 size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk,
                                            int64_t workspace_budget, int dtype, int with_grad, const void* hidden,

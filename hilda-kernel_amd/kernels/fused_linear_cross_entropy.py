@@ -153,12 +153,14 @@ def hilda_fused_linear_cross_entropy(hidden_states, weight, targets, ignore_inde
 def fused_linear_cross_entropy_plan(BT, H, V, dtype=torch.bfloat16, compute_grad=True, chunk=DEFAULT_CHUNK,
                                     workspace_budget=None):
     """The memory plan a call of that shape takes: a dict of rows per chunk, chunks, the dW mode ('deferred',
-    'fp32 accumulator' or 'in output'), whether W^T and D^T are materialised, the dX split cap, workspace bytes
-    and the cost model's time estimate (ms)."""
+    'fp32 accumulator' or 'in output'; for the vocabulary-tiled plan 'vocab tiles, ...' with chunk the
+    vocabulary columns a tile and chunks the tiles), whether W^T and D^T are materialised, the dX split cap,
+    workspace bytes and the cost model's time estimate (ms)."""
     info = (ctypes.c_int64 * 8)()
     _lib.call("hk_fused_linear_cross_entropy_plan", int(BT), int(H), int(V), int(chunk),
               _lib.fl_budget(workspace_budget), _lib._DTYPE_CODE[dtype], int(compute_grad), None, None, info)
-    modes = {0: "deferred", 1: "fp32 accumulator", 2: "in output"}
+    modes = {0: "deferred", 1: "fp32 accumulator", 2: "in output", 3: "vocab tiles, dX fp32",
+             4: "vocab tiles, dX in output"}
     return dict(chunk=info[0], chunks=info[1], dw=modes[info[2]], w_transposed=bool(info[3]),
                 d_transposed=bool(info[4]), dx_splits=info[5], workspace_bytes=info[6], model_ms=info[7] / 1e6)
 

@@ -421,7 +421,70 @@ def bench_c4(K, dev, reps, flush, cpu=False):
     return e
 
 
+def peak_mib(fn, dev):
+    """Peak device memory of one call of fn above what was allocated before it, in MiB, measured as the
+    reference's benchmark measures it (bench_fused_linear_ce.py:171-178): after a warm-up call, reset the peak
+    statistics, run, read torch.cuda.max_memory_allocated."""
+    fn()
+    torch.cuda.synchronize(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    fn()
+    torch.cuda.synchronize(dev)
+    return round((torch.cuda.max_memory_allocated(dev) - base) / 2**20, 1)
+
+
+def flce_memory(K, dev, N, H, V, dtype, budgets=(None,), reps=3, flush=None, seed=0):
+    """fwd+bwd peak memory and time of FusedLinearCE against torch's unfused hidden @ W.T + cross_entropy on
+    the same GPU. Peak: leaves allocated inside the measured function, as the reference's bench_memory does
+    (bench_fused_linear_ce.py:181-214). Time: resident leaves, flushed cache, median of reps."""
+    from kernels import fused_linear_cross_entropy as fl
+    g = torch.Generator(device=dev).manual_seed(seed)
+    tg = torch.randint(0, V, (N,), device=dev, generator=g)
+
+    def fresh(f):
+        def fn():
+            h = torch.randn(N, H, device=dev, dtype=dtype, requires_grad=True)
+            w = torch.randn(V, H, device=dev, dtype=dtype, requires_grad=True)
+            f(h, w).backward()
+        return fn
+
+    hs = torch.randn(N, H, device=dev, dtype=dtype, generator=g).requires_grad_(True)
+    ws = (0.02 * torch.randn(V, H, device=dev, dtype=dtype, generator=g)).requires_grad_(True)
+
+    def resident(f):
+        def fn():
+            return torch.autograd.grad([f(hs, ws)], [hs, ws])
+        return fn
+
+    def unfused(h, w):
+        return torch.nn.functional.cross_entropy(h @ w.T, tg)
+
+    out = {"config": f"N={N} H={H} V={V} {str(dtype).replace('torch.', '')}"}
+    pu = peak_mib(fresh(unfused), dev)
+    tu = statistics.median(time_events(resident(unfused), reps, flush, warmup=1))
+    out["unfused_torch"] = {"peak_mib": pu, "ms": round(tu, 3)}
+    torch.cuda.empty_cache()
+    for b in budgets:
+        f = (lambda h, w, b=b: K.hilda_fused_linear_cross_entropy(h, w, tg, workspace_budget=b))
+        p = peak_mib(fresh(f), dev)
+        t = statistics.median(time_events(resident(f), reps, flush, warmup=1))
+        plan = fl.fused_linear_cross_entropy_plan(N, H, V, dtype, workspace_budget=b)
+        out["default" if b is None else str(b)] = {
+            "peak_mib": p, "saving": round(1 - p / pu, 4), "ms": round(t, 3), "speed_vs_unfused": round(tu / t, 3),
+            "plan": {k: plan[k] for k in ("chunk", "chunks", "dw", "w_transposed", "d_transposed")},
+            "workspace_mib": round(plan["workspace_bytes"] / 2**20, 1)}
+        torch.cuda.empty_cache()
+    del hs, ws
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_c5(K, dev, reps, flush, cpu=False):
+    """C5 in two memory plans: the unlimited workspace budget ('fastest': two 8192-row chunks, every chunk's
+    D^T kept and one dW GEMM) is the entry's headline time; the default plan (the reference's memory class)
+    beside it, each with its fwd+bwd peak memory against torch's unfused path."""
+    from kernels import fused_linear_cross_entropy as fl
     c = workloads.c5_fused_linear_ce(device=dev)
     h = c["hidden"].requires_grad_(True)
     w = c["weight"].requires_grad_(True)
@@ -429,24 +492,49 @@ def bench_c5(K, dev, reps, flush, cpu=False):
     BT, H = h.shape
     V = w.shape[0]
     n_valid = int((t != -100).sum())
-
-    def fn():
-        loss = K.hilda_fused_linear_cross_entropy(h, w, t)
-        return torch.autograd.grad([loss], [h, w])
-
     work = 6 * n_valid * H * V  # conservative: ignored rows need no FLOPs
-    e = op_entry("C5", time_events(fn, reps, flush, warmup=1), work, "TFLOP/s", BF16_PEAK_TFLOPS)
+
+    def run(budget):
+        def fn():
+            loss = K.hilda_fused_linear_cross_entropy(h, w, t, workspace_budget=budget)
+            return torch.autograd.grad([loss], [h, w])
+        return fn
+
+    e = op_entry("C5 (workspace_budget='fastest')", time_events(run("fastest"), reps, flush, warmup=1), work,
+                 "TFLOP/s", BF16_PEAK_TFLOPS)
     dense = 6 * BT * H * V
     e["dense_equivalent_tflops"] = round(dense / (e["ms"] * 1e-3) / 1e12, 2)
     e["n_valid"] = n_valid
-    log(f"  fused_linear_cross_entropy (C5): {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  ({e['frac']:.1%}); "
-        f"dense-equivalent {e['dense_equivalent_tflops']} TFLOP/s")
+    e["plan"] = fl.fused_linear_cross_entropy_plan(BT, H, V, torch.bfloat16, workspace_budget="fastest")
+    d_ms = statistics.median(time_events(run(None), max(3, reps // 2), flush, warmup=1))
+    e["default_plan"] = {"ms": round(d_ms, 3), "value": round(work / (d_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                         "plan": fl.fused_linear_cross_entropy_plan(BT, H, V, torch.bfloat16)}
+    log(f"  fused_linear_cross_entropy (C5): fastest plan {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  "
+        f"({e['frac']:.1%}); default plan {d_ms:.3f} ms")
+    del h, w, c
+    torch.cuda.empty_cache()
+    # peak memory at C5 (fresh leaves of the same shapes) and at the reference's memory configs
+    # (bench_fused_linear_ce.py:270-274, fp16), default plan
+    e["memory"] = flce_memory(K, dev, BT, H, V, torch.bfloat16, budgets=(None, "fastest"), reps=3, flush=flush)
+    m = e["memory"]
+    log(f"    C5 peak: unfused {m['unfused_torch']['peak_mib']} MiB ({m['unfused_torch']['ms']} ms), default "
+        f"{m['default']['peak_mib']} MiB ({m['default']['saving']:.1%} less), fastest {m['fastest']['peak_mib']} "
+        f"MiB ({m['fastest']['saving']:.1%} less)")
+    e["reference_memory_configs"] = []
+    for N_, H_, V_ in ((8192, 4096, 32000), (8192, 4096, 128256), (4096, 4096, 128256)):
+        r = flce_memory(K, dev, N_, H_, V_, torch.float16, budgets=(None,), reps=3, flush=flush)
+        e["reference_memory_configs"].append(r)
+        log(f"    {r['config']}: unfused {r['unfused_torch']['peak_mib']} MiB {r['unfused_torch']['ms']} ms; "
+            f"default {r['default']['peak_mib']} MiB ({r['default']['saving']:.1%} less) {r['default']['ms']} ms")
     if cpu:
         import oracle
         rows = 128
-        hc = h[:rows].detach().cpu().requires_grad_(True)
-        wc = w.detach().cpu().requires_grad_(True)
-        tc = t[:rows].cpu()
+        c = workloads.c5_fused_linear_ce(device=dev)
+        hc = c["hidden"][:rows].detach().cpu().requires_grad_(True)
+        wc = c["weight"].detach().cpu().requires_grad_(True)
+        tc = c["targets"][:rows].cpu()
+        del c
+        torch.cuda.empty_cache()
 
         def step():
             loss = oracle.linear_ce_ref(hc, wc, tc)

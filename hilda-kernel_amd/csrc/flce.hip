@@ -164,6 +164,7 @@ struct EpiDw {
   int64_t lda;  // a multiple of 4
   int rows_lim, cols_lim;
   bool vec;     // out rows aligned for 4-element stores
+  const int* inv_n = nullptr;  // nullable: the values are multiplied by 1 / max(*inv_n, 1) first
   __device__ __forceinline__ Prior load(int row, int col, int n) const {
     if (row >= rows_lim || col >= cols_lim) return Prior{0.f, 0.f, 0.f, 0.f};
     n = min(n, cols_lim - col);
@@ -177,9 +178,10 @@ struct EpiDw {
   __device__ __forceinline__ void store(int row, int col, const float* v, int n, const Prior& x) const {
     if (row >= rows_lim || col >= cols_lim) return;
     n = min(n, cols_lim - col);
+    const float f = inv_n ? 1.f / (float)max(*inv_n, 1) : 1.f;
     float r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = kReads ? x[e] + v[e] : v[e];
+    for (int e = 0; e < 4; ++e) r[e] = kReads ? x[e] + v[e] * f : v[e] * f;
     if constexpr (MODE == 2 || MODE == 3) {
       float* p = acc + (int64_t)row * lda + col;
       if (n == 4) {
@@ -417,62 +419,56 @@ struct VtRow {
   float m, sx, zt, pad;
 };
 
-constexpr int kVtLanes = 256;
-constexpr int kVtVec = 4;  // 16-byte vectors a lane holds: rows of up to 256 x 4 x 16 bytes
+constexpr int kVtLanes = 256;  // four waves a block, one row a wave at a time
 
-template <typename T>
-__device__ __forceinline__ void vt_load(const T* row, int64_t w, float (&x)[kVtVec][16 / sizeof(T)]) {
-  constexpr int E = 16 / (int)sizeof(T);
-#pragma unroll
-  for (int k = 0; k < kVtVec; ++k) {
-    const int64_t j0 = ((int64_t)k * kVtLanes + threadIdx.x) * E;
-    if (j0 + E <= w) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(row + j0);
-      const T* e = reinterpret_cast<const T*>(&v);
-#pragma unroll
-      for (int i = 0; i < E; ++i) x[k][i] = to_f32<T>(e[i]) * kLog2e;
-    } else {
-#pragma unroll
-      for (int i = 0; i < E; ++i) x[k][i] = j0 + i < w ? to_f32<T>(row[j0 + i]) * kLog2e : -__builtin_huge_valf();
-    }
-  }
-}
-
-// One block a row (grid-stride): the tile's max and non-target sum, merged into the row state.
+// One wave a row (grid-stride over the rows): per lane an online maximum and
+// sum of 2^(z - m) over the row's 16-byte vectors (the target column left
+// out), then the wave's (max, sum) by DPP reductions; merged into the row state.
 template <typename T>
 __global__ __launch_bounds__(kVtLanes) void vt_lse_kernel(const T* __restrict__ L, int64_t ld, int64_t w, int64_t v0,
                                                         const int64_t* __restrict__ targets, int64_t ignore_index,
                                                         VtRow* __restrict__ state, int64_t rows, int first) {
   constexpr int E = 16 / (int)sizeof(T);
-  __shared__ float red[kVtLanes / kWave];
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nw = (int64_t)gridDim.x * (kVtLanes / kWave);
+  const float ninf = -__builtin_huge_valf();
+  for (int64_t r = (int64_t)blockIdx.x * (kVtLanes / kWave) + threadIdx.x / kWave; r < rows; r += nw) {
     const int64_t t = targets[r];
-    if (t == ignore_index) continue;  // uniform in the block
+    if (t == ignore_index) continue;  // uniform in the wave
     const int64_t tl = t - v0;         // the target's column in this tile, if it is here
-    float x[kVtVec][E];
-    vt_load<T>(L + r * ld, w, x);
-    float m = -__builtin_huge_valf();
+    const T* row = L + r * ld;
+    float m = ninf, sx = 0.f, zt = ninf;
+    for (int64_t j0 = (int64_t)lane * E; j0 < w; j0 += kWave * E) {
+      float x[E];
+      if (j0 + E <= w) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + j0);
+        const T* e = reinterpret_cast<const T*>(&v);
 #pragma unroll
-    for (int k = 0; k < kVtVec; ++k)
+        for (int i = 0; i < E; ++i) x[i] = to_f32<T>(e[i]) * kLog2e;
+      } else {
 #pragma unroll
-      for (int i = 0; i < E; ++i) m = fmaxf(m, x[k][i]);
-    m = block_max<kVtLanes / kWave>(m, red);
-    float sx = 0.f, zt = -__builtin_huge_valf();
+        for (int i = 0; i < E; ++i) x[i] = j0 + i < w ? to_f32<T>(row[j0 + i]) * kLog2e : ninf;
+      }
+      float cm = m;
 #pragma unroll
-    for (int k = 0; k < kVtVec; ++k)
+      for (int i = 0; i < E; ++i) cm = fmaxf(cm, x[i]);
+      float cs = 0.f;
 #pragma unroll
       for (int i = 0; i < E; ++i) {
-        const int64_t j = ((int64_t)k * kVtLanes + threadIdx.x) * E + i;
-        if (j == tl) zt = x[k][i];
-        else sx += exp2_fast(x[k][i] - m);  // (-inf columns add 0)
+        if (j0 + i == tl) zt = x[i];
+        else cs += exp2_fast(x[i] - cm);
       }
-    sx = block_sum<kVtLanes / kWave>(sx, red);
-    zt = block_max<kVtLanes / kWave>(zt, red);
-    if (threadIdx.x == 0) {
-      VtRow q = first ? VtRow{-__builtin_huge_valf(), 0.f, -__builtin_huge_valf(), 0.f} : state[r];
-      const float M = fmaxf(q.m, m);
-      q.sx = (q.sx > 0.f ? q.sx * exp2_fast(q.m - M) : 0.f) + (sx > 0.f ? sx * exp2_fast(m - M) : 0.f);
-      q.m = M;
+      sx = (sx > 0.f ? sx * exp2_fast(m - cm) : 0.f) + cs;
+      m = cm;
+    }
+    const float M = wave_max(m);
+    sx = wave_sum(sx > 0.f ? sx * exp2_fast(m - M) : 0.f);
+    zt = wave_max(zt);
+    if (lane == 0) {
+      VtRow q = first ? VtRow{ninf, 0.f, ninf, 0.f} : state[r];
+      const float Mn = fmaxf(q.m, M);
+      q.sx = (q.sx > 0.f ? q.sx * exp2_fast(q.m - Mn) : 0.f) + (sx > 0.f ? sx * exp2_fast(M - Mn) : 0.f);
+      q.m = Mn;
       if (tl >= 0 && tl < w) q.zt = zt;
       state[r] = q;
     }
@@ -499,9 +495,9 @@ __global__ __launch_bounds__(256) void vt_finalize_kernel(VtRow* __restrict__ st
   }
 }
 
-// The gradient tile in place: D = (p - onehot) * g with g = s * row_scale[r]
-// (s = 1 / max(n_valid, 1) when scale), the target entry -(1 - p_t) * g;
-// columns [w, wz) and ignored rows are zero.
+// The gradient tile in place, one wave a row: D = (p - onehot) * g with
+// g = s * row_scale[r] (s = 1 / max(n_valid, 1) when scale), the target entry
+// -(1 - p_t) * g; columns [w, wz) and ignored rows are zero.
 template <typename T>
 __global__ __launch_bounds__(kVtLanes) void vt_grad_kernel(T* __restrict__ L, int64_t ld, int64_t w, int64_t wz,
                                                          int64_t v0, const int64_t* __restrict__ targets,
@@ -510,26 +506,33 @@ __global__ __launch_bounds__(kVtLanes) void vt_grad_kernel(T* __restrict__ L, in
                                                          const float* __restrict__ row_scale, int64_t rows) {
   constexpr int E = 16 / (int)sizeof(T);
   const float s = scale ? 1.f / (float)max(*n_valid, 1) : 1.f;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nw = (int64_t)gridDim.x * (kVtLanes / kWave);
+  for (int64_t r = (int64_t)blockIdx.x * (kVtLanes / kWave) + threadIdx.x / kWave; r < rows; r += nw) {
     T* row = L + r * ld;
     const int64_t t = targets[r];
     const bool dead = t == ignore_index;
     const VtRow q = dead ? VtRow{0.f, 0.f, 0.f, 0.f} : state[r];
     const float g = dead ? 0.f : s * (row_scale ? row_scale[r] : 1.f);
     const int64_t tl = t - v0;
-    float x[kVtVec][E];
-    if (!dead) vt_load<T>(row, w, x);
-#pragma unroll
-    for (int k = 0; k < kVtVec; ++k) {
-      const int64_t j0 = ((int64_t)k * kVtLanes + threadIdx.x) * E;
-      if (j0 >= wz) continue;
+    for (int64_t j0 = (int64_t)lane * E; j0 < wz; j0 += kWave * E) {
       T out[E];
+      if (j0 + E <= w && !dead) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + j0);
+        const T* e = reinterpret_cast<const T*>(&v);
 #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        const int64_t j = j0 + i;
-        float d = 0.f;
-        if (!dead && j < w) d = j == tl ? -q.sx * g : exp2_fast(x[k][i] - q.m) * g;
-        out[i] = from_f32<T>(d);
+        for (int i = 0; i < E; ++i) {
+          const float d = j0 + i == tl ? -q.sx * g : exp2_fast(to_f32<T>(e[i]) * kLog2e - q.m) * g;
+          out[i] = from_f32<T>(d);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const int64_t j = j0 + i;
+          float d = 0.f;
+          if (!dead && j < w) d = j == tl ? -q.sx * g : exp2_fast(to_f32<T>(row[j]) * kLog2e - q.m) * g;
+          out[i] = from_f32<T>(d);
+        }
       }
       if (j0 + E <= wz) {
         *reinterpret_cast<u32x4*>(row + j0) = *reinterpret_cast<const u32x4*>(out);
@@ -539,7 +542,6 @@ __global__ __launch_bounds__(kVtLanes) void vt_grad_kernel(T* __restrict__ L, in
     }
   }
 }
-
 
 // The tile's target entries set to zero (after the tile's dW GEMM has read them):
 // dX is then summed across the tiles from softmax terms alone, of like size, and
@@ -554,7 +556,9 @@ __global__ __launch_bounds__(256) void vt_drop_targets_kernel(T* __restrict__ L,
   }
 }
 
-// dX[r] += -(1 - p_target) * g * W[target] for every live row, in fp32, rounded once (one block a row).
+// dX[r] = s * (dX[r] - (1 - p_target) * row_scale[r] * W[target]) for every live row, in fp32, rounded once
+// (one block a row): dX was summed in the output without s (s = 1 / max(n_valid, 1) when scale), which keeps
+// fp16 sums out of the subnormal range (unscaled, they stay below twice the largest |W|).
 template <typename T>
 __global__ __launch_bounds__(256) void vt_target_dx_kernel(T* __restrict__ dX, int64_t H, const T* __restrict__ W,
                                                            int64_t ldw, const int64_t* __restrict__ targets,
@@ -566,10 +570,11 @@ __global__ __launch_bounds__(256) void vt_target_dx_kernel(T* __restrict__ dX, i
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const int64_t t = targets[r];
     if (t == ignore_index || t < 0 || t >= V) continue;
-    const float c = -state[r].sx * s * (row_scale ? row_scale[r] : 1.f);
+    const float c = -state[r].sx * (row_scale ? row_scale[r] : 1.f);
     const T* wr = W + t * ldw;
     T* o = dX + r * H;
-    for (int64_t j = threadIdx.x; j < H; j += 256) o[j] = from_f32<T>(to_f32<T>(o[j]) + c * to_f32<T>(wr[j]));
+    for (int64_t j = threadIdx.x; j < H; j += 256)
+      o[j] = from_f32<T>(s * (to_f32<T>(o[j]) + c * to_f32<T>(wr[j])));
   }
 }
 
@@ -697,6 +702,7 @@ struct FlShape {
   size_t row_extra;    // and per chunk row
   int64_t chunk_cap;   // rows per chunk at most (<= 0: no cap below 8192)
   bool vt_ok = false;  // the vocabulary-tiled plan applies (CrossEntropy on 16-bit inputs)
+  bool f16 = false;    // fp16 inputs (see fl_plan)
 };
 
 struct FlPlan {
@@ -824,10 +830,14 @@ FlPlan vt_layout(const FlShape& s, int64_t Vt, int dw) {
 // MN-contiguous, the dX GEMM with W MN-contiguous, idle CUs when a GEMM has
 // fewer than 256 tiles, the row passes' HBM bytes and dX's read-modify-writes.
 double vt_cost(const FlShape& s, const FlPlan& p) {
-  const double Rg = 1.25e15, Rm = 5.0e12, pen = 1.15, launch = 5e-6;
+  const double Rg = 1.25e15, Rm = 5.0e12, pen = 1.2, launch = 5e-6;
   const double es = s.es, BT = (double)s.BT, Hp = (double)p.Hp, V = (double)s.V;
   const double F = 2.0 * BT * Hp * V;
-  auto fill = [](int64_t tiles) { return tiles >= 256 ? 1.0 : 256.0 / (double)std::max<int64_t>(tiles, 1); };
+  // a GEMM of `tiles` 256x256 tiles takes whole waves of 256 (one workgroup a CU)
+  auto fill = [](int64_t tiles) {
+    tiles = std::max<int64_t>(tiles, 1);
+    return (double)(cdiv(tiles, 256) * 256) / (double)tiles;
+  };
   const int64_t tb = cdiv(s.BT, 256), tv = cdiv(p.Vt, 256), th = cdiv(p.Hp, 256);
   double t = F / Rg * fill(tb * tv) + BT * V * es / Rm + p.ntiles * 3 * launch;
   if (p.gather) t += 2.0 * es * BT * Hp / Rm;
@@ -848,21 +858,25 @@ double vt_cost(const FlShape& s, const FlPlan& p) {
 // GEMM that leaves CUs idle, and the HBM bytes of the transposes, the dW
 // read-modify-writes, the split partials and the gathers, plus launches.
 double fl_cost(const FlShape& s, const FlPlan& p) {
-  const double Rg = 1.25e15, Rm = 5.0e12, pen = 1.15, launch = 5e-6;
+  const double Rg = 1.25e15, Rm = 5.0e12, pen = 1.2, launch = 5e-6;
   const double es = s.es, BT = (double)s.BT, Hp = (double)p.Hp, V = (double)s.V;
   const double F = 2.0 * BT * Hp * V;
+  // row waste of a chunk's last 256-row tile, and whole waves of 256 workgroups (one a CU)
   const double q = (double)(cdiv(p.C, 256) * 256) / (double)p.C;
+  auto waves = [](int64_t wgs) {
+    wgs = std::max<int64_t>(wgs, 1);
+    return (double)(cdiv(wgs, 256) * 256) / (double)wgs;
+  };
   const double nch = (double)p.nch;
-  double t = F / Rg * q + nch * 6 * launch;
+  double t = F / Rg * q * waves(cdiv(p.C, 256) * cdiv(s.V, 256)) + nch * 6 * launch;
   if (p.gather) t += 2.0 * es * BT * Hp / Rm;
   if (p.wpad) t += 2.0 * es * V * Hp / Rm;
   if (s.grad) {
     const int64_t tiles = cdiv(p.C, 256) * cdiv(p.Hp, 256);
     const int sp = gemm::auto_splits((int)tiles, (int)(p.ldl / dx_bk(s.es)), p.ksplit);
-    const double util = std::min(1.0, (double)(tiles * sp) / 256.0);
-    t += F / Rg * q / util * (p.wt ? 1.0 : pen);
+    t += F / Rg * q * waves(tiles * sp) * (p.wt ? 1.0 : pen);
     if (sp > 1) t += nch * 2.0 * sp * (double)p.C * Hp * 4 / Rm;
-    t += F / Rg * (p.dt ? 1.0 : pen);
+    t += F / Rg * waves(cdiv(s.V, 256) * cdiv(p.Hp, 256)) * (p.dt ? 1.0 : pen);
     double rmw = es * V * Hp;
     if (p.dw == kDwAcc && p.nch > 1) rmw = 8.0 * V * Hp * (nch - 1) + es * V * Hp;
     if (p.dw == kDwOut) rmw = es * V * Hp * (2 * nch - 1);
@@ -940,6 +954,10 @@ bool forced_form(int* dw, bool* wt, bool* dt, int64_t* vt, bool* bad) {
 // unfused path, the low end of the reference's claim (README.md:42).
 constexpr size_t kSmallWorkspace = (size_t)40 << 20;
 
+// A plan that sums dW (and dX) in fp32 is taken over a faster one that sums in
+// the 16-bit output unless it is modelled this much slower.
+constexpr double kExactSlack = 1.5;
+
 // dW summed in fp32 (or computed whole): every form but accumulation in a
 // 16-bit output over several chunks.
 bool exact_dw(const FlShape& s, const FlPlan& p) { return !s.grad || p.dw != kDwOut || p.nch <= 1 || s.es == 4; }
@@ -948,10 +966,10 @@ bool exact_dw(const FlShape& s, const FlPlan& p) { return !s.grad || p.dw != kDw
 // The plan for a byte budget: budget == 0 the default (at most the larger of
 // kSmallWorkspace and what the reference's chunk costs in the leanest form),
 // budget < 0 unlimited, else at most `budget` bytes. Within the budget: the
-// fastest candidate by fl_cost whose dW is summed in fp32; only when none
-// fits, the fastest one that accumulates dW in the 16-bit output (the
-// reference's arithmetic, fused_linear_cross_entropy.py:161). HK_EINVAL when
-// nothing fits.
+// fastest candidate by fl_cost (vt_cost) whose sums are in fp32, unless the
+// fastest of all, which accumulates in the 16-bit output (the reference's
+// arithmetic, fused_linear_cross_entropy.py:161), is modelled more than
+// kExactSlack times faster. HK_EINVAL when nothing fits.
 int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
   int f_dw = 0;
   int64_t f_vt = 0;
@@ -975,8 +993,30 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
   } else {
     cap = budget < 0 ? SIZE_MAX : (size_t)budget;
   }
-  bool found = false;
-  FlPlan best;
+  // the fastest candidate overall, the fastest whose dW (and dX) are summed in fp32, and (fp16 inputs) the
+  // fastest that does not sum dW in the fp16 output over several chunks: gradients scaled by 1/n sit in
+  // fp16's subnormal range there, where each rounding costs percent-level error (the vocabulary-tiled plan
+  // sums dX unscaled, which stays in the normal range)
+  bool found = false, found_ex = false, found_safe = false;
+  FlPlan best, best_ex, best_safe;
+  auto consider = [&](const FlPlan& p) {
+    auto better = [&](const FlPlan& a, const FlPlan& b) {
+      return a.cost < b.cost || (a.cost == b.cost && a.total < b.total);
+    };
+    if (!found || better(p, best)) {
+      best = p;
+      found = true;
+    }
+    if (exact_dw(s, p) && (!found_ex || better(p, best_ex))) {
+      best_ex = p;
+      found_ex = true;
+    }
+    const bool risky = s.f16 && !p.vtile && !exact_dw(s, p);
+    if (!risky && (!found_safe || better(p, best_safe))) {
+      best_safe = p;
+      found_safe = true;
+    }
+  };
   std::vector<int64_t> cs;
   for (int64_t C = cmax; C >= 8; C = (C > 64 ? (C - 1) / 64 * 64 : C / 2 & ~(int64_t)7)) {
     cs.push_back(C);
@@ -990,13 +1030,7 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
         FlPlan p = fl_layout(s, C, wt, dt, dw, sm);
         if (p.total > cap) continue;
         p.cost = fl_cost(s, p);
-        const bool ex = exact_dw(s, p), bex = found && exact_dw(s, best);
-        const bool better = !found || (ex && !bex) ||
-                            (ex == bex && (p.cost < best.cost || (p.cost == best.cost && p.total < best.total)));
-        if (better) {
-          best = p;
-          found = true;
-        }
+        consider(p);
         break;  // fewer splits only if more do not fit
       }
     });
@@ -1009,12 +1043,7 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
         FlPlan p = vt_layout(s, Vt, dw);
         if (p.total > cap) continue;
         p.cost = vt_cost(s, p);
-        const bool ex = exact_dw(s, p), bex = found && exact_dw(s, best);
-        if (!found || (ex && !bex) ||
-            (ex == bex && (p.cost < best.cost || (p.cost == best.cost && p.total < best.total)))) {
-          best = p;
-          found = true;
-        }
+        consider(p);
       }
   }
   if (!found && forced) {
@@ -1026,7 +1055,10 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
     set_error("workspace budget %lld bytes is below the smallest plan (%zu bytes)", (long long)budget, small.total);
     return HK_EINVAL;
   }
-  *out = best;
+  // fp32 sums unless they cost more than half as much time again as the fastest plan (fp16: the fastest
+  // plan without fp16 dW sums over chunks, when one fits)
+  const FlPlan& fast = s.f16 && found_safe ? best_safe : best;
+  *out = found_ex && best_ex.cost <= kExactSlack * fast.cost ? best_ex : fast;
   return HK_OK;
 }
 
@@ -1223,20 +1255,25 @@ int vtiled_ce(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, char* ws
   if (rc || !grad) return rc;
   const bool dvec = H % 4 == 0 && aligned_to(dX, 16);
   const bool wvec = H % 4 == 0 && aligned_to(dWo, 16);
+  // dX summed in the output over several tiles: D without the 1/n of 'mean' (applied by dW's epilogue and
+  // by the last pass over dX), and without its target entries (see vt_drop_targets_kernel)
+  const bool out_sum = p.ntiles > 1 && !acc;
+  const int* dw_scale = out_sum && scale ? n_valid : nullptr;
   for (int64_t ti = 0; ti < p.ntiles; ++ti) {
     const int64_t v0 = ti * Vt, w = std::min<int64_t>(Vt, V - v0), w8 = pad8(w);
     rc = logits(v0, w);
     if (rc) return rc;
     hipLaunchKernelGGL((vt_grad_kernel<T>), rgrid, dim3(kVtLanes), 0, st, Lt, Vt, w, w8, v0, targets, ignore_index,
-                       state, n_valid, scale ? 1 : 0, row_scale, BT);
+                       state, n_valid, scale && !out_sum ? 1 : 0, row_scale, BT);
     rc = check_launch("vt_grad_kernel");
     if (rc) return rc;
     // dW of the tile's rows: D [BT, w8] (k = the row, m = the tile column) and X [BT, Hp] (k = the row,
     // n = the hidden column), both read MN-contiguous; K = BT
     rc = launch_gemm_mn<T, true, true>(Lt, Xk, (int)w8, (int)Hp, (int)BT, Vt, ldx,
-                                       EpiDw<T, 0>{dWo + v0 * H, H, nullptr, Hp, (int)w, (int)H, wvec}, st);
+                                       EpiDw<T, 0>{dWo + v0 * H, H, nullptr, Hp, (int)w, (int)H, wvec, dw_scale},
+                                       st);
     if (rc) return rc;
-    if (p.ntiles > 1 && !acc) {
+    if (out_sum) {
       // summed in the 16-bit output: the softmax terms only (see vt_drop_targets_kernel)
       hipLaunchKernelGGL((vt_drop_targets_kernel<T>), dim3((unsigned)std::min<int64_t>(cdiv(BT, 256), 4096)),
                          dim3(256), 0, st, Lt, Vt, w, v0, targets, ignore_index, BT);
@@ -1257,7 +1294,7 @@ int vtiled_ce(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, char* ws
     else rc = dx_gemm(EpiDw<T, 4>{dX, H, acc, Hp, bl, hl, dvec});
     if (rc) return rc;
   }
-  if (p.ntiles > 1 && !acc) {
+  if (out_sum) {
     hipLaunchKernelGGL((vt_target_dx_kernel<T>), rgrid, dim3(256), 0, st, dX, H, Wk, ldw, targets, ignore_index, V,
                        state, n_valid, scale ? 1 : 0, row_scale, BT);
     rc = check_launch("vt_target_dx_kernel");
@@ -1288,6 +1325,7 @@ FlShape flce_shape(int64_t BT, int64_t H, int64_t V, int dtype, bool grad, int64
   s.ce = true;
   s.chunk_cap = chunk;
   s.vt_ok = s.es == 2;  // (the tiled dW GEMM reads both operands MN-contiguous: 16-bit only)
+  s.f16 = dtype == HK_F16;
   return s;
 }
 
@@ -1332,6 +1370,7 @@ FlShape fljsd_shape(int64_t BT, int64_t H, int64_t Ht, int64_t V, int dtype, boo
   *t_gather = labels || Ht % 8 != 0 || (t_in && !aligned_to(t_in, 16));
   *t_wpad = Ht % 8 != 0 || (t_w && !aligned_to(t_w, 16));
   const JsdExtra e0 = jsd_extra(BT, Ht, V, 0, s.es, *t_gather, *t_wpad);
+  s.f16 = dtype == HK_F16;
   s.fixed_extra = e0.total + 4 * 256;
   s.row_extra = (size_t)pad64(V) * s.es + (*t_gather ? (size_t)pad8(Ht) * s.es : 0);
   s.chunk_cap = chunk;

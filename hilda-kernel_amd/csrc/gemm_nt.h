@@ -578,23 +578,32 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 }
 
 // ---------------------------------------------------------------------------
-// Both operands K-contiguous and K % BK == 0 (every FusedLinearCE GEMM): the
-// same tiles and pipeline with nothing but MFMAs, LDS reads, DMA and scalar
-// work in the K loop.
+// K % BK == 0 (every fused-linear GEMM): the same tiles and pipeline with
+// nothing but MFMAs, LDS reads, DMA and scalar work in the K loop.
 // * LDS holds [A stage 0][A stage 1][B stage 0][B stage 1]. A fragment's LDS
-//   address is one of 16 per-lane bases (sub-step x row parity; the XOR
-//   swizzle of row R + 32 i depends on i only through its parity) plus an
-//   immediate, and the K loop is unrolled by two so the stage offset is an
-//   immediate too.
-// * No column masking: the DMA offsets are fixed per lane. An odd stage count
-//   gets one trailing all-zero stage (zero-length buffer loads).
+//   address is a per-lane base plus an immediate, and the K loop is unrolled
+//   by two so the stage offset is an immediate too.
+//   - K-contiguous operand: stage [rows][BK]; one of 16 bases (sub-step x row
+//     parity; the XOR swizzle of row R + 32 i depends on i only through its
+//     parity); one ds_read_b128 a fragment.
+//   - MN-contiguous operand (AMN / BMN, 16-bit): stage [BK][rows], 16-byte
+//     chunk index XOR 4 (k % 4); one base per fragment of the wave tile (the
+//     swizzle of row R + 32 t is chunk 4 (t ^ k % 4) + ...), the sub-step and
+//     half in the immediate; two ds_read_b64_tr_b16 a fragment. Its buffer is
+//     rebuilt per stage at the stage's first k-row, spanning the k-rows inside
+//     the stored K extent (Shape::ka / kb); chunks past the matrix's M or N are
+//     redirected out of it.
+// * No column masking of a K-contiguous operand: its DMA offsets are fixed per
+//   lane. An odd stage count gets one trailing all-zero stage (zero-length
+//   buffer loads).
 // * Each sub-step issues two MFMAs, then all of the next sub-step's LDS reads,
 //   then its remaining MFMAs (measured 3-4% faster than one read per MFMA).
 // ---------------------------------------------------------------------------
-template <typename T, class C, class Epi>
+template <typename T, class C, class Epi, bool AMN = false, bool BMN = false>
 __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A, const T* __restrict__ B, Shape g,
                                                         Epi epi) {
   static_assert(C::STAGES == 2 && C::CPR == 8, "two stages of 128-byte rows");
+  static_assert(sizeof(T) == 2 || (!AMN && !BMN), "MN-contiguous operands are 16-bit (ds_read_b64_tr_b16)");
   constexpr int kStageBytes = C::STAGES * C::STAGE * (int)sizeof(T);
   constexpr int kEpiBytes = epilogue_lds_bytes<C, Epi>();
   constexpr int kLdsBytes = kStageBytes > kEpiBytes ? kStageBytes : kEpiBytes;
@@ -607,6 +616,9 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
   static_assert(kABytes + (C::TM - 1) * 32 * C::BK * (int)sizeof(T) < 65536 &&
                     kBBytes + (C::TN - 1) * 32 * C::BK * (int)sizeof(T) < 65536,
                 "stage and row offsets fit the 16-bit LDS immediate");
+  static_assert(kABytes + (C::BK - 4) * C::BM * (int)sizeof(T) < 65536 &&
+                    kBBytes + (C::BK - 4) * C::BN * (int)sizeof(T) < 65536,
+                "stage and k-row offsets fit the 16-bit LDS immediate");
 
   apply_bound(g, C::BK);
   const int nbm = (g.M + C::BM - 1) / C::BM, nbn = (g.N + C::BN - 1) / C::BN;
@@ -637,45 +649,87 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     KT = min(per, KT - kt0);
   }
 
-  // Fragment (ks, row R + 32 i) of the MFMA layout: lane l reads row R + 32 i + l%32,
-  // 16-byte chunk 2 ks + l/32, stored at chunk (2 ks + l/32) ^ swz_xor(row). With R a
-  // multiple of 64, swz_xor(R + 32 i + fr) = (fr & 7) ^ (fr >> 3) ^ 4 (i & 1).
-  uint32_t abase[C::NKS][2], bbase[C::NKS][2];
+  // K-contiguous fragment (ks, row R + 32 i) of the MFMA layout: lane l reads row R + 32 i + l%32,
+  // 16-byte chunk 2 ks + l/32, stored at chunk (2 ks + l/32) ^ swz_xor(row). With R a multiple of 64,
+  // swz_xor(R + 32 i + fr) = (fr & 7) ^ (fr >> 3) ^ 4 (i & 1).
+  // MN-contiguous fragment t (rows R + 32 t ..): lane 16 q + i of a tr16 read points at k-row
+  // 16 ks + 8 (q >> 1) + 4 h + i / 4 and row R + 32 t + 16 (q & 1) + 4 (i % 4); its chunk is row / 8
+  // XOR 4 (k % 4), k % 4 = i / 4 for every (ks, h).
+  constexpr int KB = AMN ? 1 : C::NKS, KBN = BMN ? 1 : C::NKS;
+  uint32_t abase[KB][AMN ? C::TM : 2], bbase[KBN][BMN ? C::TN : 2];
   {
     const int sx0 = (fr & 7) ^ (fr >> 3);
+    const int q = lane >> 4, ii = lane & 15, kq = ii >> 2;
+    auto mn_base = [&](int R, int t, int rows) {
+      const int r = R + 32 * t + 16 * (q & 1) + 4 * (ii & 3);
+      const int chunk = (r >> 3) ^ (4 * kq);
+      return (uint32_t)(((8 * (q >> 1) + kq) * rows + chunk * 8 + (r & 7)) * (int)sizeof(T));
+    };
+    if constexpr (AMN) {
 #pragma unroll
-    for (int ks = 0; ks < C::NKS; ++ks)
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const int ch = ((2 * ks + fk) ^ sx0 ^ (4 * p)) * C::EPC;
-        abase[ks][p] = (uint32_t)(((wm * C::WTM + fr) * C::BK + ch) * (int)sizeof(T));
-        bbase[ks][p] = (uint32_t)(kBRegion + ((wn * C::WTN + fr) * C::BK + ch) * (int)sizeof(T));
-        asm volatile("" : "+v"(abase[ks][p]));  // kept in registers, not recomputed per read
-        asm volatile("" : "+v"(bbase[ks][p]));
+      for (int t = 0; t < C::TM; ++t) {
+        abase[0][t] = mn_base(wm * C::WTM, t, C::BM);
+        asm volatile("" : "+v"(abase[0][t]));
       }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < C::NKS; ++ks)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int ch = ((2 * ks + fk) ^ sx0 ^ (4 * p)) * C::EPC;
+          abase[ks][p] = (uint32_t)(((wm * C::WTM + fr) * C::BK + ch) * (int)sizeof(T));
+          asm volatile("" : "+v"(abase[ks][p]));  // kept in registers, not recomputed per read
+        }
+    }
+    if constexpr (BMN) {
+#pragma unroll
+      for (int t = 0; t < C::TN; ++t) {
+        bbase[0][t] = (uint32_t)kBRegion + mn_base(wn * C::WTN, t, C::BN);
+        asm volatile("" : "+v"(bbase[0][t]));
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < C::NKS; ++ks)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int ch = ((2 * ks + fk) ^ sx0 ^ (4 * p)) * C::EPC;
+          bbase[ks][p] = (uint32_t)(kBRegion + ((wn * C::WTN + fr) * C::BK + ch) * (int)sizeof(T));
+          asm volatile("" : "+v"(bbase[ks][p]));
+        }
+    }
   }
-  // DMA: lane offsets inside the panel (row r, chunk swizzled by r); the stage's
-  // first column goes in the scalar offset. A 1 KiB load fills kLoadElems
-  // elements of LDS.
+  // DMA: lane offsets inside the panel. K-contiguous: row r, chunk swizzled by r; the stage's
+  // first column goes in the scalar offset. MN-contiguous: k-row k, chunk swizzled by k % 4, chunks
+  // at or past the matrix's M (N) redirected out of the buffer; the buffer is rebuilt per stage.
+  // A 1 KiB load fills kLoadElems elements of LDS.
   constexpr int IA = C::IA, IB = C::IB;
   constexpr int kLoadElems = 1024 / (int)sizeof(T);
   uint32_t va[IA], vb[IB];
+  auto dma_offset = [&](bool mn, int q, int64_t ld, int rows_valid) -> uint32_t {
+    if (mn) {
+      constexpr int CPK = C::BM / 8;  // chunks per k-row (BM == BN)
+      const int k = q / CPK, key = ((q % CPK) ^ (4 * (k & 3))) * 8;
+      return key < rows_valid ? (uint32_t)(k * ld + key) * (uint32_t)sizeof(T) : kOobOffset;
+    }
+    const int r = q / 8;
+    return (uint32_t)(r * ld + ((q % 8) ^ swz_xor<8>(r)) * C::EPC) * (uint32_t)sizeof(T);
+  };
+  static_assert(!(AMN || BMN) || C::BM == C::BN, "MN-contiguous stage tiles assume BM == BN");
+  const int rva = min(C::BM, g.M - m0), rvb = min(C::BN, g.N - n0);
 #pragma unroll
-  for (int i = 0; i < IA; ++i) {
-    const int q = (wave * IA + i) * 64 + lane, r = q / 8;
-    va[i] = (uint32_t)(r * g.lda + ((q % 8) ^ swz_xor<8>(r)) * C::EPC) * (uint32_t)sizeof(T);
-  }
+  for (int i = 0; i < IA; ++i) va[i] = dma_offset(AMN, (wave * IA + i) * 64 + lane, g.lda, rva);
 #pragma unroll
-  for (int i = 0; i < IB; ++i) {
-    const int q = (wave * IB + i) * 64 + lane, r = q / 8;
-    vb[i] = (uint32_t)(r * g.ldb + ((q % 8) ^ swz_xor<8>(r)) * C::EPC) * (uint32_t)sizeof(T);
-  }
-  const T* const pa = A + (int64_t)m0 * g.lda + kt0 * C::BK;
-  const T* const pb = B + (int64_t)n0 * g.ldb + kt0 * C::BK;
-  // buffer ranges: the panel's rows inside the matrix (rows past it read zero;
-  // with a split's K offset the range still ends where the panel's last row can reach)
-  const int nra = (int)(min(C::BM, g.M - m0) * g.lda * (int64_t)sizeof(T));
-  const int nrb = (int)(min(C::BN, g.N - n0) * g.ldb * (int64_t)sizeof(T));
+  for (int i = 0; i < IB; ++i) vb[i] = dma_offset(BMN, (wave * IB + i) * 64 + lane, g.ldb, rvb);
+  // K-contiguous: the panel from this split's first column, its rows inside the matrix (rows past it read
+  // zero; with a split's K offset the range still ends where the panel's last row can reach).
+  // MN-contiguous: the panel's columns from this split's first k-row.
+  const T* const pa = AMN ? A + (int64_t)kt0 * C::BK * g.lda + m0 : A + (int64_t)m0 * g.lda + kt0 * C::BK;
+  const T* const pb = BMN ? B + (int64_t)kt0 * C::BK * g.ldb + n0 : B + (int64_t)n0 * g.ldb + kt0 * C::BK;
+  const int nra = AMN ? 0 : (int)(rva * g.lda * (int64_t)sizeof(T));
+  const int nrb = BMN ? 0 : (int)(rvb * g.ldb * (int64_t)sizeof(T));
+  if (g.ka <= 0) g.ka = g.K;
+  if (g.kb <= 0) g.kb = g.K;
+  const int kva = g.ka - kt0 * C::BK, kvb = g.kb - kt0 * C::BK;  // stored k-rows from this split's start
 
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -684,35 +738,77 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     constexpr int st = decltype(stage_c)::value;
     const bool live = kst < KT;  // past KT: zero-length buffers, the loads return zeros
     const int k0b = live ? kst * C::BK * (int)sizeof(T) : 0;
-    const __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pa), 0, live ? nra : 0, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rb =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pb), 0, live ? nrb : 0, kRsrcWord3);
+    __amdgpu_buffer_rsrc_t ra, rb;
+    int sa = k0b, sb = k0b;
+    if constexpr (AMN) {
+      const int kr = live ? max(0, min(C::BK, kva - kst * C::BK)) : 0;
+      ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pa + (int64_t)kst * C::BK * g.lda), 0,
+                                             (int)(kr * g.lda * (int64_t)sizeof(T)), kRsrcWord3);
+      sa = 0;
+    } else {
+      ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pa), 0, live ? nra : 0, kRsrcWord3);
+    }
+    if constexpr (BMN) {
+      const int kr = live ? max(0, min(C::BK, kvb - kst * C::BK)) : 0;
+      rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pb + (int64_t)kst * C::BK * g.ldb), 0,
+                                             (int)(kr * g.ldb * (int64_t)sizeof(T)), kRsrcWord3);
+      sb = 0;
+    } else {
+      rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(pb), 0, live ? nrb : 0, kRsrcWord3);
+    }
 #pragma unroll
     for (int i = 0; i < IA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds + (st * kABytes) / (int)sizeof(T) + (wave * IA + i) * kLoadElems,
-                                               16, va[i], k0b, 0, 0);
+                                               16, va[i], sa, 0, 0);
 #pragma unroll
     for (int i = 0; i < IB; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, lds + (kBRegion + st * kBBytes) / (int)sizeof(T) + (wave * IB + i) * kLoadElems, 16, vb[i], k0b, 0,
+          rb, lds + (kBRegion + st * kBBytes) / (int)sizeof(T) + (wave * IB + i) * kLoadElems, 16, vb[i], sb, 0,
           0);
 #endif
   };
 
   u32x4 fa[2][C::TM], fb[2][C::TN];
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  // an MN-contiguous fragment: two transposing reads (k-rows 16 ks + 4 h + ...)
+  auto tr_frag = [&](uint32_t base, int off, int rows) -> u32x4 {
+    v4i16 h[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      h[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_v4i16*)(lds_raw + base + off + 4 * hh * rows * (int)sizeof(T)));
+    const u32x2 lo = __builtin_bit_cast(u32x2, h[0]), hi = __builtin_bit_cast(u32x2, h[1]);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  };
+#endif
   // fragments of sub-step ks, in the order mma() consumes them
   auto frag = [&](auto stage_c, int ks, u32x4* a, u32x4* b) {
     constexpr int st = decltype(stage_c)::value;
 #pragma unroll
     for (int t = 0; t < C::TM * C::TN; ++t) {
       const int i = t / C::TN, j = t % C::TN;
-      if (j == 0)
-        a[i] = *reinterpret_cast<const u32x4*>(lds_raw + abase[ks][i & 1] +
-                                               (st * kABytes + i * 32 * C::BK * (int)sizeof(T)));
-      if (i == 0)
-        b[j] = *reinterpret_cast<const u32x4*>(lds_raw + bbase[ks][j & 1] +
-                                               (st * kBBytes + j * 32 * C::BK * (int)sizeof(T)));
+      if (j == 0) {
+        if constexpr (AMN) {
+#if defined(__HIP_DEVICE_COMPILE__)
+          a[i] = tr_frag(abase[0][i], st * kABytes + 16 * ks * C::BM * (int)sizeof(T), C::BM);
+#endif
+        } else {
+          a[i] = *reinterpret_cast<const u32x4*>(lds_raw + abase[ks][i & 1] +
+                                                 (st * kABytes + i * 32 * C::BK * (int)sizeof(T)));
+        }
+      }
+      if (i == 0) {
+        if constexpr (BMN) {
+#if defined(__HIP_DEVICE_COMPILE__)
+          b[j] = tr_frag(bbase[0][j], st * kBBytes + 16 * ks * C::BN * (int)sizeof(T), C::BN);
+#endif
+        } else {
+          b[j] = *reinterpret_cast<const u32x4*>(lds_raw + bbase[ks][j & 1] +
+                                                 (st * kBBytes + j * 32 * C::BK * (int)sizeof(T)));
+        }
+      }
     }
   };
   auto mma = [&](int buf, int first, int count) { mma_frags<T, C>(acc, fa[buf], fb[buf], first, count); };
@@ -721,6 +817,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  constexpr int NRD = (AMN ? 2 : 1) * C::TM + (BMN ? 2 : 1) * C::TN;  // LDS read instructions a sub-step
   constexpr int kPre = 2;  // MFMAs of a sub-step issued ahead of the next sub-step's reads
   static_assert(C::TM * C::TN > kPre, "sub-step split");
   // sub-steps 0 .. NKS-2 of the stage in buffer CUR
@@ -730,7 +827,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
       frag(stage_c, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
       mma(ks & 1, 0, C::TM * C::TN);
       __builtin_amdgcn_sched_group_barrier(0x008, kPre, 0);                          // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, C::NR, 0);                         // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);                           // LDS read
       __builtin_amdgcn_sched_group_barrier(0x008, C::MPF * C::TM * C::TN - kPre, 0);  // MFMA
     }
   };
@@ -749,9 +846,9 @@ __global__ __launch_bounds__(C::NT) void gemm_kk_kernel(const T* __restrict__ A,
     issue(cur_c, kt + 2);
     mma(LB, Q, R);
 #pragma unroll
-    for (int t = 0; t < C::NR + C::NI || t < RM; ++t) {
-      if (t < C::NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);             // LDS read
-      else if (t < C::NR + C::NI) __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
+    for (int t = 0; t < NRD + C::NI || t < RM; ++t) {
+      if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);             // LDS read
+      else if (t < NRD + C::NI) __builtin_amdgcn_sched_group_barrier(0x010, 1, 1);  // global->LDS load
       if (t < RM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                  // MFMA
     }
   };
@@ -828,10 +925,14 @@ int launch(const T* A, const T* B, int M, int N, int K, int64_t lda, int64_t ldb
   if (!check(AMN, M, lda, "A") || !check(BMN, N, ldb, "B")) return -1;
   Shape g{M, N, K, lda, ldb, lim, lim_off, lim_k ? 1 : 0, ksplit < 1 ? 1 : ksplit, ka, kb};
   const int64_t blocks = (int64_t)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN) * g.ksplit;
-  if constexpr (!AMN && !BMN && C::STAGES == 2 && C::CPR == 8) {
-    // (the K-contiguous kernel reads every operand to K: the extents must be K)
-    if (K % C::BK == 0 && (ka == 0 || ka == K) && (kb == 0 || kb == K)) {
-      hipLaunchKernelGGL((gemm_kk_kernel<T, C, Epi>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g, epi);
+  if constexpr (C::STAGES == 2 && C::CPR == 8 && C::BM == C::BN) {
+    // The pipelined kernel: K a whole number of stages; a K-contiguous operand read to K (its extent must be
+    // K), an MN-contiguous one to its extent (k-rows past it read zero).
+    const bool a_ok = AMN || ka == 0 || ka == K;
+    const bool b_ok = BMN || kb == 0 || kb == K;
+    if (K % C::BK == 0 && a_ok && b_ok) {
+      hipLaunchKernelGGL((gemm_kk_kernel<T, C, Epi, AMN, BMN>), dim3((unsigned)blocks), dim3(C::NT), 0, st, A, B, g,
+                         epi);
       return check_launch("gemm_kk_kernel");
     }
   }

@@ -145,9 +145,9 @@ def _flce_plan(BT, H, V, budget=0, dtype=2, grad=1, chunk=0):
 def test_fused_linear_workspace_queries():
     lib = _lib.load()
     MiB = 2**20
-    # an unknown dtype needs no workspace; a gradient call needs more than a loss-only call
+    # an unknown dtype needs no workspace; with no limit a gradient call needs more than a loss-only call
     assert _flce_ws(16384, 4096, 128256, dtype=5) == 0
-    assert 0 < _flce_ws(16384, 4096, 128256, grad=0) < _flce_ws(16384, 4096, 128256)
+    assert 0 < _flce_ws(16384, 4096, 128256, grad=0, budget=-1) < _flce_ws(16384, 4096, 128256, budget=-1)
     # the default plan costs what the reference's chunk costs (fused_linear_cross_entropy.py:112-114):
     # chunk logits about the size of the hidden states, plus the gathered rows, their transpose and a quarter
     # of the chunk for split partials; nothing grows with BT x V

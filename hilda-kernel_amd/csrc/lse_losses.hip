@@ -368,8 +368,11 @@ struct NoTarget {
 // every lane with the row's log2-sum-exp of x * c; ctx = pre(row) runs before
 // the row's reduction (for loads that should overlap it). target_of(ctx)
 // names a column that the reduction leaves out and adds back afterwards
-// (target_merge), exactly as the gradient kernels do, so a forward-only call
-// returns bitwise the same results as the gradient form.
+// (target_merge), exactly as the gradient kernels do: with the target column
+// named, as the GRPO forward-only path does, a forward-only call returns
+// bitwise the same results as the gradient form. The CrossEntropy inference
+// and selective log-softmax forwards name none (NoTarget) and reduce over
+// every column, so their results agree with the gradient forms' to rounding.
 template <typename T, int VEC, int NCH, int BLOCK, class RowPtr, class NextLive, class Pre, class TargetOf,
           class Emit>
 __device__ __forceinline__ void lse_rows_resident(int n, float c, int64_t rows, float* red, RowPtr row_ptr,
@@ -1409,8 +1412,13 @@ int grpo_rows_launch(void* dlogits, const void* logits, int64_t row0, int64_t nr
       auto go = [&](auto grad_c) {
         constexpr bool GRAD = decltype(grad_c)::value;
         if (cfg.vec == 1) return run(grpo_kernel<T, 1, 1, 1024, false, GRAD>, 1024);
-        if constexpr (NCH == 0) return run(grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>, BLOCK);
-        else return run(grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>, BLOCK);
+        if constexpr (NCH == 0) {
+          return run(grpo_kernel<T, 16 / sizeof(T), 1, BLOCK, false, GRAD>, BLOCK);
+        } else {
+          // the resident form takes its leading full vectors untested (see form_fits)
+          if (!form_fits(width, cfg)) return HK_EINVAL;
+          return run(grpo_kernel<T, 16 / sizeof(T), NCH, BLOCK, true, GRAD>, BLOCK);
+        }
       };
       if (dlogits) return go(std::true_type{});
       return go(std::false_type{});

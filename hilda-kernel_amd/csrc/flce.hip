@@ -1101,9 +1101,30 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
   // the chunk buffer's columns the row step never writes are the dX GEMM's K padding: zero
   rc = zero_cols<T>(Lg, ldl, p.Vr, ldl, C, st);
   if (rc) return rc;
+  // The transposes (HBM-bound) run on a side stream beside the GEMMs
+  // (MFMA-bound; a transpose workgroup fits in the registers and LDS a GEMM
+  // workgroup leaves free on its CU): W^T beside the first chunk's logits, each
+  // chunk's X^T and D^T beside its dX GEMM. `side_pending`: the side stream
+  // holds work the caller's stream has not joined yet.
+  hipStream_t side = nullptr;
+  bool side_pending = false;
+  if (grad) {
+    const int dev = current_device();
+    side = dev >= 0 ? side_stream(dev) : nullptr;
+    if (!side) return HK_EINVAL;
+  }
+  auto fork = [&]() { return stream_after(side, st); };
+  auto join = [&]() {
+    if (!side_pending) return HK_OK;
+    side_pending = false;
+    return stream_after(st, side);
+  };
   if (grad && p.wt) {
-    rc = launch_transpose<T>(Wt, Wk, V, ldl, Hp, ldw, ldl, st);  // W^T [Hp, ldl], zero columns past V
+    rc = fork();
     if (rc) return rc;
+    rc = launch_transpose<T>(Wt, Wk, V, ldl, Hp, ldw, ldl, side);  // W^T [Hp, ldl], zero columns past V
+    if (rc) return rc;
+    side_pending = true;
   }
   const int64_t BTp = pad8(BT), ldxt = ld_t(defer ? BT : C);
   const bool dvec = H % 4 == 0 && aligned_to(dX, 16);    // 4-element stores of dX rows
@@ -1112,6 +1133,10 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
   for (int64_t ci = 0; ci < p.nch; ++ci) {
     const int64_t r0 = ci * C;
     const int64_t cs = std::min<int64_t>(C, BT - r0);
+    if (ci > 0) {  // the previous chunk's transposes still read Xg and Lg
+      rc = join();
+      if (rc) return rc;
+    }
     // the chunk's hidden rows, K-contiguous
     const T* Xc = X + r0 * H;
     int64_t ldxc = H;
@@ -1128,6 +1153,25 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
     rc = row_step(Lg, r0, cs);
     if (rc) return rc;
     if (!grad) continue;
+    // X_c^T (zeros past the live rows) into X^T: columns [r0, r0 + cs) of [Hp, BT] when
+    // deferred, else [Hp, C]; and D_c^T when materialised: into columns [r0, r0 + cs) of
+    // D^T [V8, BTp] (zeros past the live rows) when deferred, else D^T [V8, C]. On the
+    // side stream, beside the dX GEMM, which also only reads the chunk.
+    const int64_t csp = pad8(cs);
+    {
+      rc = join();  // W^T, which the dX GEMM reads
+      if (rc) return rc;
+      rc = fork();
+      if (rc) return rc;
+      T* xt_dst = defer ? Xt + r0 : Xt;
+      const int64_t xrp = defer ? (ci + 1 < p.nch ? cs : BTp - r0) : csp;
+      rc = launch_transpose<T>(xt_dst, Xc, cs, xrp, Hp, ldxc, ldxt, side, n_live, r0);
+      if (rc) return rc;
+      if (defer) rc = launch_transpose<T>(Dt + r0, Lg, cs, xrp, p.V8, ldl, ldxt, side, n_live, r0);
+      else if (p.dt) rc = launch_transpose<T>(Dt, Lg, cs, csp, p.V8, ldl, ldxt, side, n_live, r0);
+      if (rc) return rc;
+      side_pending = true;
+    }
     // dX_c = D_c W, stored into the live rows' original places; a short chunk
     // splits K (= ldl) and sums the splits' fp32 partials in a second pass
     T* dst = rowmap ? dX : dX + r0 * H;
@@ -1148,21 +1192,11 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
       rc = check_launch("splitk_sum_kernel");
       if (rc) return rc;
     }
-    // X_c^T (zeros past the live rows) into X^T: columns [r0, r0 + cs) of [Hp, BT] when
-    // deferred, else [Hp, C]
-    const int64_t csp = pad8(cs);
-    T* xt_dst = defer ? Xt + r0 : Xt;
-    const int64_t xrp = defer ? (ci + 1 < p.nch ? cs : BTp - r0) : csp;
-    rc = launch_transpose<T>(xt_dst, Xc, cs, xrp, Hp, ldxc, ldxt, st, n_live, r0);
-    if (rc) return rc;
-    if (defer) {
-      // D_c^T into columns [r0, r0 + cs) of D^T [V8, BTp]; zeros past the live rows
-      rc = launch_transpose<T>(Dt + r0, Lg, cs, xrp, p.V8, ldl, ldxt, st, n_live, r0);
-      if (rc) return rc;
-      continue;
-    }
+    if (defer) continue;
     // dW (+)= D_c^T X_c; K = cs is padded to a multiple of 8 with zeros on both operands, and cut
     // on the device to the live rows
+    rc = join();
+    if (rc) return rc;
     auto dw_gemm = [&](auto epi) {
       if (p.dt)
         return launch_gemm<T>(Dt, Xt, (int)V, (int)Hp, (int)csp, ldxt, ldxt, epi, st, n_live, (int)r0, true);
@@ -1171,10 +1205,6 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
       return launch_gemm_mn<T, true, false>(Lg, Xt, (int)p.V8, (int)Hp, (int)csp, ldl, ldxt, epi, st, n_live,
                                             (int)r0, true, 1, 0, (int)cs);
     };
-    if (p.dt) {
-      rc = launch_transpose<T>(Dt, Lg, cs, csp, p.V8, ldl, ldxt, st, n_live, r0);
-      if (rc) return rc;
-    }
     const int vl = (int)V, hl = (int)H;
     if (p.nch == 1) rc = dw_gemm(EpiDw<T, 0>{dWo, H, nullptr, Hp, vl, hl, wvec});
     else if (p.dw == kDwOut) rc = ci == 0 ? dw_gemm(EpiDw<T, 0>{dWo, H, nullptr, Hp, vl, hl, wvec})
@@ -1184,6 +1214,8 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
     else rc = dw_gemm(EpiDw<T, 4>{dWo, H, acc, Hp, vl, hl, wvec});
     if (rc) return rc;
   }
+  rc = join();  // (also leaves no work of this call behind on the side stream)
+  if (rc) return rc;
   if (defer && p.nch > 0) {
     rc = launch_gemm<T>(Dt, Xt, (int)V, (int)Hp, (int)BTp, ldxt, ldxt,
                         EpiDw<T, 0>{dWo, H, nullptr, Hp, (int)V, (int)H, wvec}, st, n_live, 0, true);

@@ -76,6 +76,40 @@ int check_launch(const char* what) {
   return HK_OK;
 }
 
+hipStream_t side_stream(int device) {
+  // per host thread: a stream another thread is capturing into is never handed out
+  thread_local hipStream_t streams[kMaxDevices] = {};
+  if (device < 0 || device >= kMaxDevices) {
+    set_error("device %d out of range for the side-stream table", device);
+    return nullptr;
+  }
+  if (!streams[device]) {
+    hipStream_t s = nullptr;
+    const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      set_error("hipStreamCreateWithFlags failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    streams[device] = s;
+  }
+  return streams[device];
+}
+
+int stream_after(hipStream_t to, hipStream_t from) {
+  hipEvent_t ev = nullptr;
+  HK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  hipError_t e = hipEventRecord(ev, from);
+  if (e == hipSuccess) e = hipStreamWaitEvent(to, ev, 0);
+  // (released by the runtime once the recorded work has completed)
+  const hipError_t d = hipEventDestroy(ev);
+  if (e == hipSuccess) e = d;
+  if (e != hipSuccess) {
+    set_error("stream fork/join failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  return HK_OK;
+}
+
 }  // namespace hk
 
 extern "C" {

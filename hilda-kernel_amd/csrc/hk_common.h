@@ -306,6 +306,16 @@ int blocks_per_cu(const void* kernel, int block);  // resident blocks a CU (occu
 int current_device();                // -1 on failure (error recorded)
 int check_launch(const char* what);  // 0 or hipError_t after a launch
 
+// A second stream on `device` (which must be current) for HBM-bound work that
+// runs beside an MFMA-bound kernel of the caller's stream: default priority,
+// non-blocking (no implicit ordering with the null stream), one per host
+// thread and device, created on first use and kept until the process ends.
+// nullptr on failure (error recorded).
+hipStream_t side_stream(int device);
+// Order `to` after the work enqueued on `from` so far (an event recorded on
+// `from`, waited on by `to`; a stream capture follows the edge).
+int stream_after(hipStream_t to, hipStream_t from);
+
 inline bool aligned_to(const void* p, size_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }

@@ -102,3 +102,26 @@ def test_graph_losses_step():
         return loss, gce, gloss, clip, ggl, fl_loss, gh, gw
 
     _check_replays(step)
+
+
+@pytest.mark.parametrize("form", ["defer,wt,dt", "acc,wt,dt", "out,wmn,dmn", "acc,wmn,dt"])
+def test_graph_fused_linear_forms(form, monkeypatch):
+    """FusedLinearCE's chunked memory forms under capture. Their transposes run on a second stream between
+    event fork/joins (W^T beside the first logits GEMM, each chunk's X^T and D^T beside its dX GEMM), which
+    the capture must follow; compacted rows, several chunks."""
+    monkeypatch.setenv("HILDA_FL_FORM", form)
+    dev = gpu()
+    g = torch.Generator(device=dev).manual_seed(11)
+    bf = torch.bfloat16
+    h = torch.randn(520, 192, generator=g, device=dev).to(bf)
+    wt = (0.05 * torch.randn(1500, 192, generator=g, device=dev)).to(bf)
+    th = torch.randint(0, 1500, (520,), generator=g, device=dev)
+    th[130:260] = -100
+    from kernels import fused_linear_cross_entropy as fl
+
+    def step():
+        loss, gh, gw, _ = fl.fused_linear_cross_entropy_forward(h, wt, th, -100, "mean", compute_grad=True,
+                                                                chunk=128, workspace_budget="fastest")
+        return loss, gh, gw
+
+    _check_replays(step)

@@ -434,6 +434,34 @@ def peak_mib(fn, dev):
     return round((torch.cuda.max_memory_allocated(dev) - base) / 2**20, 1)
 
 
+def torch_gemms_c5(dev, H, V, n_live, reps, flush, chunk=8192):
+    """torch.mm (hipBLASLt) on the three GEMM shapes of C5's fastest plan, bf16 in, bf16 out: a full chunk's
+    logits X W^T and dX = D W, and the one dW = D^T X over the live rows. The library's own GEMMs on these
+    shapes are the rows of a kernel trace of the same run; this is the vendor library's time beside them."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+    x = torch.randn(chunk, H, generator=g, device=dev).to(bf)
+    w = (0.02 * torch.randn(V, H, generator=g, device=dev)).to(bf)
+    d = (1e-3 * torch.randn(chunk, V, generator=g, device=dev)).to(bf)
+    out = {}
+    lg = torch.empty(chunk, V, dtype=bf, device=dev)
+    dx = torch.empty(chunk, H, dtype=bf, device=dev)
+    shapes = [("logits", lambda: torch.mm(x, w.t(), out=lg), 2 * chunk * H * V, [chunk, V, H]),
+              ("dx", lambda: torch.mm(d, w, out=dx), 2 * chunk * H * V, [chunk, H, V])]
+    for name, fn, flops, mnk in shapes:
+        ms = statistics.median(time_events(fn, reps, flush, warmup=1))
+        out[name] = {"mnk": mnk, "ms": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    del lg, dx, d, x
+    dt = (1e-3 * torch.randn(V, n_live, generator=g, device=dev)).to(bf)
+    xk = torch.randn(n_live, H, generator=g, device=dev).to(bf)
+    dw = torch.empty(V, H, dtype=bf, device=dev)
+    ms = statistics.median(time_events(lambda: torch.mm(dt, xk, out=dw), reps, flush, warmup=1))
+    out["dw"] = {"mnk": [V, H, n_live], "ms": round(ms, 3), "tflops": round(2 * n_live * H * V / (ms * 1e-3) / 1e12, 1)}
+    del dt, xk, dw, w
+    torch.cuda.empty_cache()
+    return out
+
+
 def flce_memory(K, dev, N, H, V, dtype, budgets=(None,), reps=3, flush=None, seed=0):
     """fwd+bwd peak memory and time of FusedLinearCE against torch's unfused hidden @ W.T + cross_entropy on
     the same GPU. Peak: leaves allocated inside the measured function, as the reference's bench_memory does
@@ -513,6 +541,10 @@ def bench_c5(K, dev, reps, flush, cpu=False):
         f"({e['frac']:.1%}); default plan {d_ms:.3f} ms")
     del h, w, c
     torch.cuda.empty_cache()
+    e["torch_gemms"] = torch_gemms_c5(dev, H, V, n_valid, max(3, reps // 2), flush)
+    tg = e["torch_gemms"]
+    log(f"    hipBLASLt (torch.mm) on the same GEMMs: logits {tg['logits']['ms']} ms, dX {tg['dx']['ms']} ms, "
+        f"dW {tg['dw']['ms']} ms")
     # peak memory at C5 (fresh leaves of the same shapes) and at the reference's memory configs
     # (bench_fused_linear_ce.py:270-274, fp16), default plan
     e["memory"] = flce_memory(K, dev, BT, H, V, torch.bfloat16, budgets=(None, "fastest"), reps=3, flush=flush)

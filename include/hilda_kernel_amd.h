@@ -270,10 +270,12 @@ int hk_attn_res_bwd(void* dV, void* dw_query, void* dw_norm, const void* dh, con
 /* ----------------------------------------------------------------------- */
 /* CrossEntropy                                                            */
 /* ----------------------------------------------------------------------- */
-/* Bytes of device workspace the CrossEntropy entry points use: 256 (n_valid)
- * plus 4 per row for the launch plan of hk_cross_entropy_fwd_grad, which deals
- * the rows that get a gradient out evenly over the GPU. A workspace of 256
- * bytes or more but less than this is accepted and runs without the plan. */
+/* Bytes of device workspace the CrossEntropy entry points use:
+ * 256 + roundup(4 * rows, 256) for rows < 2^31 (256 beyond): 256 for the
+ * counts, then the launch plan of hk_cross_entropy_fwd_grad (4 bytes a row),
+ * which deals the rows that get a gradient out evenly over the GPU. A
+ * workspace of 256 bytes or more but less than this is accepted and runs
+ * without the plan. */
 size_t hk_cross_entropy_workspace_size(int64_t rows);
 
 /* Replaces cross_entropy_forward's training path (cross_entropy.py:206-236:
@@ -341,12 +343,19 @@ int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_
  * hidden/weight pointers (nullable: taken as 16-byte aligned); 0 for an
  * invalid shape or a budget no plan fits.
  *   chunk: most rows per chunk (<= 0: 8192).
- *   workspace_budget: 0 selects the default plan, whose workspace is what the
- *     reference's chunk costs (fused_linear_cross_entropy.py:112-114: chunk
- *     logits about the size of the hidden states, at least 64 rows) plus a
- *     quarter of that for split partial sums; < 0 no limit (the fastest plan);
- *     > 0 at most that many bytes. Within the budget the plan with the least
- *     modelled time is taken (hk_fused_linear_cross_entropy_plan reports it). */
+ *   workspace_budget: 0 selects the default budget: the larger of 40 MiB and
+ *     what the reference's chunk costs (fused_linear_cross_entropy.py:112-114:
+ *     C0 = next_pow2(ceil(BT / ceil(V / H))) rows, 64 to 8192, whose logits
+ *     are about the size of the hidden states) in the leanest layout, plus an
+ *     eighth of the chunk's logits bytes for split partial sums; < 0 no limit
+ *     (the fastest plan); > 0 at most that many bytes. Within the budget the
+ *     plan with the least modelled time is taken, except that a plan which
+ *     sums dW in the 16-bit output across chunks gives way to one that sums it
+ *     exactly (fp32, or written once) when that one is modelled at most 1.5x
+ *     slower; for fp16 inputs such a plan is compared only with the plans
+ *     that do not sum dW in the fp16 output over row chunks (there gradients
+ *     scaled by 1/n fall in fp16's subnormal range), when one fits
+ *     (hk_fused_linear_cross_entropy_plan reports the choice). */
 size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk,
                                                     int64_t workspace_budget, int dtype, int with_grad,
                                                     const void* hidden, const void* weight);
@@ -355,8 +364,11 @@ size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64
  * benchmarks and tests. info[8] = rows per chunk, chunks, dW mode (0: every
  * chunk's D^T kept and one dW GEMM after the loop; 1: an fp32 [V,H]
  * accumulator; 2: accumulated in the output, rounded per chunk for 16-bit
- * inputs), W^T materialised (else W read MN-contiguous), D^T materialised
- * (else D read MN-contiguous), dX split cap, workspace bytes, modelled ns. */
+ * inputs; 3 and 4: vocabulary tiles, each tile's dW rows written once, dX
+ * summed over the tiles in an fp32 buffer (3) or in the output (4); rows per
+ * chunk and chunks are then the tile's columns and the tile count), W^T
+ * materialised (else W read MN-contiguous), D^T materialised (else D read
+ * MN-contiguous), dX split cap, workspace bytes, modelled ns. */
 int hk_fused_linear_cross_entropy_plan(int64_t BT, int64_t H, int64_t V, int64_t chunk, int64_t workspace_budget,
                                        int dtype, int with_grad, const void* hidden, const void* weight,
                                        int64_t* info);

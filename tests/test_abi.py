@@ -265,3 +265,34 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load()
+
+
+def test_fl_budget_argument(monkeypatch):
+    """workspace_budget as the C ABI takes it: None reads $HILDA_FL_WORKSPACE_BUDGET (unset: the default, 0),
+    'default' 0, 'fastest' / 'unlimited' -1, bytes as an int or a numeric string, negatives -1; other strings raise."""
+    monkeypatch.delenv(_lib.BUDGET_ENV, raising=False)
+    assert _lib.fl_budget(None) == 0
+    monkeypatch.setenv(_lib.BUDGET_ENV, "fastest")
+    assert _lib.fl_budget(None) == -1
+    monkeypatch.setenv(_lib.BUDGET_ENV, "1.5e9")
+    assert _lib.fl_budget(None) == 1_500_000_000
+    assert _lib.fl_budget("default") == 0 and _lib.fl_budget("Unlimited") == -1
+    assert _lib.fl_budget(64 << 20) == 64 << 20 and _lib.fl_budget(-7) == -1 and _lib.fl_budget(0) == 0
+    with pytest.raises(ValueError):
+        _lib.fl_budget("lots")
+
+
+@needs_lib
+def test_fl_budget_env_selects_the_plan(monkeypatch):
+    """The environment variable reaches the plan when the call leaves workspace_budget None."""
+    from kernels.fused_linear_cross_entropy import fused_linear_cross_entropy_plan as plan
+    import torch
+    shape = (16384, 4096, 128256, torch.bfloat16)
+    monkeypatch.delenv(_lib.BUDGET_ENV, raising=False)
+    default = plan(*shape)
+    fastest = plan(*shape, workspace_budget="fastest")
+    assert default != fastest
+    monkeypatch.setenv(_lib.BUDGET_ENV, "fastest")
+    assert plan(*shape) == fastest
+    monkeypatch.setenv(_lib.BUDGET_ENV, str(default["workspace_bytes"]))
+    assert plan(*shape)["workspace_bytes"] <= default["workspace_bytes"]

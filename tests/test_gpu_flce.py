@@ -525,3 +525,49 @@ def test_flce_vocab_tiles_peaked_rows(V, monkeypatch):
                                                             compute_grad=True, workspace_budget=-1)
     _rows_check("dweight", gw, dw_ref, 0.0)
     _rows_check("dhidden", gi, dh_ref, 0.0)
+
+
+def test_flce_threads_and_streams():
+    """Two host threads, each on its own torch stream, run FusedLinearCE at once in the fastest plan (W^T, X^T and
+    D^T transposed on the library's side stream, one per host thread, between event fork/joins); every result
+    equals the same call made alone on the default stream, bit for bit (the sums run in a fixed order)."""
+    import threading
+    dev = gpu()
+    g = torch.Generator(device=dev).manual_seed(21)
+    bf = torch.bfloat16
+    cases = []
+    for _ in range(2):
+        h = torch.randn(640, 256, generator=g, device=dev).to(bf)
+        w = (0.05 * torch.randn(3000, 256, generator=g, device=dev)).to(bf)
+        t = torch.randint(0, 3000, (640,), generator=g, device=dev)
+        t[::5] = -100
+        cases.append((h, w, t))
+
+    def run(h, w, t):
+        return fl.fused_linear_cross_entropy_forward(h, w, t, -100, "mean", compute_grad=True, chunk=128,
+                                                     workspace_budget="fastest")[:3]
+
+    assert fl.fused_linear_cross_entropy_plan(640, 256, 3000, bf, True, 128, "fastest")["w_transposed"]
+    ref = [run(*c) for c in cases]
+    torch.cuda.synchronize()
+    out, errs = [None, None], []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream(device=dev)
+            with torch.cuda.stream(s):
+                for _ in range(4):
+                    out[i] = run(*cases[i])
+            s.synchronize()
+        except Exception as e:  # surfaced by the assert below
+            errs.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errs, errs
+    for i in range(2):
+        for a, b in zip(out[i], ref[i]):
+            assert torch.equal(a, b)

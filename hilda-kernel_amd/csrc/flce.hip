@@ -703,6 +703,7 @@ struct FlShape {
   int64_t chunk_cap;   // rows per chunk at most (<= 0: no cap below 8192)
   bool vt_ok = false;  // the vocabulary-tiled plan applies (CrossEntropy on 16-bit inputs)
   bool f16 = false;    // fp16 inputs (see fl_plan)
+  size_t default_floor = 0;  // the default budget is at least this many bytes
 };
 
 struct FlPlan {
@@ -989,7 +990,7 @@ int fl_plan(const FlShape& s, int64_t budget, FlPlan* out) {
     // the reference's chunk logits, the gathered rows and their transpose, and an
     // eighth of the chunk's bytes for the dX GEMM's split partials
     const FlPlan b = lean(C0, 1);
-    cap = std::max(kSmallWorkspace, b.total + (size_t)C0 * pad64(s.V) * s.es / 8);
+    cap = std::max({kSmallWorkspace, s.default_floor, b.total + (size_t)C0 * pad64(s.V) * s.es / 8});
   } else {
     cap = budget < 0 ? SIZE_MAX : (size_t)budget;
   }
@@ -1366,6 +1367,15 @@ FlShape flce_shape(int64_t BT, int64_t H, int64_t V, int dtype, bool grad, int64
 
 namespace hk {
 namespace {
+// Default-budget floor of the fused-linear losses without a vocabulary-tiled
+// plan (JSD, GRPO): twice the bytes of the weight (the size of its gradient,
+// which the op allocates anyway, twice over). Below it their plans fall back
+// to the reference's short chunks, whose dW GEMM re-reads and rewrites the
+// whole weight gradient every chunk: FusedLinearJSD at BT 8192, H 4096,
+// V 128256 bf16 took 93 ms with a 150 MB plan, 33 ms at 2 GiB, 32 ms with no
+// limit (8.3 GB); FusedLinear-GRPO at B 16, L+1 1024, V 151936 95, 44 and 36 ms.
+size_t weight_pair_bytes(int64_t V, int64_t H, int es) { return 2 * (size_t)V * (size_t)pad8(H) * (size_t)es; }
+
 struct JsdExtra {
   size_t lc, labc, lt, xtc, wtp, total;
 };
@@ -1406,6 +1416,7 @@ FlShape fljsd_shape(int64_t BT, int64_t H, int64_t Ht, int64_t V, int dtype, boo
   s.fixed_extra = e0.total + 4 * 256;
   s.row_extra = (size_t)pad64(V) * s.es + (*t_gather ? (size_t)pad8(Ht) * s.es : 0);
   s.chunk_cap = chunk;
+  s.default_floor = weight_pair_bytes(V, H, s.es);
   return s;
 }
 }  // namespace
@@ -1416,6 +1427,7 @@ FlShape flgrpo_shape(int64_t B, int64_t L, int64_t H, int64_t V, int dtype, bool
   s.ce = false;
   s.vt_ok = false;
   s.fixed_extra = grpo_scratch_bytes(B, L);
+  s.default_floor = weight_pair_bytes(V, H, s.es);
   return s;
 }
 }  // namespace

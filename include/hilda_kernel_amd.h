@@ -195,7 +195,10 @@ int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const
  * shape, chunk, budget, dtype, gradient and label choice and the same input
  * pointers (nullable: taken as 16-byte aligned); Ht: the teacher's hidden
  * size. 0 for an invalid shape or a budget no plan fits (see
- * hk_fused_linear_cross_entropy_workspace_size for chunk and budget). */
+ * hk_fused_linear_cross_entropy_workspace_size for chunk and budget; the
+ * default budget here is at least twice the student weight's bytes, 2*V*H*es:
+ * without a vocabulary-tiled plan, smaller budgets mean short row chunks whose
+ * dW pass rewrites the whole weight gradient each chunk). */
 size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk,
                                           int64_t workspace_budget, int dtype, int with_grad, int with_labels,
                                           const void* s_input, const void* s_weight, const void* t_input,
@@ -223,9 +226,11 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
 /* No counterpart in the reference: its GRPO op takes materialised logits
  * (grpo_loss.py:241-330). This is that op behind the lm_head, chunked like
  * fused_linear_cross_entropy_forward (fused_linear_cross_entropy.py:103-171),
- * so the (B, L+1, V) logits never exist. Bytes of workspace it needs for a
- * call with the same arguments (0 for an invalid shape or a budget no plan
- * fits; chunk and budget as for hk_fused_linear_cross_entropy_workspace_size). */
+ * so the (B, L+1, V) logits are never formed whole under the default budget.
+ * Bytes of workspace it needs for a call with the same arguments (0 for an
+ * invalid shape or a budget no plan fits; chunk and budget as for
+ * hk_fused_linear_cross_entropy_workspace_size, the default budget at least
+ * twice the weight's bytes as for hk_fused_linear_jsd_workspace_size). */
 size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk,
                                            int64_t workspace_budget, int dtype, int with_grad, const void* hidden,
                                            const void* weight);

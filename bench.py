@@ -166,6 +166,9 @@ class C2Step:
         return torch.autograd.grad([c], [self.a, self.b], [self.dc])
 
     def step(self):
+        # each op's backward right after its forward (one autograd pass over all three outputs measured
+        # 2% slower on the GPU: its reverse order re-reads the earlier ops' inputs after they left the
+        # Infinity Cache, while it saved 100 us of host time a step that the GPU hides anyway)
         self.fused_add()
         self.rope()
         self.swiglu()

@@ -1120,6 +1120,15 @@ int chunked_lm_head(const T* X, const T* W, int64_t BT, int64_t H, int64_t V, ch
     side_pending = false;
     return stream_after(st, side);
   };
+  // An error return also leaves the caller's stream ordered after the side
+  // stream's work: the caller may free the workspace as soon as we return.
+  struct JoinOnExit {
+    hipStream_t st, side;
+    bool& pending;
+    ~JoinOnExit() {
+      if (pending) (void)stream_after(st, side);
+    }
+  } join_on_exit{st, side, side_pending};
   if (grad && p.wt) {
     rc = fork();
     if (rc) return rc;

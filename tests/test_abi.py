@@ -296,3 +296,23 @@ def test_fl_budget_env_selects_the_plan(monkeypatch):
     assert plan(*shape) == fastest
     monkeypatch.setenv(_lib.BUDGET_ENV, str(default["workspace_bytes"]))
     assert plan(*shape)["workspace_bytes"] <= default["workspace_bytes"]
+
+
+@needs_lib
+def test_fused_jsd_grpo_default_budget_floor():
+    """FusedLinearJSD and FusedLinear-GRPO (no vocabulary-tiled plan) take a default budget of at least twice the
+    weight's bytes: their default workspace at the benchmark shapes is larger than the reference-chunk budget that
+    FusedLinearCE's default gets, at most that floor (plus the fixed scratch) and no more than the unlimited plan."""
+    lib = _lib.load()
+    V, H = 128256, 4096
+    floor = 2 * V * H * 2
+    jsd = lambda budget: lib.hk_fused_linear_jsd_workspace_size(8192, H, H, V, 0, budget, 2, 1, 0, None, None, None,
+                                                                 None)
+    grpo = lambda budget: lib.hk_fused_linear_grpo_workspace_size(16, 1023, H, 151936, 0, budget, 2, 1, None, None)
+    d_jsd, f_jsd = jsd(0), jsd(-1)
+    assert _flce_ws(8192, H, V) < d_jsd <= floor + (64 << 20) and d_jsd < f_jsd
+    g_floor = 2 * 151936 * H * 2
+    d_grpo, f_grpo = grpo(0), grpo(-1)
+    assert _flce_ws(16 * 1024, H, 151936) < d_grpo <= g_floor + (64 << 20) and d_grpo < f_grpo
+    # an explicit budget is still honoured below the floor
+    assert 0 < jsd(256 << 20) <= 256 << 20

@@ -497,8 +497,6 @@ __global__ __launch_bounds__(C::NT) void gemm_nt_kernel(const T* __restrict__ A,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int fr = lane & 31, fk = lane >> 5;
-
   Operand<T, C, C::BM, AMN> opa;
   Operand<T, C, C::BN, BMN> opb;
   opa.init(A, g.lda, m0, g.M, g.ka, wave, lane);

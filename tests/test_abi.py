@@ -316,3 +316,50 @@ def test_fused_jsd_grpo_default_budget_floor():
     assert _flce_ws(16 * 1024, H, 151936) < d_grpo <= g_floor + (64 << 20) and d_grpo < f_grpo
     # an explicit budget is still honoured below the floor
     assert 0 < jsd(256 << 20) <= 256 << 20
+
+
+@needs_lib
+def test_fused_linear_plans_property_sweep():
+    """Over many shapes, dtypes and budgets the planner's answer is self-consistent: a plan that fits reports the
+    bytes the size query returns, within any positive budget; its rows per chunk (or vocabulary columns per
+    tile) and chunk (tile) count cover BT (V); the chunk cap is honoured; a budget of 0 bytes more than the
+    answer gives the same plan; and loss-only calls never need more than gradient calls."""
+    import random
+    rnd = random.Random(7)
+    lib = _lib.load()
+    cases = 0
+    for _ in range(300):
+        BT = rnd.choice([1, 7, 64, 300, 1000, 4096, 8192, 16384, 50000])
+        H = rnd.choice([8, 64, 264, 1000, 4096, 4099])
+        V = rnd.choice([8, 1000, 2001, 32000, 50257, 128256])
+        dt = rnd.choice([0, 1, 2])
+        chunk = rnd.choice([0, 0, 64, 1000])
+        budget = rnd.choice([0, 0, -1, 1 << 20, 64 << 20, 1 << 30])
+        info = (ctypes.c_int64 * 8)()
+        rc = lib.hk_fused_linear_cross_entropy_plan(BT, H, V, chunk, budget, dt, 1, None, None, info)
+        ws = lib.hk_fused_linear_cross_entropy_workspace_size(BT, H, V, chunk, budget, dt, 1, None, None)
+        if rc != 0:
+            assert ws == 0 and budget > 0, (BT, H, V, dt, chunk, budget)
+            continue
+        cases += 1
+        rows_or_cols, n, mode, wt, dtr, splits, total, model_ns = list(info)
+        assert total == ws > 0
+        if budget > 0:
+            assert total <= budget
+        assert model_ns > 0 and splits >= 1
+        if mode in (3, 4):  # vocabulary tiles: columns a tile, tiles
+            assert dt != 0 and chunk == 0 and rows_or_cols % 256 == 0 and rows_or_cols * n >= V
+        else:
+            assert rows_or_cols * n >= BT and rows_or_cols <= 8192
+            if chunk > 0:
+                assert rows_or_cols <= max(8, chunk)
+            if dt == 0:
+                assert wt and dtr  # fp32 reads no MN-contiguous operand
+        # the same plan under a budget of exactly its bytes
+        info2 = (ctypes.c_int64 * 8)()
+        assert lib.hk_fused_linear_cross_entropy_plan(BT, H, V, chunk, total, dt, 1, None, None, info2) == 0
+        assert info2[6] <= total
+        # a loss-only call never needs more
+        assert lib.hk_fused_linear_cross_entropy_workspace_size(BT, H, V, chunk, -1, dt, 0, None, None) <= \
+            lib.hk_fused_linear_cross_entropy_workspace_size(BT, H, V, chunk, -1, dt, 1, None, None)
+    assert cases > 150

@@ -340,6 +340,15 @@ def bench_fljsd(K, dev, reps, flush, BT=8192, H=4096, V=128256):
     e["peak_mib"] = {"fastest": peak_mib(run("fastest"), dev), "default": peak_mib(run(None), dev)}
     log(f"  fused_linear_jsd: fastest plan {e['ms']:.3f} ms  {e['value']:.1f} TFLOP/s  ({e['frac']:.1%}), peak "
         f"{e['peak_mib']['fastest']} MiB; default plan {d_ms:.3f} ms, peak {e['peak_mib']['default']} MiB")
+    del si, sw, ti, tw
+    torch.cuda.empty_cache()
+    # the reference's memory configs (bench_fused_linear_jsd.py:163-165,180), default plan
+    e["reference_memory_configs"] = []
+    for N_, V_ in ((4096, 32000), (2048, 128256)):
+        r = fljsd_memory(K, dev, N_, H, V_, torch.float16, reps=3, flush=flush)
+        e["reference_memory_configs"].append(r)
+        log(f"    {r['config']}: torch fp32 {r['torch_fp32']['peak_mib']} MiB {r['torch_fp32']['ms']} ms; default "
+            f"{r['default']['peak_mib']} MiB ({r['default']['saving']:.1%} less) {r['default']['ms']} ms")
     return e
 
 
@@ -515,6 +524,62 @@ def flce_memory(K, dev, N, H, V, dtype, budgets=(None,), reps=3, flush=None, see
             "workspace_mib": round(plan["workspace_bytes"] / 2**20, 1)}
         torch.cuda.empty_cache()
     del hs, ws
+    torch.cuda.empty_cache()
+    return out
+
+
+def fljsd_memory(K, dev, N, H, V, dtype, reps=3, flush=None, seed=0):
+    """FusedLinearJSD's fwd+bwd peak memory and time against the reference's PyTorch path, the way the reference's
+    benchmark measures them (bench_fused_linear_jsd.py:30-41,180-206): linear + log_softmax + JSD on fp32 copies of
+    all four inputs, leaves allocated inside the measured function. Time: resident leaves, flushed cache."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def torch_jsd(si, sw, ti, tw, beta=0.5, temperature=1.0):
+        # every intermediate named, so each lives as long as in the reference's function: its peak memory
+        s_logits = (si @ sw.t()) / temperature
+        t_logits = (ti @ tw.t()) / temperature
+        x = s_logits.log_softmax(dim=-1)
+        y = t_logits.log_softmax(dim=-1)
+        q = x.exp()
+        p = y.exp()
+        m = beta * p + (1 - beta) * q
+        log_m = m.log()
+        loss = beta * (p * (y - log_m)).sum(-1) + (1 - beta) * (q * (x - log_m)).sum(-1)
+        return loss.mean()
+
+    def ours(si, sw, ti, tw):
+        return K.hilda_fused_linear_jsd(si, sw, ti, tw)
+
+    def upcast(si, sw, ti, tw):
+        return torch_jsd(si.float(), sw.float(), ti.float(), tw.float())
+
+    def fresh(f):
+        def fn():
+            si = torch.randn(N, H, device=dev, dtype=dtype, requires_grad=True)
+            sw = torch.randn(V, H, device=dev, dtype=dtype, requires_grad=True)
+            ti = torch.randn(N, H, device=dev, dtype=dtype)
+            tw = torch.randn(V, H, device=dev, dtype=dtype)
+            f(si, sw, ti, tw).backward()
+        return fn
+
+    si = torch.randn(N, H, device=dev, dtype=dtype, generator=g).requires_grad_(True)
+    sw = (0.02 * torch.randn(V, H, device=dev, dtype=dtype, generator=g)).requires_grad_(True)
+    ti = torch.randn(N, H, device=dev, dtype=dtype, generator=g)
+    tw = 0.02 * torch.randn(V, H, device=dev, dtype=dtype, generator=g)
+
+    def resident(f):
+        return lambda: torch.autograd.grad([f(si, sw, ti, tw)], [si, sw])
+
+    out = {"config": f"N={N} H={H} V={V} {str(dtype).replace('torch.', '')}"}
+    pu = peak_mib(fresh(upcast), dev)
+    tu = statistics.median(time_events(resident(upcast), reps, flush, warmup=1))
+    out["torch_fp32"] = {"peak_mib": pu, "ms": round(tu, 3)}
+    torch.cuda.empty_cache()
+    p = peak_mib(fresh(ours), dev)
+    t = statistics.median(time_events(resident(ours), reps, flush, warmup=1))
+    out["default"] = {"peak_mib": p, "saving": round(1 - p / pu, 4), "ms": round(t, 3),
+                      "speed_vs_torch": round(tu / t, 2)}
+    del si, sw, ti, tw
     torch.cuda.empty_cache()
     return out
 

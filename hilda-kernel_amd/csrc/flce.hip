@@ -1376,14 +1376,32 @@ FlShape flce_shape(int64_t BT, int64_t H, int64_t V, int dtype, bool grad, int64
 
 namespace hk {
 namespace {
-// Default-budget floor of the fused-linear losses without a vocabulary-tiled
-// plan (JSD, GRPO): twice the bytes of the weight (the size of its gradient,
-// which the op allocates anyway, twice over). Below it their plans fall back
-// to the reference's short chunks, whose dW GEMM re-reads and rewrites the
-// whole weight gradient every chunk: FusedLinearJSD at BT 8192, H 4096,
-// V 128256 bf16 took 93 ms with a 150 MB plan, 33 ms at 2 GiB, 32 ms with no
-// limit (8.3 GB); FusedLinear-GRPO at B 16, L+1 1024, V 151936 95, 44 and 36 ms.
+// Default-budget floor of FusedLinear-GRPO (no vocabulary-tiled plan and no
+// reference to follow): twice the bytes of the weight (the size of its
+// gradient, which the op allocates anyway, twice over). Below it the plans
+// fall back to short chunks, whose dW GEMM re-reads and rewrites the whole
+// weight gradient every chunk: at B 16, L+1 1024, H 4096, V 151936 bf16 95 ms
+// with a 150 MB plan, 44 ms at the floor, 36 ms with no limit.
 size_t weight_pair_bytes(int64_t V, int64_t H, int es) { return 2 * (size_t)V * (size_t)pad8(H) * (size_t)es; }
+
+// Default-budget floor of FusedLinearJSD: what the reference's chunk loop
+// holds at once (fused_linear_jsd.py:133-135,159-203) in its dW product: per
+// logit of a chunk of the reference's rows, the student and teacher logits in
+// the input dtype, their fp32 log-softmax copies, the fp32 dX and dlogits and
+// the dlogits cast back (22 bytes; 16 for fp32 inputs, whose .float() and
+// .to() return the tensor itself), plus the [V, H] product dlogits^T X before
+// it is added into grad_weight. The op's outputs are the reference's, so a
+// workspace within this keeps its peak memory at or below the reference's.
+// (Smaller budgets mean short chunks: BT 8192, H 4096, V 128256 bf16 ran
+// 60 ms at 256 MiB, 38 ms at 1 GiB, 35 ms at 1.5 GiB, 31 ms with no limit.)
+size_t jsd_reference_bytes(int64_t BT, int64_t H, int64_t V, int es) {
+  // the reference's chunk rows, unclamped (fused_linear_jsd.py:133-135), at most BT
+  const int64_t per = std::max<int64_t>(1, cdiv(BT, cdiv(V, H)));
+  int64_t c = 1;
+  while (c < per) c <<= 1;
+  c = std::min<int64_t>(c, BT);
+  return (size_t)c * (size_t)V * (es == 4 ? 16 : 22) + (size_t)V * (size_t)H * (size_t)es;
+}
 
 struct JsdExtra {
   size_t lc, labc, lt, xtc, wtp, total;
@@ -1425,7 +1443,7 @@ FlShape fljsd_shape(int64_t BT, int64_t H, int64_t Ht, int64_t V, int dtype, boo
   s.fixed_extra = e0.total + 4 * 256;
   s.row_extra = (size_t)pad64(V) * s.es + (*t_gather ? (size_t)pad8(Ht) * s.es : 0);
   s.chunk_cap = chunk;
-  s.default_floor = weight_pair_bytes(V, H, s.es);
+  s.default_floor = jsd_reference_bytes(BT, H, V, s.es);
   return s;
 }
 }  // namespace
@@ -1438,6 +1456,22 @@ FlShape flgrpo_shape(int64_t B, int64_t L, int64_t H, int64_t V, int dtype, bool
   s.fixed_extra = grpo_scratch_bytes(B, L);
   s.default_floor = weight_pair_bytes(V, H, s.es);
   return s;
+}
+}  // namespace
+}  // namespace hk
+
+namespace hk {
+namespace {
+// The plan queries' info[8] (the layout the header gives).
+void plan_info(const FlPlan& p, int64_t* info) {
+  info[0] = p.C;
+  info[1] = p.nch;
+  info[2] = p.vtile ? 3 + (p.dw == kDwAcc ? 0 : 1) : p.dw;
+  info[3] = p.wt ? 1 : 0;
+  info[4] = p.dt ? 1 : 0;
+  info[5] = p.ksplit;
+  info[6] = (int64_t)p.total;
+  info[7] = (int64_t)(p.cost * 1e9);
 }
 }  // namespace
 }  // namespace hk
@@ -1466,14 +1500,7 @@ int hk_fused_linear_cross_entropy_plan(int64_t BT, int64_t H, int64_t V, int64_t
   if (const int rc = fl_plan(flce_shape(BT, H, V, dtype, with_grad != 0, chunk, hidden, weight), workspace_budget,
                              &p))
     return rc;
-  info[0] = p.C;
-  info[1] = p.nch;
-  info[2] = p.vtile ? 3 + (p.dw == kDwAcc ? 0 : 1) : p.dw;
-  info[3] = p.wt ? 1 : 0;
-  info[4] = p.dt ? 1 : 0;
-  info[5] = p.ksplit;
-  info[6] = (int64_t)p.total;
-  info[7] = (int64_t)(p.cost * 1e9);
+  plan_info(p, info);
   return HK_OK;
 }
 
@@ -1579,6 +1606,23 @@ size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int
               workspace_budget, &p) != HK_OK)
     return 0;
   return p.total;
+}
+
+int hk_fused_linear_jsd_plan(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int64_t workspace_budget,
+                             int dtype, int with_grad, int with_labels, const void* s_input, const void* s_weight,
+                             const void* t_input, const void* t_weight, int64_t* info) {
+  HK_REQUIRE(fl_dtype_ok(dtype), "fused linear JSD supports fp32, bf16 and fp16 (got %d)", dtype);
+  if (const int rc = fl_check_dims(BT, H, V)) return rc;
+  HK_REQUIRE(Ht > 0 && Ht < (1LL << 30), "invalid teacher hidden size Ht=%lld", (long long)Ht);
+  HK_REQUIRE(info, "null pointer argument");
+  bool tg, tw;
+  FlPlan p;
+  if (const int rc = fl_plan(fljsd_shape(BT, H, Ht, V, dtype, with_grad != 0, chunk, with_labels != 0, s_input,
+                                         s_weight, t_input, t_weight, &tg, &tw),
+                             workspace_budget, &p))
+    return rc;
+  plan_info(p, info);
+  return HK_OK;
 }
 
 int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void* s_input, const void* s_weight,
@@ -1697,6 +1741,21 @@ size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int6
   if (fl_plan(flgrpo_shape(B, L, H, V, dtype, with_grad != 0, chunk, hidden, weight), workspace_budget, &p) != HK_OK)
     return 0;
   return p.total;
+}
+
+int hk_fused_linear_grpo_plan(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int64_t workspace_budget,
+                              int dtype, int with_grad, const void* hidden, const void* weight, int64_t* info) {
+  HK_REQUIRE(B > 0 && L >= 0 && B <= (1LL << 31) && L <= (1LL << 31), "invalid shape B=%lld L=%lld", (long long)B,
+             (long long)L);
+  HK_REQUIRE(fl_dtype_ok(dtype), "fused linear GRPO supports fp32, bf16 and fp16 (got %d)", dtype);
+  if (const int rc = fl_check_dims(B * (L + 1), H, V)) return rc;
+  HK_REQUIRE(info, "null pointer argument");
+  FlPlan p;
+  if (const int rc = fl_plan(flgrpo_shape(B, L, H, V, dtype, with_grad != 0, chunk, hidden, weight),
+                             workspace_budget, &p))
+    return rc;
+  plan_info(p, info);
+  return HK_OK;
 }
 
 int hk_fused_linear_grpo(float* loss_out, float* kl_out, float* clip_out, float* lse_rows, float* loss_rows,

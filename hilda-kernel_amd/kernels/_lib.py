@@ -54,6 +54,7 @@ SIGNATURES = {
     "hk_attn_res_bwd_workspace_size": (_sz, [_i64, _i64]),
     "hk_attn_res_bwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _sz, _p]),
     "hk_fused_linear_jsd_workspace_size": (_sz, [_i64] * 6 + [_i32, _i32, _i32, _p, _p, _p, _p]),
+    "hk_fused_linear_jsd_plan": (_i32, [_i64] * 6 + [_i32, _i32, _i32, _p, _p, _p, _p, _p]),
     "hk_fused_linear_jsd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
                                    _i64, _i64, _p, _sz, _p]),
     "hk_cross_entropy_workspace_size": (_sz, [_i64]),
@@ -70,6 +71,7 @@ SIGNATURES = {
     "hk_grpo_loss_fwd": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _p,
                                 _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _i32, _p, _sz, _p]),
     "hk_fused_linear_grpo_workspace_size": (_sz, [_i64] * 6 + [_i32, _i32, _p, _p]),
+    "hk_fused_linear_grpo_plan": (_i32, [_i64] * 6 + [_i32, _i32, _p, _p, _p]),
     "hk_fused_linear_grpo": (_i32, [_p] * 7 + [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i64,
                                                _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32,
                                                _i32, _i64, _i64, _p, _sz, _p]),

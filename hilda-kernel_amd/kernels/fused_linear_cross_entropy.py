@@ -159,6 +159,11 @@ def fused_linear_cross_entropy_plan(BT, H, V, dtype=torch.bfloat16, compute_grad
     info = (ctypes.c_int64 * 8)()
     _lib.call("hk_fused_linear_cross_entropy_plan", int(BT), int(H), int(V), int(chunk),
               _lib.fl_budget(workspace_budget), _lib._DTYPE_CODE[dtype], int(compute_grad), None, None, info)
+    return plan_dict(info)
+
+
+def plan_dict(info):
+    """A plan query's info[8] as the dict fused_linear_cross_entropy_plan returns."""
     modes = {0: "deferred", 1: "fp32 accumulator", 2: "in output", 3: "vocab tiles, dX fp32",
              4: "vocab tiles, dX in output"}
     return dict(chunk=info[0], chunks=info[1], dw=modes[info[2]], w_transposed=bool(info[3]),

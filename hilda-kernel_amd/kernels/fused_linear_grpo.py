@@ -22,6 +22,7 @@ import torch
 
 from . import _lib
 from .cross_entropy import scale_rows_
+from .fused_linear_cross_entropy import plan_dict
 from .grpo_loss import _f32, _ids_arg, _mask_arg
 
 DEFAULT_CHUNK = 0  # no cap: the workspace budget sets the chunk (at most 8192 rows)
@@ -71,6 +72,17 @@ def fused_linear_grpo_forward(hidden, weight, completion_ids, advantages, old_lo
               _lib.ptr(mask), mcode, msb, msl, B, L, H, V, float(temperature), float(beta), float(eps_low),
               float(eps_high), dt, int(chunk), budget, ws.data_ptr(), ws.numel(), _lib.stream_of(dev))
     return loss, kl_mean, clip_ratio, grad_hidden, grad_weight, rows
+
+
+def fused_linear_grpo_plan(B, L, H, V, dtype=torch.bfloat16, compute_grad=True, chunk=DEFAULT_CHUNK,
+                           workspace_budget=None):
+    """The memory plan a call with B sequences of L completion tokens takes: the dict
+    fused_linear_cross_entropy_plan returns (rows per chunk counted over the B*(L+1) positions)."""
+    import ctypes
+    info = (ctypes.c_int64 * 8)()
+    _lib.call("hk_fused_linear_grpo_plan", int(B), int(L), int(H), int(V), int(chunk), _lib.fl_budget(workspace_budget),
+              _lib._DTYPE_CODE[dtype], int(compute_grad), None, None, info)
+    return plan_dict(info)
 
 
 class HildaFusedLinearGRPOFunction(torch.autograd.Function):

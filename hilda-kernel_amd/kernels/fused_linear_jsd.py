@@ -11,8 +11,11 @@ scales the saved gradients by the upstream gradient on the device, and a unit
 upstream gradient leaves them untouched (the reference's ``torch.equal`` test
 at :228, without the host synchronisation).
 
-Memory follows ``workspace_budget`` exactly as for FusedLinearCrossEntropy
-(the default: the reference's chunk, its teacher logits chunk beside it).
+Memory follows ``workspace_budget`` as for FusedLinearCrossEntropy. The
+default budget is at least what the reference's chunk loop holds at once
+(:133-135,159-203: its chunk's logits, their fp32 log-softmax copies, dX and
+dlogits, and the [V, H] product dlogits^T X), so with the same outputs the
+default peak memory is at most the reference's.
 
 Differences from the reference, by design:
   * the reference keeps fp32 copies of both logits chunks and of dX
@@ -32,7 +35,7 @@ import torch
 
 from . import _lib
 from .cross_entropy import scale_rows_
-from .fused_linear_cross_entropy import DEFAULT_CHUNK
+from .fused_linear_cross_entropy import DEFAULT_CHUNK, plan_dict
 
 
 def fused_linear_jsd_forward(student_input, student_weight, teacher_input, teacher_weight, labels=None, beta=0.5,
@@ -72,6 +75,18 @@ def fused_linear_jsd_forward(student_input, student_weight, teacher_input, teach
               float(beta), float(temperature), dt, int(chunk), budget, ws.data_ptr(), ws.numel(),
               _lib.stream_of(dev))
     return loss, grad_input, grad_weight
+
+
+def fused_linear_jsd_plan(BT, H, V, dtype=torch.bfloat16, Ht=None, compute_grad=True, with_labels=False,
+                          chunk=DEFAULT_CHUNK, workspace_budget=None):
+    """The memory plan a call of that shape takes (not in the reference): the dict fused_linear_cross_entropy_plan
+    returns. Ht, the teacher's hidden size, defaults to H."""
+    import ctypes
+    info = (ctypes.c_int64 * 8)()
+    _lib.call("hk_fused_linear_jsd_plan", int(BT), int(H), int(H if Ht is None else Ht), int(V), int(chunk),
+              _lib.fl_budget(workspace_budget), _lib._DTYPE_CODE[dtype], int(compute_grad), int(with_labels), None,
+              None, None, None, info)
+    return plan_dict(info)
 
 
 class HildaFusedLinearJSDFunction(torch.autograd.Function):

@@ -199,14 +199,25 @@ int hk_jsd_fwd(float* loss_out, float* loss_rows, void* dX, const void* X, const
  * shape, chunk, budget, dtype, gradient and label choice and the same input
  * pointers (nullable: taken as 16-byte aligned); Ht: the teacher's hidden
  * size. 0 for an invalid shape or a budget no plan fits (see
- * hk_fused_linear_cross_entropy_workspace_size for chunk and budget; the
- * default budget here is at least twice the student weight's bytes, 2*V*H*es:
- * without a vocabulary-tiled plan, smaller budgets mean short row chunks whose
- * dW pass rewrites the whole weight gradient each chunk). */
+ * hk_fused_linear_cross_entropy_workspace_size for chunk and budget). The
+ * default budget here is at least what the reference's chunk loop holds at
+ * once (fused_linear_jsd.py:133-135,159-203): c*V*22 bytes (16 for fp32) for
+ * its chunk tensors, c = next_pow2(ceil(BT / ceil(V/H))) rows at most BT, and
+ * V*H*es for its dlogits^T X product. The outputs are the reference's, so the
+ * default peak memory stays at or below the reference's; without a
+ * vocabulary-tiled plan, smaller budgets mean short row chunks whose dW pass
+ * rewrites the whole weight gradient each chunk. */
 size_t hk_fused_linear_jsd_workspace_size(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk,
                                           int64_t workspace_budget, int dtype, int with_grad, int with_labels,
                                           const void* s_input, const void* s_weight, const void* t_input,
                                           const void* t_weight);
+
+/* No counterpart in the reference: the plan the call above sizes, in
+ * hk_fused_linear_cross_entropy_plan's info[8] layout (never vocabulary
+ * tiles). */
+int hk_fused_linear_jsd_plan(int64_t BT, int64_t H, int64_t Ht, int64_t V, int64_t chunk, int64_t workspace_budget,
+                             int dtype, int with_grad, int with_labels, const void* s_input, const void* s_weight,
+                             const void* t_input, const void* t_weight, int64_t* info);
 
 /* Replaces fused_linear_jsd_forward (fused_linear_jsd.py:114-205): per chunk,
  * student logits s_input[BT,H] * s_weight[V,H]^T and teacher logits
@@ -234,10 +245,18 @@ int hk_fused_linear_jsd(float* loss_out, void* dinput, void* dweight, const void
  * Bytes of workspace it needs for a call with the same arguments (0 for an
  * invalid shape or a budget no plan fits; chunk and budget as for
  * hk_fused_linear_cross_entropy_workspace_size, the default budget at least
- * twice the weight's bytes as for hk_fused_linear_jsd_workspace_size). */
+ * twice the weight's bytes, 2*V*H*es: without a vocabulary-tiled plan,
+ * smaller budgets mean short row chunks whose dW pass rewrites the whole
+ * weight gradient each chunk). */
 size_t hk_fused_linear_grpo_workspace_size(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk,
                                            int64_t workspace_budget, int dtype, int with_grad, const void* hidden,
                                            const void* weight);
+
+/* No counterpart in the reference: the plan the call above sizes, in
+ * hk_fused_linear_cross_entropy_plan's info[8] layout (rows per chunk over
+ * the B*(L+1) positions; never vocabulary tiles). */
+int hk_fused_linear_grpo_plan(int64_t B, int64_t L, int64_t H, int64_t V, int64_t chunk, int64_t workspace_budget,
+                              int dtype, int with_grad, const void* hidden, const void* weight, int64_t* info);
 
 /* hidden (B, L+1, H) and weight [V, H] (fp32, bf16 or fp16, contiguous, any H and V): logits =
  * hidden weight^T, then exactly hk_grpo_loss_fwd's loss, kl_mean, clip_ratio

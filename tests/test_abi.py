@@ -298,24 +298,49 @@ def test_fl_budget_env_selects_the_plan(monkeypatch):
     assert plan(*shape)["workspace_bytes"] <= default["workspace_bytes"]
 
 
+def _reference_jsd_transient(BT, H, V, es):
+    """Bytes fused_linear_jsd_forward (fused_linear_jsd.py:133-203) holds at once beside its inputs and outputs, at
+    its dW product: the chunk's tensors, each named, and the [V, H] product dlogits_compute.t() @ s_chunk."""
+    inc = -(-V // H)
+    per = -(-BT // inc)
+    cs = min(1 << (per - 1).bit_length(), BT)  # triton.next_power_of_2, the last chunk may be shorter
+    cell = cs * V
+    upcast = es != 4  # .float() / .to() of an fp32 tensor return the tensor itself
+    tensors = {
+        "s_logits": cell * es, "t_logits": cell * es,
+        "s_logprobs": cell * 4 if upcast else 0, "t_logprobs": cell * 4 if upcast else 0,
+        "dX": cell * 4, "dlogits": cell * 4, "dlogits_compute": cell * es if upcast else 0,
+        "loss_per_row": cs * 4,
+    }
+    return sum(tensors.values()) + V * H * es
+
+
 @needs_lib
 def test_fused_jsd_grpo_default_budget_floor():
-    """FusedLinearJSD and FusedLinear-GRPO (no vocabulary-tiled plan) take a default budget of at least twice the
-    weight's bytes: their default workspace at the benchmark shapes is larger than the reference-chunk budget that
-    FusedLinearCE's default gets, at most that floor (plus the fixed scratch) and no more than the unlimited plan."""
+    """FusedLinearJSD's default workspace is at most what the reference's own chunk loop holds at once (so, with the
+    same outputs, its peak memory is at most the reference's) and uses that room: more than a 256 MiB plan, no more
+    than the unlimited one. FusedLinear-GRPO (no reference) takes at least twice the weight's bytes. Both beat the
+    reference-chunk budget FusedLinearCE's default gets."""
     lib = _lib.load()
-    V, H = 128256, 4096
-    floor = 2 * V * H * 2
-    jsd = lambda budget: lib.hk_fused_linear_jsd_workspace_size(8192, H, H, V, 0, budget, 2, 1, 0, None, None, None,
-                                                                 None)
+    jsd = lambda BT, H, V, dt, budget: lib.hk_fused_linear_jsd_workspace_size(BT, H, H, V, 0, budget, dt, 1, 0, None,
+                                                                              None, None, None)
+    # the reference's memory configs (bench_fused_linear_jsd.py:163-166,180) and the benchmark shape
+    for BT, H, V, dt, es in [(4096, 4096, 32000, 1, 2), (2048, 4096, 128256, 1, 2), (8192, 4096, 128256, 2, 2),
+                             (2048, 4096, 32000, 0, 4)]:
+        ref = _reference_jsd_transient(BT, H, V, es)
+        d, f = jsd(BT, H, V, dt, 0), jsd(BT, H, V, dt, -1)
+        assert 0 < d <= ref, (BT, H, V, dt, d, ref)
+        assert d <= f
+        if f > d:
+            assert d > jsd(BT, H, V, dt, 256 << 20) or jsd(BT, H, V, dt, 256 << 20) == 0
+    assert _flce_ws(8192, 4096, 128256) < jsd(8192, 4096, 128256, 2, 0)
+    H = 4096
     grpo = lambda budget: lib.hk_fused_linear_grpo_workspace_size(16, 1023, H, 151936, 0, budget, 2, 1, None, None)
-    d_jsd, f_jsd = jsd(0), jsd(-1)
-    assert _flce_ws(8192, H, V) < d_jsd <= floor + (64 << 20) and d_jsd < f_jsd
     g_floor = 2 * 151936 * H * 2
     d_grpo, f_grpo = grpo(0), grpo(-1)
     assert _flce_ws(16 * 1024, H, 151936) < d_grpo <= g_floor + (64 << 20) and d_grpo < f_grpo
     # an explicit budget is still honoured below the floor
-    assert 0 < jsd(256 << 20) <= 256 << 20
+    assert 0 < jsd(8192, H, 128256, 2, 256 << 20) <= 256 << 20
 
 
 @needs_lib
@@ -363,3 +388,52 @@ def test_fused_linear_plans_property_sweep():
         assert lib.hk_fused_linear_cross_entropy_workspace_size(BT, H, V, chunk, -1, dt, 0, None, None) <= \
             lib.hk_fused_linear_cross_entropy_workspace_size(BT, H, V, chunk, -1, dt, 1, None, None)
     assert cases > 150
+
+
+@needs_lib
+def test_fused_jsd_grpo_plans_property_sweep():
+    """FusedLinearJSD's and FusedLinear-GRPO's plan queries agree with their size queries over many shapes, dtypes
+    and budgets: the reported bytes are the size query's and fit a positive budget, the chunks cover the rows
+    (GRPO: B*(L+1) positions), the chunk cap holds, no vocabulary tiles, and fp32 reads no MN-contiguous operand."""
+    import random
+    rnd = random.Random(11)
+    lib = _lib.load()
+    cases = 0
+    for _ in range(200):
+        H = rnd.choice([8, 64, 264, 1000, 4096, 4099])
+        V = rnd.choice([8, 1000, 2001, 32000, 50257, 128256])
+        dt = rnd.choice([0, 1, 2])
+        chunk = rnd.choice([0, 0, 64, 1000])
+        budget = rnd.choice([0, 0, -1, 1 << 20, 64 << 20, 1 << 30])
+        info = (ctypes.c_int64 * 8)()
+        if rnd.random() < 0.5:
+            BT = rnd.choice([1, 7, 64, 300, 1000, 4096, 8192])
+            Ht = rnd.choice([H, 8, 1000])
+            labels = rnd.choice([0, 1])
+            rc = lib.hk_fused_linear_jsd_plan(BT, H, Ht, V, chunk, budget, dt, 1, labels, None, None, None, None,
+                                              info)
+            ws = lib.hk_fused_linear_jsd_workspace_size(BT, H, Ht, V, chunk, budget, dt, 1, labels, None, None, None,
+                                                        None)
+            rows = BT
+        else:
+            B, L = rnd.choice([1, 3, 16]), rnd.choice([0, 5, 127, 1023])
+            rc = lib.hk_fused_linear_grpo_plan(B, L, H, V, chunk, budget, dt, 1, None, None, info)
+            ws = lib.hk_fused_linear_grpo_workspace_size(B, L, H, V, chunk, budget, dt, 1, None, None)
+            rows = B * (L + 1)
+        if rc != 0:
+            assert ws == 0 and budget > 0
+            continue
+        cases += 1
+        c, n, mode, wt, dtr, splits, total, model_ns = list(info)
+        assert total == ws > 0 and mode in (0, 1, 2) and splits >= 1 and model_ns > 0
+        if budget > 0:
+            assert total <= budget
+        assert c * n >= rows and c <= 8192
+        if chunk > 0:
+            assert c <= max(8, chunk)
+        if dt == 0:
+            assert wt and dtr
+    assert cases > 100
+    # argument checks run before any HIP call
+    assert lib.hk_fused_linear_jsd_plan(8, 8, 8, 8, 0, 0, 2, 1, 0, None, None, None, None, None) == -1
+    assert lib.hk_fused_linear_grpo_plan(0, 5, 8, 8, 0, 0, 2, 1, None, None, info) == -1

@@ -898,6 +898,33 @@ def dw_sweep(dev, reps):
                 del x, w, dy, xf, rs
 
 
+# The shapes the reference's benchmarks time (triton-kernels/benchmarks/), shared by --reference-configs and
+# --vs-torch; dtypes by name (torch.float16 / torch.bfloat16).
+REF_SHAPES = {
+    "rms_norm": ((4, 512, 4096, "float16"), (8, 1024, 4096, "float16"), (4, 2048, 4096, "float16"),
+                 (8, 2048, 4096, "float16"), (4, 1024, 8192, "float16"), (4, 1024, 4096, "bfloat16")),  # :169-177
+    "fused_add_rms_norm": ((4, 2048, 4096, "float16"), (4, 2048, 5120, "float16"), (4, 2048, 8192, "float16"),
+                           (4, 2048, 4096, "bfloat16"), (2, 1024, 4096, "float16")),  # :198-204
+    "rope": ((4, 2048, 32, 8, 128, "float16"), (4, 2048, 32, 32, 128, "float16"), (4, 2048, 64, 8, 128, "float16"),
+             (8, 2048, 32, 8, 128, "float16"), (4, 2048, 32, 8, 128, "bfloat16"),
+             (4, 512, 32, 8, 128, "float16")),  # :263-271
+    "glu": ((8192, 11008, "float16"), (8192, 14336, "float16"), (8192, 28672, "float16"), (8192, 14336, "bfloat16"),
+            (2048, 14336, "float16")),  # bench_swiglu.py:196-203, bench_geglu.py:191-198
+    "cross_entropy": ((8192, 32000, "float16"), (8192, 128256, "float16"), (8192, 32000, "bfloat16"),
+                      (8192, 128256, "bfloat16"), (2048, 32000, "float16")),  # :257-264
+    "grpo": ((8, 512, 32000, 0.0), (8, 512, 32000, 0.1), (4, 1024, 32000, 0.0), (4, 512, 128256, 0.0)),  # :204-209
+    "kl_div": ((8192, 32000, "float16"), (8192, 128256, "float16"), (8192, 32000, "bfloat16"),
+               (2048, 32000, "float16")),  # :156-161
+    "jsd": ((8192, 32000, "float16"), (4096, 128256, "float16"), (8192, 32000, "bfloat16")),  # :173-177
+    "attn_res": ((4, 4096, "float16"), (8, 4096, "float16"), (8, 8192, "float16"), (16, 4096, "float16"),
+                 (8, 4096, "bfloat16")),  # :205-211, B 4, T 2048
+}
+
+
+def _dt(name):
+    return getattr(torch, name)
+
+
 def reference_configs(dev, reps):
     """Every HBM-bound op on the shapes the reference's benchmarks time, fwd and bwd separately, with the
     algorithmic bytes of each call over a device copy of the same bytes; the fused-linear ops in TFLOP/s.
@@ -923,16 +950,16 @@ def reference_configs(dev, reps):
                     f"{gbs / cc:.0%} |")
         log(rows[-1])
 
-    for B, T, H, dt in ((4, 512, 4096, F16), (8, 1024, 4096, F16), (4, 2048, 4096, F16), (8, 2048, 4096, F16),
-                        (4, 1024, 8192, F16), (4, 1024, 4096, BF16)):
+    for B, T, H, dt in REF_SHAPES["rms_norm"]:
+        dt = _dt(dt)
         R, es = B * T, torch.tensor([], dtype=dt).element_size()
         x, w, dy = rnd(R, H, dt=dt), rnd(H, dt=dt), rnd(R, H, dt=dt)
         _, xf, rs = rn.rms_norm_forward(x, w)
         hbm("RMSNorm fwd", f"{B}x{T}x{H}", dt, lambda: rn.rms_norm_forward(x, w), 2 * R * H * es)
         hbm("RMSNorm bwd", f"{B}x{T}x{H}", dt, lambda: rn.rms_norm_backward(dy, xf, w, rs), 3 * R * H * es)
         del x, dy, xf
-    for B, T, H, dt in ((4, 2048, 4096, F16), (4, 2048, 5120, F16), (4, 2048, 8192, F16), (4, 2048, 4096, BF16),
-                        (2, 1024, 4096, F16)):
+    for B, T, H, dt in REF_SHAPES["fused_add_rms_norm"]:
+        dt = _dt(dt)
         R, es = B * T, torch.tensor([], dtype=dt).element_size()
         x, r, w, dy, ds = rnd(R, H, dt=dt), rnd(R, H, dt=dt), rnd(H, dt=dt), rnd(R, H, dt=dt), rnd(R, H, dt=dt)
         _, s_, rs = fa.fused_add_rms_norm_forward(x, r, w)
@@ -940,8 +967,8 @@ def reference_configs(dev, reps):
         hbm("FusedAddRMSNorm bwd", f"{B}x{T}x{H}", dt, lambda: fa.fused_add_rms_norm_backward(dy, ds, s_, w, rs),
             4 * R * H * es)
         del x, r, dy, ds, s_
-    for B, T, nq, nk, hd, dt in ((4, 2048, 32, 8, 128, F16), (4, 2048, 32, 32, 128, F16), (4, 2048, 64, 8, 128, F16),
-                                 (8, 2048, 32, 8, 128, F16), (4, 2048, 32, 8, 128, BF16), (4, 512, 32, 8, 128, F16)):
+    for B, T, nq, nk, hd, dt in REF_SHAPES["rope"]:
+        dt = _dt(dt)
         q, k = rnd(B, nq, T, hd, dt=dt), rnd(B, nk, T, hd, dt=dt)
         cos, sin = rnd(1, T, hd // 2, dt=dt), rnd(1, T, hd // 2, dt=dt)
         nb = 2 * (q.numel() + k.numel()) * q.element_size()
@@ -951,14 +978,14 @@ def reference_configs(dev, reps):
     for name, mod in (("SwiGLU", sw), ("GeGLU", gg)):
         fwd = mod.swiglu_forward if mod is sw else mod.geglu_forward
         bwd = mod.swiglu_backward if mod is sw else mod.geglu_backward
-        for N, D, dt in ((8192, 11008, F16), (8192, 14336, F16), (8192, 28672, F16), (8192, 14336, BF16),
-                         (2048, 14336, F16)):
+        for N, D, dt in REF_SHAPES["glu"]:
+            dt = _dt(dt)
             a, b, dc = rnd(N, D, dt=dt), rnd(N, D, dt=dt), rnd(N, D, dt=dt)
             hbm(f"{name} fwd", f"{N}x{D}", dt, lambda: fwd(a, b), 3 * N * D * 2)
             hbm(f"{name} bwd", f"{N}x{D}", dt, lambda: bwd(a, b, dc), 5 * N * D * 2)
             del a, b, dc
-    for N, V, dt in ((8192, 32000, F16), (8192, 128256, F16), (8192, 32000, BF16), (8192, 128256, BF16),
-                     (2048, 32000, F16)):
+    for N, V, dt in REF_SHAPES["cross_entropy"]:
+        dt = _dt(dt)
         x = rnd(N, V, dt=dt)
         t = torch.randint(0, V, (N,), generator=gen, device=dev)
         es = x.element_size()
@@ -966,7 +993,7 @@ def reference_configs(dev, reps):
             2 * N * V * es)
         hbm("CrossEntropy fwd", f"{N}x{V}", dt, lambda: ce.cross_entropy_forward(x, t), N * V * es)
         del x
-    for B, L, V, beta in ((8, 512, 32000, 0.0), (8, 512, 32000, 0.1), (4, 1024, 32000, 0.0), (4, 512, 128256, 0.0)):
+    for B, L, V, beta in REF_SHAPES["grpo"]:
         x = rnd(B, L + 1, V, dt=BF16)
         ids = torch.randint(0, V, (B, L), generator=gen, device=dev)
         adv, old, ref = rnd(B), rnd(B, L) - 5, rnd(B, L) - 5
@@ -979,18 +1006,21 @@ def reference_configs(dev, reps):
         hbm("selective log-softmax", f"{B}x{L}x{V}", BF16,
             lambda: gl.fused_selective_log_softmax(x, ids, 1.0, mask), nb)
         del x
-    for N, V, dt in ((8192, 32000, F16), (8192, 128256, F16), (8192, 32000, BF16), (2048, 32000, F16)):
+    for N, V, dt in REF_SHAPES["kl_div"]:
+        dt = _dt(dt)
         yp, yt = rnd(N, V).log_softmax(-1).to(dt), rnd(N, V).softmax(-1).to(dt)
         g1 = torch.ones((), device=dev)
         es = yp.element_size()
         hbm("KLDiv fwd", f"{N}x{V}", dt, lambda: kl.kl_div_forward(yp, yt), 2 * N * V * es)
         hbm("KLDiv bwd", f"{N}x{V}", dt, lambda: kl.kl_div_backward(yt, g1), 2 * N * V * es)
         del yp, yt
-    for N, V, dt in ((8192, 32000, F16), (4096, 128256, F16), (8192, 32000, BF16)):
+    for N, V, dt in REF_SHAPES["jsd"]:
+        dt = _dt(dt)
         X, Y = rnd(N, V).log_softmax(-1).to(dt), rnd(N, V).log_softmax(-1).to(dt)
         hbm("JSD fwd+grad", f"{N}x{V}", dt, lambda: js.jsd_forward(X, Y, 0.5), 3 * N * V * X.element_size())
         del X, Y
-    for n, D, dt in ((4, 4096, F16), (8, 4096, F16), (8, 8192, F16), (16, 4096, F16), (8, 4096, BF16)):
+    for n, D, dt in REF_SHAPES["attn_res"]:
+        dt = _dt(dt)
         ntok = 4 * 2048
         Vb, wq, wn, dh = rnd(n, ntok, D, dt=dt), (0.02 * rnd(D)).to(dt), rnd(D, dt=dt), rnd(ntok, D, dt=dt)
         _, V3, alpha, rs = ar.attn_res_forward(Vb, wq, wn)
@@ -1033,6 +1063,161 @@ def reference_configs(dev, reps):
     print("\n".join(mm))
 
 
+def vs_torch(dev, reps):
+    """The reference's published metric (README.md:13-49: fwd+bwd speedup over PyTorch eager, RoPE forward only) on
+    this GPU: each op through the library's autograd API against the PyTorch baseline of the reference's own
+    benchmark (the bench_*.py line each row cites), on the same shapes and inputs. The reference's lambdas draw
+    their inputs with torch.randn inside the timed region; here the inputs are resident, upstream gradients random
+    and each rep starts after a cache flush, so the ratio is of the ops alone. Prints a markdown table."""
+    import kernels as K
+    flush = Flusher(dev)
+    F = torch.nn.functional
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *shape, dt=torch.float32: torch.randn(*shape, generator=gen, device=dev).to(dt)  # noqa: E731
+    dname = {torch.float16: "fp16", torch.bfloat16: "bf16"}
+    rows = []
+
+    def pair(op, shape, dt, claim, base, ours, wrt, fwd_only=False):
+        """base, ours: () -> output tensor or tuple; wrt: the tensors whose gradients both compute."""
+        def run(f):
+            if fwd_only:
+                def fn():
+                    with torch.no_grad():
+                        return f()
+                return fn
+            outs = f()
+            outs = outs if isinstance(outs, tuple) else (outs,)
+            outs = [o for o in outs if o is not None and o.requires_grad]
+            g = [None if o.dim() == 0 else torch.randn(o.shape, generator=gen, device=dev).to(o.dtype) for o in outs]
+            del outs
+
+            def fn():
+                o = f()
+                o = o if isinstance(o, tuple) else (o,)
+                o = [t for t in o if t is not None and t.requires_grad]
+                return torch.autograd.grad(o, wrt, g)
+            return fn
+        tb = statistics.median(time_events(run(base), reps, flush, warmup=2))
+        to = statistics.median(time_events(run(ours), reps, flush, warmup=2))
+        rows.append(f"| {op} | {shape} | {dname[dt]} | {tb * 1e3:.1f} us | {to * 1e3:.1f} us | {tb / to:.2f}x | "
+                    f"{claim} |")
+        log(rows[-1])
+
+    def t_rms(x, w, eps=1e-6):  # bench_rms_norm.py:37-41 (its output promotes to fp32, as there)
+        return x * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps) * w
+
+    def t_fadd(x, r, w, eps=1e-6):  # bench_fused_add_rms_norm.py:37-41
+        s_ = x + r
+        rms = torch.sqrt(torch.mean(s_.float() ** 2, dim=-1, keepdim=True) + eps)
+        return (s_.float() / rms).to(s_.dtype) * w, s_
+
+    def t_rope(q, k, cos, sin):  # bench_rope.py:40-59 (HuggingFace rotate-half)
+        c = torch.cat([cos, cos], dim=-1).unsqueeze(1)
+        s_ = torch.cat([sin, sin], dim=-1).unsqueeze(1)
+
+        def rot(x):
+            h = x.shape[-1] // 2
+            return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+        return q * c + rot(q) * s_, k * c + rot(k) * s_
+
+    def t_grpo(logits, ids, adv, old, ref, beta, eps=0.2):  # bench_grpo.py:30-57, on logits.float() (:157)
+        L = logits.shape[1] - 1
+        logp = logits[:, :-1, :].log_softmax(dim=-1).gather(-1, ids[:, -L:].unsqueeze(-1)).squeeze(-1)
+        ratio = torch.exp(logp - old)
+        a = adv.unsqueeze(-1)
+        per_token = -torch.min(ratio * a, torch.clamp(ratio, 1 - eps, 1 + eps) * a)
+        if beta != 0.0:
+            per_token = per_token + beta * (torch.exp(ref - logp) - (ref - logp) - 1)
+        mask = torch.ones_like(per_token)
+        return ((per_token * mask).sum(-1) / mask.sum(-1).clamp(min=1.0)).mean()
+
+    def t_jsd(x, y, beta=0.5):  # bench_jsd.py:30-45, on fp32 copies (:129)
+        q, p = x.exp(), y.exp()
+        log_m = (beta * p + (1 - beta) * q).log()
+        return (beta * (p * (y - log_m)).sum(-1) + (1 - beta) * (q * (x - log_m)).sum(-1)).mean()
+
+    def t_attn_res(v, wq, wn, eps=1e-6):  # bench_attn_res.py:33-51; its einsums as fp32 matmuls on contiguous operands
+        vf = v.float()
+        k = (vf / torch.sqrt(vf.pow(2).mean(dim=-1, keepdim=True) + eps)).to(v.dtype) * wn
+        alpha = torch.matmul(k.float(), wq.float()).softmax(dim=0)  # [N, B, T]
+        h = torch.matmul(alpha.permute(1, 2, 0).unsqueeze(-2).contiguous(), vf.permute(1, 2, 0, 3).contiguous())
+        return h.squeeze(-2).to(v.dtype)
+
+    for B, T, H, dt in REF_SHAPES["rms_norm"]:
+        dt = _dt(dt)
+        x, w = rnd(B, T, H, dt=dt).requires_grad_(True), torch.ones(H, device=dev, dtype=dt, requires_grad=True)
+        pair("RMSNorm fwd+bwd", f"{B}x{T}x{H}", dt, "1.18-8.21x", lambda: t_rms(x, w), lambda: K.hilda_rms_norm(x, w),
+             [x, w])
+        del x
+    for B, T, H, dt in REF_SHAPES["fused_add_rms_norm"]:
+        dt = _dt(dt)
+        x, r = rnd(B, T, H, dt=dt).requires_grad_(True), rnd(B, T, H, dt=dt).requires_grad_(True)
+        w = torch.ones(H, device=dev, dtype=dt)
+        pair("FusedAddRMSNorm fwd+bwd", f"{B}x{T}x{H}", dt, "4.15-5.66x", lambda: t_fadd(x, r, w),
+             lambda: K.hilda_fused_add_rms_norm(x, r, w), [x, r])
+        del x, r
+    for B, T, nq, nk, hd, dt in REF_SHAPES["rope"]:
+        dt = _dt(dt)
+        q, k = rnd(B, nq, T, hd, dt=dt).requires_grad_(True), rnd(B, nk, T, hd, dt=dt).requires_grad_(True)
+        cos, sin = rnd(1, T, hd // 2, dt=dt), rnd(1, T, hd // 2, dt=dt)
+        pair("RoPE fwd", f"{B}x{T} q{nq} k{nk}", dt, "1.27-1.34x", lambda: t_rope(q, k, cos, sin),
+             lambda: K.hilda_rope(q, k, cos, sin), [q, k], fwd_only=True)
+        pair("RoPE fwd+bwd", f"{B}x{T} q{nq} k{nk}", dt, "-", lambda: t_rope(q, k, cos, sin),
+             lambda: K.hilda_rope(q, k, cos, sin), [q, k])
+        del q, k
+    for name, base, ours, claim in (("SwiGLU", lambda a, b: F.silu(a) * b, K.hilda_swiglu, "1.26-1.68x"),
+                                    ("GeGLU", lambda a, b: F.gelu(a, approximate="tanh") * b, K.hilda_geglu,
+                                     "1.25-1.68x")):
+        for N, D, dt in REF_SHAPES["glu"]:  # bench_swiglu.py:46-47, bench_geglu.py:42-43
+            dt = _dt(dt)
+            a, b = rnd(N, D, dt=dt).requires_grad_(True), rnd(N, D, dt=dt).requires_grad_(True)
+            pair(f"{name} fwd+bwd", f"{N}x{D}", dt, claim, lambda: base(a, b), lambda: ours(a, b), [a, b])
+            del a, b
+    for N, V, dt in REF_SHAPES["cross_entropy"]:  # bench_cross_entropy.py:217-228, 10% ignored
+        dt = _dt(dt)
+        x = rnd(N, V, dt=dt).requires_grad_(True)
+        t = torch.randint(0, V, (N,), generator=gen, device=dev)
+        t[torch.rand(N, generator=gen, device=dev) < 0.1] = -100
+        pair("CrossEntropy fwd+bwd", f"{N}x{V}", dt, "1.66-2.55x", lambda: F.cross_entropy(x, t, ignore_index=-100),
+             lambda: K.hilda_cross_entropy(x, t), [x])
+        del x
+    for B, L, V, beta in REF_SHAPES["grpo"]:  # bench_grpo.py:150-166, bf16 logits
+        x = (0.1 * rnd(B, L + 1, V)).to(torch.bfloat16).requires_grad_(True)
+        ids = torch.randint(0, V, (B, L), generator=gen, device=dev)
+        adv, old = rnd(B), 0.01 * rnd(B, L)
+        # with beta != 0 both get reference log-probs: the reference's bench passes none (its kernel then reads a
+        # one-element dummy at every token's offset, grpo_loss.py:150-153,277), which this library rejects
+        ref = old + 0.1 * rnd(B, L) if beta else None
+        pair("GRPO fwd+bwd", f"{B}x{L}x{V} beta {beta}", torch.bfloat16, "6.10-6.61x",
+             lambda: t_grpo(x.float(), ids, adv, old, ref, beta),
+             lambda: K.hilda_grpo_loss(x, ids, adv, old, ref, beta=beta)[0], [x])
+        del x
+    for N, V, dt in REF_SHAPES["kl_div"]:  # bench_kl_div.py:108-116
+        dt = _dt(dt)
+        yp = rnd(N, V, dt=dt).log_softmax(dim=-1).requires_grad_(True)
+        yt = rnd(N, V, dt=dt).softmax(dim=-1)
+        pair("KLDiv fwd+bwd", f"{N}x{V}", dt, "1.71-1.84x", lambda: F.kl_div(yp, yt, reduction="batchmean"),
+             lambda: K.hilda_kl_div(yp, yt, reduction="batchmean"), [yp])
+        del yp, yt
+    for N, V, dt in REF_SHAPES["jsd"]:  # bench_jsd.py:124-132
+        dt = _dt(dt)
+        xj = rnd(N, V, dt=dt).log_softmax(dim=-1).requires_grad_(True)
+        yj = rnd(N, V, dt=dt).log_softmax(dim=-1)
+        pair("JSD fwd+bwd", f"{N}x{V}", dt, "9.18-11.02x", lambda: t_jsd(xj.float(), yj.float()),
+             lambda: K.hilda_jsd(xj, yj, beta=0.5), [xj])
+        del xj, yj
+    for n, D, dt in REF_SHAPES["attn_res"]:  # bench_attn_res.py:168-181
+        dt = _dt(dt)
+        v = rnd(n, 4, 2048, D, dt=dt).requires_grad_(True)
+        wq, wn = (0.02 * rnd(D)).to(dt), torch.ones(D, device=dev, dtype=dt)
+        pair("AttnRes fwd+bwd", f"N {n}, 4x2048x{D}", dt, "20.55-24.01x", lambda: t_attn_res(v, wq, wn),
+             lambda: K.hilda_attn_res(v, wq, wn), [v])
+        del v
+    print("| Op | Shape | dtype | PyTorch eager | this library | speedup | reference's claim (RTX 5090) |")
+    print("|---|---|---|---|---|---|---|")
+    print("\n".join(rows))
+
+
 C2_OPS = ("fused_add_rms_norm", "rope", "swiglu")
 
 
@@ -1073,6 +1258,9 @@ def main(argv=None):
     ap.add_argument("--dw-sweep", action="store_true",
                     help="instead of the step: RMSNorm backward, dW by fp64 atomics against partial rows over rows x H, "
                          "as a markdown table")
+    ap.add_argument("--vs-torch", action="store_true",
+                    help="instead of the step: every op's fwd+bwd against the reference benchmarks' PyTorch "
+                         "baselines on their shapes, the reference's published speedup metric, as a markdown table")
     ap.add_argument("--reference-configs", action="store_true",
                     help="instead of the step: every op on the reference benchmarks' own shapes, as a markdown table")
     ap.add_argument("--only-copy", action="store_true",
@@ -1100,6 +1288,9 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.reference_configs:
         reference_configs(dev, max(3, args.op_reps // 2))
+        return 0
+    if args.vs_torch:
+        vs_torch(dev, max(3, args.op_reps // 2))
         return 0
     if args.dw_sweep:
         dw_sweep(dev, args.op_reps)

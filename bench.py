@@ -485,7 +485,8 @@ def torch_gemms_c5(dev, H, V, n_live, reps, flush, chunk=8192):
 def flce_memory(K, dev, N, H, V, dtype, budgets=(None,), reps=3, flush=None, seed=0):
     """fwd+bwd peak memory and time of FusedLinearCE against torch's unfused hidden @ W.T + cross_entropy on
     the same GPU. Peak: leaves allocated inside the measured function, as the reference's bench_memory does
-    (bench_fused_linear_ce.py:181-214). Time: resident leaves, flushed cache, median of reps."""
+    (bench_fused_linear_ce.py:181-214). Time: resident leaves, flushed cache, median of reps. budgets: None (the
+    default), 'fastest', bytes, or 'reference_form' (16-bit only): the reference's own memory and dW arithmetic."""
     from kernels import fused_linear_cross_entropy as fl
     g = torch.Generator(device=dev).manual_seed(seed)
     tg = torch.randint(0, V, (N,), device=dev, generator=g)
@@ -514,11 +515,25 @@ def flce_memory(K, dev, N, H, V, dtype, budgets=(None,), reps=3, flush=None, see
     out["unfused_torch"] = {"peak_mib": pu, "ms": round(tu, 3)}
     torch.cuda.empty_cache()
     for b in budgets:
-        f = (lambda h, w, b=b: K.hilda_fused_linear_cross_entropy(h, w, tg, workspace_budget=b))
-        p = peak_mib(fresh(f), dev)
-        t = statistics.median(time_events(resident(f), reps, flush, warmup=1))
-        plan = fl.fused_linear_cross_entropy_plan(N, H, V, dtype, workspace_budget=b)
-        out["default" if b is None else str(b)] = {
+        key = "default" if b is None else str(b)
+        forced = b == "reference_form"
+        if forced:
+            # the reference's footprint and dW arithmetic: a workspace of what its chunk loop holds at once (the
+            # chunk's logits and the [V, H] product dlogits^T X, fused_linear_cross_entropy.py:113-161) and dW summed
+            # in the weight dtype over row chunks (fewer than its chunks), through the planner's debugging override
+            inc = -(-V // H)
+            per = -(-N // inc)
+            b = min(1 << (per - 1).bit_length(), N) * V * 2 + V * H * 2
+            os.environ["HILDA_FL_FORM"] = "out,wmn,dmn"
+        try:
+            f = (lambda h, w, b=b: K.hilda_fused_linear_cross_entropy(h, w, tg, workspace_budget=b))
+            p = peak_mib(fresh(f), dev)
+            t = statistics.median(time_events(resident(f), reps, flush, warmup=1))
+            plan = fl.fused_linear_cross_entropy_plan(N, H, V, dtype, workspace_budget=b)
+        finally:
+            if forced:
+                del os.environ["HILDA_FL_FORM"]
+        out[key] = {
             "peak_mib": p, "saving": round(1 - p / pu, 4), "ms": round(t, 3), "speed_vs_unfused": round(tu / t, 3),
             "plan": {k: plan[k] for k in ("chunk", "chunks", "dw", "w_transposed", "d_transposed")},
             "workspace_mib": round(plan["workspace_bytes"] / 2**20, 1)}
@@ -623,17 +638,21 @@ def bench_c5(K, dev, reps, flush, cpu=False):
         f"dW {tg['dw']['ms']} ms")
     # peak memory at C5 (fresh leaves of the same shapes) and at the reference's memory configs
     # (bench_fused_linear_ce.py:270-274, fp16), default plan
-    e["memory"] = flce_memory(K, dev, BT, H, V, torch.bfloat16, budgets=(None, "fastest"), reps=3, flush=flush)
+    e["memory"] = flce_memory(K, dev, BT, H, V, torch.bfloat16, budgets=(None, "fastest", "reference_form"), reps=3,
+                              flush=flush)
     m = e["memory"]
     log(f"    C5 peak: unfused {m['unfused_torch']['peak_mib']} MiB ({m['unfused_torch']['ms']} ms), default "
         f"{m['default']['peak_mib']} MiB ({m['default']['saving']:.1%} less), fastest {m['fastest']['peak_mib']} "
-        f"MiB ({m['fastest']['saving']:.1%} less)")
+        f"MiB ({m['fastest']['saving']:.1%} less); the reference's footprint and dW arithmetic "
+        f"{m['reference_form']['peak_mib']} MiB, {m['reference_form']['ms']} ms")
     e["reference_memory_configs"] = []
     for N_, H_, V_ in ((8192, 4096, 32000), (8192, 4096, 128256), (4096, 4096, 128256)):
-        r = flce_memory(K, dev, N_, H_, V_, torch.float16, budgets=(None,), reps=3, flush=flush)
+        r = flce_memory(K, dev, N_, H_, V_, torch.float16, budgets=(None, "reference_form"), reps=3, flush=flush)
         e["reference_memory_configs"].append(r)
         log(f"    {r['config']}: unfused {r['unfused_torch']['peak_mib']} MiB {r['unfused_torch']['ms']} ms; "
-            f"default {r['default']['peak_mib']} MiB ({r['default']['saving']:.1%} less) {r['default']['ms']} ms")
+            f"default {r['default']['peak_mib']} MiB ({r['default']['saving']:.1%} less) {r['default']['ms']} ms; "
+            f"reference form {r['reference_form']['peak_mib']} MiB ({r['reference_form']['saving']:.1%} less) "
+            f"{r['reference_form']['ms']} ms")
     if cpu:
         import oracle
         rows = 128

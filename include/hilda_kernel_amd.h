@@ -383,7 +383,15 @@ int hk_grpo_loss_fwd(void* dlogits, float* loss_out, float* kl_out, float* clip_
  *     slower; for fp16 inputs such a plan is compared only with the plans
  *     that do not sum dW in the fp16 output over row chunks (there gradients
  *     scaled by 1/n fall in fp16's subnormal range), when one fits
- *     (hk_fused_linear_cross_entropy_plan reports the choice). */
+ *     (hk_fused_linear_cross_entropy_plan reports the choice).
+ *   Debugging override (all fused-linear ops, read at every call): the
+ *   environment variable HILDA_FL_FORM="<defer|acc|out>,<wt|wmn>,<dt|dmn>"
+ *   restricts the plan to that row-chunked form (dW deferred, in an fp32
+ *   accumulator or in the output; W^T or W read MN-contiguous; D^T or D read
+ *   MN-contiguous), the chunk still from the budget; "vtile,<acc|out>,<cols>"
+ *   to the vocabulary-tiled plan with that dX sum and tile width. Calls
+ *   without gradients ignore a row-chunked form; a form that does not parse,
+ *   or does not apply to the call, fails it with HK_EINVAL. */
 size_t hk_fused_linear_cross_entropy_workspace_size(int64_t BT, int64_t H, int64_t V, int64_t chunk,
                                                     int64_t workspace_budget, int dtype, int with_grad,
                                                     const void* hidden, const void* weight);

@@ -13,8 +13,9 @@
  *  - No entry point synchronises the device or allocates device memory. The
  *    fused-linear entry points with gradients run their transposes on a
  *    second stream the library creates once per host thread and device
- *    (default priority, non-blocking), forked from `stream` and joined back
- *    to it with events before they return, so the caller sees one stream.
+ *    (default priority, non-blocking; kept until the process ends), forked
+ *    from `stream` and joined back to it with events before they return, so
+ *    the caller sees one stream.
  *  - dtype codes: HK_F32 = 0, HK_F16 = 1, HK_BF16 = 2.
  *  - Return value: 0 on success; HK_EINVAL (-1) when an argument is rejected
  *    (checked before any HIP call, so this is testable without a GPU);

@@ -232,3 +232,55 @@ def test_fused_linear_jsd_plan_forms(form, monkeypatch):
     assert_close(loss, l_ref, name="loss", rtol=2e-3, atol=2e-3)
     assert rel_fro(gi, dh_ref.to(dtype)) < 1e-2 and rel_fro(gw, dw_ref.to(dtype)) < 1e-2
     assert_close(gw.float() * n, dw_ref * n, name="dweight*n", **tol(dtype))
+
+
+def _reference_chunk_bytes(N, H, V, es=2):
+    """What fused_linear_jsd_forward holds at once in its dW product (fused_linear_jsd.py:133-135,159-203), 16-bit
+    inputs: per logit of its chunk the two logits, their fp32 log-softmax copies, the fp32 dX and dlogits and the
+    dlogits cast back, 22 bytes; plus the [V, H] product dlogits^T X."""
+    inc = -(-V // H)
+    per = -(-N // inc)
+    cs = min(1 << (per - 1).bit_length(), N)
+    return cs * V * 22 + V * H * es
+
+
+@pytest.mark.parametrize("N,V", [(4096, 32000), (2048, 128256)])
+def test_fused_linear_jsd_reference_memory_configs(N, V):
+    """benchmarks/bench_fused_linear_jsd.py:163-165,180: the reference's memory configs, fp16, beta 1/2, no
+    labels. The default plan's workspace is within what the reference's chunk loop holds at once, and its loss
+    and gradients agree with the unlimited plan's; the student gradient of sampled rows matches the fp64 oracle
+    (row r's dX depends on row r alone, scaled by 1/N)."""
+    H, dtype = 4096, torch.float16
+    dev = gpu()
+    g = torch.Generator(device=dev).manual_seed(N + V)
+    # logits of standard deviation 3: with unit logits the 1/N-scaled dlogits all round to zero in fp16 (in the
+    # reference's arithmetic as here), with much larger ones the softmaxes saturate and the gradient vanishes
+    si = torch.randn(N, H, generator=g, device=dev).to(dtype)
+    sw = (3 * torch.randn(V, H, generator=g, device=dev) / H ** 0.5).to(dtype)
+    ti = torch.randn(N, H, generator=g, device=dev).to(dtype)
+    tw = (3 * torch.randn(V, H, generator=g, device=dev) / H ** 0.5).to(dtype)
+    plan = fj.fused_linear_jsd_plan(N, H, V, dtype)
+    assert plan["workspace_bytes"] <= _reference_chunk_bytes(N, H, V)
+    out = {}
+    for budget in (None, "fastest"):
+        loss, gi, gw = fj.fused_linear_jsd_forward(si, sw, ti, tw, None, 0.5, 1.0, -100, compute_grad=True,
+                                                   workspace_budget=budget)
+        torch.cuda.synchronize()
+        out[budget] = (loss.float().item(), gi.float(), gw.float())
+    (ld, gid, gwd), (lf, gif, gwf) = out[None], out["fastest"]
+    assert abs(ld - lf) <= 1e-5 * abs(lf)
+    assert rel_fro(gid, gif) < 2e-3 and rel_fro(gwd, gwf) < 2e-3
+    rows = torch.tensor([0, 1, N // 2, N - 1])
+    w64, tw64 = sw.cpu().double(), tw.cpu().double()
+    # the rows' logits rounded to fp16 as the GEMMs return them, their dlogits from the oracle's JSD by autograd,
+    # rounded to fp16 at the op's 1/N scale as the reference rounds them (fused_linear_jsd.py:201), times W
+    ls = (si[rows].cpu().double() @ w64.T).to(dtype).double().requires_grad_(True)
+    lt = (ti[rows].cpu().double() @ tw64.T).to(dtype).double()
+    oracle.jsd_ref(torch.log_softmax(ls, -1), torch.log_softmax(lt, -1), 0.5, None).backward()
+    dl = (ls.grad * (len(rows) / N)).to(dtype).double()  # the oracle's mean is over the sampled rows
+    assert dl.abs().max() > 0  # the check is not vacuous
+    dh = dl @ w64
+    got = gid[rows.to(dev)].cpu().double()
+    assert got.abs().max() > 0
+    # dX at this scale sits in fp16's subnormal range (spacing 2^-24): one rounding of the fp32 sum apart
+    assert_close(got, dh, name="dinput rows", rtol=2e-3, atol=2.0 ** -24)
